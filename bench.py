@@ -1,0 +1,326 @@
+"""Benchmark: achieved HBM GB/s of the mHC-lite K1/K3/K4 forward+backward
+kernels at T=65536, n=4, C=1024 (bf16) on one MI355X.
+
+One "step" is one pass of the hot path over one batch: the six HIP kernels
+K1 fwd, K1 bwd-dx, K3 fwd, K3 bwd, K4 fwd, K4 bwd, each on its own synthetic
+input resident in HBM (the kernel microbenchmark of the reference's
+scripts/benchmark_kernels.py, with its mandatory-bytes model, :64-105).
+
+Prints ONE JSON line.  ``value`` = sum of the six kernels' algorithmic bytes /
+measured step time.  ``roofline`` describes the dominant kernel (largest
+average duration), timed with HIP events on the stream it runs on.
+``cpu_baseline`` times the reference's PyTorch formulation of the same six ops
+(fp32 autograd, restated in oracle/) on the host's cores, on a bounded token
+sample, reported with the same bytes model.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--T 65536] [--C 1024]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "flash-mhc_amd"))
+sys.path.insert(0, str(ROOT))
+
+import torch  # noqa: E402
+
+PEAK_GBPS = 8000.0  # MI355X HBM3E
+METRIC = "achieved HBM GB/s (% of peak) for K1/K3/K4 fwd+bwd at T=65536,n=4,C=1024"
+KERNELS = ("k1_fwd", "k1_bwd_dx", "k3_fwd", "k3_bwd", "k4_fwd", "k4_bwd")
+
+
+def bytes_model(T: int, n: int, C: int, D: int) -> dict[str, int]:
+    """Mandatory HBM bytes per launch (reference scripts/benchmark_kernels.py:64-105)."""
+    bf, f4 = 2, 4
+    nC = n * C
+    return {
+        "k1_fwd": bf * T * nC + bf * D * nC + bf * T * D + f4 * T,
+        "k1_bwd_dx": bf * T * nC + bf * D * nC + 2 * bf * T * D + f4 * T + bf * T * nC,
+        "k3_fwd": bf * T * nC + f4 * T * n + bf * T * C,
+        "k3_bwd": 2 * bf * T * nC + 2 * f4 * T * n + bf * T * C,
+        "k4_fwd": 2 * bf * T * nC + bf * T * C + f4 * T * n * n + f4 * T * n,
+        "k4_bwd": 3 * bf * T * nC + 2 * bf * T * C + 2 * f4 * T * n * n + 2 * f4 * T * n,
+    }
+
+
+def make_inputs(T: int, C: int, seed: int = 0):
+    """Synthetic inputs of the kernel-microbench config, generated on the GPU."""
+    n, D = 4, 32
+    nC = n * C
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(seed)
+
+    def rn(*shape, scale=1.0, dtype=torch.bfloat16):
+        return (torch.randn(*shape, generator=g, device=dev) * scale).to(dtype)
+
+    x = rn(T, n, C)
+    # Projection weight (D, nC) ~ N(0, 0.02) with an RMSNorm weight 1 + N(0, 0.02)
+    # folded in: rmsnorm(x) * g @ W^T == rmsnorm(x) @ (W * g)^T.
+    W = (rn(D, nC, scale=0.02, dtype=torch.float32) * (1 + rn(nC, scale=0.02, dtype=torch.float32))).to(torch.bfloat16)
+    lo = rn(T, C)
+    logits = rn(T, D, dtype=torch.float32)
+    h_pre = torch.sigmoid(logits[:, :n]).contiguous()
+    h_post = (2 * torch.sigmoid(logits[:, n : 2 * n])).contiguous()
+    perm = build_perm(n).to(dev)
+    H_res = (torch.softmax(logits[:, 2 * n :], -1) @ perm).view(T, n, n)
+    H = (H_res - h_post[:, :, None] * h_pre[:, None, :]).contiguous()
+    go1 = rn(T, D)
+    go3 = rn(T, C)
+    go4 = rn(T, n, C)
+    return dict(x=x, W=W, lo=lo, h_pre=h_pre, h_post=h_post, H=H, go1=go1, go3=go3, go4=go4)
+
+
+def build_perm(n: int) -> torch.Tensor:
+    from flash_mhc import build_permutation_matrices
+
+    return build_permutation_matrices(n)[0]
+
+
+def make_step(inp: dict, T: int, C: int):
+    """Closures launching each kernel once, with preallocated outputs."""
+    from flash_mhc import kernels as K
+
+    n = 4
+    x, W = inp["x"], inp["W"]
+    xf = x.view(T, n * C)
+    proj, inv = K.k1_fwd(xf, W)
+    bufs = dict(
+        gx1=torch.empty_like(xf),
+        out3=torch.empty((T, C), dtype=torch.bfloat16, device=x.device),
+        gx3=torch.empty_like(x),
+        gh3=torch.empty((T, n), dtype=torch.float32, device=x.device),
+        out4=torch.empty_like(x),
+        gx4=torch.empty_like(x),
+        glo4=torch.empty((T, C), dtype=torch.bfloat16, device=x.device),
+        gH4=torch.empty((T, n, n), dtype=torch.float32, device=x.device),
+        ghp4=torch.empty((T, n), dtype=torch.float32, device=x.device),
+    )
+    proj2, inv2 = torch.empty_like(proj), torch.empty_like(inv)
+    return {
+        "k1_fwd": lambda: K.k1_fwd(xf, W, proj2, inv2),
+        "k1_bwd_dx": lambda: K.k1_bwd_dx(inp["go1"], xf, W, proj, inv, bufs["gx1"]),
+        "k3_fwd": lambda: K.k3_fwd(x, inp["h_pre"], bufs["out3"]),
+        "k3_bwd": lambda: K.k3_bwd(inp["go3"], x, inp["h_pre"], bufs["gx3"], bufs["gh3"]),
+        "k4_fwd": lambda: K.k4_fwd(x, inp["lo"], inp["H"], inp["h_post"], bufs["out4"]),
+        "k4_bwd": lambda: K.k4_bwd(inp["go4"], x, inp["lo"], inp["H"], inp["h_post"],
+                                   bufs["gx4"], bufs["glo4"], bufs["gH4"], bufs["ghp4"]),
+    }
+
+
+def copy_ceiling_gbps(nbytes: int = 1 << 30, iters: int = 20) -> float:
+    """HBM GB/s of torch's device copy (read + write) of an nbytes buffer."""
+    src = torch.empty(nbytes // 2, dtype=torch.bfloat16, device="cuda").normal_()
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s.record()
+    for _ in range(iters):
+        dst.copy_(src)
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / iters
+    del src, dst
+    return 2 * nbytes / (ms * 1e-3) / 1e9
+
+
+def cpu_baseline(C: int, tokens: int, iters: int = 3) -> dict:
+    """The reference's PyTorch formulation of the six ops, fp32 autograd on the host."""
+    from oracle import mhc_oracle as O
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    n, D, T = 4, 32, tokens
+    nC = n * C
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(T, n, C, generator=g)
+    W = torch.randn(D, nC, generator=g) * 0.02
+    lo = torch.randn(T, C, generator=g)
+    hpre = torch.rand(T, n, generator=g)
+    hp = torch.rand(T, n, generator=g) * 2
+    H = torch.randn(T, n, n, generator=g) * 0.3
+    go1, go3, go4 = torch.randn(T, D, generator=g), torch.randn(T, C, generator=g), torch.randn(T, n, C, generator=g)
+
+    def leaf(t):
+        return t.clone().requires_grad_(True)
+
+    def k1():
+        xf, w = leaf(x.view(T, nC)), leaf(W)
+        O.k1_torch(xf, w).backward(go1)
+
+    def k3():
+        xs, h = leaf(x), leaf(hpre)
+        O.k3_torch(xs, h).backward(go3)
+
+    def k4():
+        xs, l, Hm, h = leaf(x), leaf(lo), leaf(H), leaf(hp)
+        O.k4_torch(xs, l, Hm, h).backward(go4)
+
+    total = 0.0
+    per = {}
+    for name, fn in (("k1", k1), ("k3", k3), ("k4", k4)):
+        fn()
+        ts = []
+        for _ in range(iters):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        per[name] = statistics.median(ts)
+        total += per[name]
+    bm = bytes_model(T, n, C, D)
+    nbytes = sum(bm.values())
+    try:
+        cpu_model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
+    except (OSError, StopIteration):
+        cpu_model = "unknown"
+    return {
+        "value": round(nbytes / total / 1e9, 3),
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"T={T} tokens of the same n=4, C={C} workload, fp32 on the host CPU ({cpu_model}); "
+                   f"K1/K3/K4 forward+autograd backward with the reference's PyTorch formulas; "
+                   f"median of {iters} after 1 warmup; bytes from the same model as the GPU kernels"),
+        "tokens_per_s": round(T / total, 1),
+        "seconds_per_pass": {k: round(v, 4) for k, v in per.items()},
+    }
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--T", type=int, default=65536)
+    ap.add_argument("--C", type=int, default=1024)
+    ap.add_argument("--cpu-tokens", type=int, default=8192)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--traffic", type=str, default=str(ROOT / "profiles" / "traffic_k4_bwd_T65536_C1024.json"),
+                    help="measured HBM traffic summary (rocprofv3 --pmc) for the dominant kernel")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: the K1/K3/K4 path is independent per token, "
+              "so N GPUs would each run this same per-GPU workload on T/N tokens with no "
+              "communication; run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+
+    from flash_mhc import _abi
+
+    _abi.load()  # fail loudly if the extension is missing
+    T, C, n, D = args.T, args.C, 4, 32
+    inp = make_inputs(T, C)
+    launch = make_step(inp, T, C)
+    bm = bytes_model(T, n, C, D)
+
+    def step(events=None):
+        for i, k in enumerate(KERNELS):
+            if events is not None:
+                events[i][0].record()
+            launch[k]()
+            if events is not None:
+                events[i][1].record()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    K_steps = args.steps
+    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in KERNELS]
+           for _ in range(K_steps)]
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    s0 = torch.cuda.Event(enable_timing=True)
+    s1 = torch.cuda.Event(enable_timing=True)
+    s0.record()
+    for k in range(K_steps):
+        step(evs[k])
+    s1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_start
+    ms_total = s0.elapsed_time(s1)
+    ms_per_step = ms_total / K_steps
+
+    per = {}
+    for i, name in enumerate(KERNELS):
+        ts = [evs[k][i][0].elapsed_time(evs[k][i][1]) for k in range(K_steps)]
+        avg = sum(ts) / len(ts)
+        per[name] = {
+            "avg_us": round(avg * 1e3, 2),
+            "median_us": round(statistics.median(ts) * 1e3, 2),
+            "GBps": round(bm[name] / (avg * 1e-3) / 1e9, 1),
+            "frac": round(bm[name] / (avg * 1e-3) / 1e9 / PEAK_GBPS, 4),
+            "bytes": bm[name],
+        }
+    total_bytes = sum(bm.values())
+    value = total_bytes / (ms_per_step * 1e-3) / 1e9
+    sum_kernel_ms = sum(p["avg_us"] for p in per.values()) / 1e3
+    dom = max(per, key=lambda k: per[k]["avg_us"])
+
+    traffic = None
+    tpath = Path(args.traffic)
+    if tpath.exists():
+        try:
+            tr = json.loads(tpath.read_text())
+            if tr.get("kernel") == dom and tr.get("T") == T and tr.get("C") == C:
+                traffic = tr.get("traffic_bytes")
+        except (OSError, ValueError):
+            traffic = None
+
+    ceiling = copy_ceiling_gbps()
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": K_steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": (f"mHC-lite K1/K3/K4 forward+backward kernel microbench: six HIP kernels per step, "
+                         f"T={T}, n=4, C={C}, D_out=32, bf16 activations, fp32 coefficients"),
+            "T": T, "n": n, "C": C, "D_out": D,
+        },
+        "frac_of_peak": round(value / PEAK_GBPS, 4),
+        "tokens_per_s": round(T / (ms_per_step * 1e-3), 1),
+        "sum_kernel_ms": round(sum_kernel_ms, 4),
+        "copy_ceiling_GBps": round(ceiling, 1),
+        "kernels": per,
+        "roofline": {
+            "kernel": dom,
+            "bound": "hbm",
+            "achieved": per[dom]["GBps"],
+            "peak": PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": per[dom]["frac"],
+            "traffic": traffic,
+        },
+        "wall_s": round(wall, 3),
+    }
+    del inp, launch
+    torch.cuda.empty_cache()
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(C, args.cpu_tokens)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

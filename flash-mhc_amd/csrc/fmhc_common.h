@@ -1,0 +1,136 @@
+// Shared device helpers for the mHC-lite K1/K3/K4 HIP kernels (gfx950, wave64).
+//
+// Data conventions used by every kernel in this library:
+//   * bf16 tensors arrive as uint16_t bit patterns, row-major and contiguous.
+//   * fp32 accumulation everywhere; every bf16 output is rounded exactly once,
+//     round-to-nearest-even, by the hardware v_cvt_pk_bf16_f32 conversion.
+//   * The "vector" code paths move 16 bytes (8 bf16) per lane per memory
+//     instruction; they need C % 8 == 0 and 16-byte aligned base pointers.
+//     The "scalar" code paths move one element per lane and accept any C and
+//     any 2-byte alignment.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/flash_mhc_hip.h"
+
+namespace fmhc {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+
+// Streaming loads/stores.  Data that is read or written exactly once per
+// launch carries the nontemporal hint so it does not evict the small,
+// reused operands (W, coefficients) from the caches.
+#ifndef FMHC_NT_LOADS
+#define FMHC_NT_LOADS 1
+#endif
+#ifndef FMHC_NT_STORES
+#define FMHC_NT_STORES 1
+#endif
+
+template <typename V>
+__device__ __forceinline__ V ld_stream(const V* p) {
+#if FMHC_NT_LOADS
+  return __builtin_nontemporal_load(p);
+#else
+  return *p;
+#endif
+}
+
+template <typename V>
+__device__ __forceinline__ void st_stream(V* p, V v) {
+#if FMHC_NT_STORES
+  __builtin_nontemporal_store(v, p);
+#else
+  *p = v;
+#endif
+}
+
+// bf16 bit pattern -> fp32 (exact).
+__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// Two fp32 -> packed bf16 pair, round-to-nearest-even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  bf16x2 r = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+  return __builtin_bit_cast(uint32_t, r);
+}
+__device__ __forceinline__ uint16_t f32_to_bf16(float a) {
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(a));
+}
+
+__device__ __forceinline__ void unpack8(const u32x4 v, float f[8]) {
+  f[0] = bf_lo(v.x); f[1] = bf_hi(v.x);
+  f[2] = bf_lo(v.y); f[3] = bf_hi(v.y);
+  f[4] = bf_lo(v.z); f[5] = bf_hi(v.z);
+  f[6] = bf_lo(v.w); f[7] = bf_hi(v.w);
+}
+
+__device__ __forceinline__ u32x4 pack8(const float f[8]) {
+  u32x4 v;
+  v.x = pack_bf16x2(f[0], f[1]);
+  v.y = pack_bf16x2(f[2], f[3]);
+  v.z = pack_bf16x2(f[4], f[5]);
+  v.w = pack_bf16x2(f[6], f[7]);
+  return v;
+}
+
+// Element group moved by one lane per step: VEC = 8 (one 16-byte vector) or
+// VEC = 1 (one bf16 scalar).  `idx` counts groups, so the element offset is
+// idx * VEC.
+template <int VEC>
+struct Lanes;
+
+template <>
+struct Lanes<8> {
+  __device__ static __forceinline__ void load(const uint16_t* __restrict__ row, int idx, float f[8]) {
+    unpack8(ld_stream(reinterpret_cast<const u32x4*>(row) + idx), f);
+  }
+  __device__ static __forceinline__ void store(uint16_t* __restrict__ row, int idx, const float f[8]) {
+    st_stream(reinterpret_cast<u32x4*>(row) + idx, pack8(f));
+  }
+};
+
+template <>
+struct Lanes<1> {
+  __device__ static __forceinline__ void load(const uint16_t* __restrict__ row, int idx, float f[1]) {
+    f[0] = bf16_to_f32(row[idx]);
+  }
+  __device__ static __forceinline__ void store(uint16_t* __restrict__ row, int idx, const float f[1]) {
+    row[idx] = f32_to_bf16(f[0]);
+  }
+};
+
+// Sum over the LPT consecutive lanes that share one token (LPT a power of
+// two <= 64).  Every lane of the group receives the total.
+template <int LPT>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int m = LPT / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  return v;
+}
+
+// Status helpers shared by the C entry points.
+inline int hip_status(hipError_t e) {
+  return e == hipSuccess ? FMHC_OK : FMHC_ERR_HIP_BASE + static_cast<int>(e);
+}
+
+inline int launch_status() { return hip_status(hipGetLastError()); }
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline unsigned int blocks_for(int64_t items, int64_t per_block) {
+  return static_cast<unsigned int>((items + per_block - 1) / per_block);
+}
+
+}  // namespace fmhc

@@ -1,0 +1,381 @@
+// K1: fused RMSNorm over the flattened n*C stream + the D_out = 32 wide
+// coefficient projection, and the x-gradient of that op.
+//
+//   forward   inv_rms[t] = rsqrt(sum_k x[t,k]^2 / nC + 1e-6)
+//             out[t,d]   = bf16(inv_rms[t] * sum_k x[t,k] * W[d,k])
+//   backward  scale[t]    = (sum_d go[t,d] * proj_out[t,d]) * inv_rms[t]^2 / nC
+//             grad_x[t,k] = bf16(inv_rms[t] * sum_d go[t,d] * W[d,k] - scale[t] * x[t,k])
+//
+// Follows src/flash_mhc/kernels.py:250-303 (forward: project first, then
+// normalise, eps 1e-6) and :306-376 (dx from the stored bf16 projection, no
+// second pass over x).  Both contractions run on the gfx950 matrix cores with
+// v_mfma_f32_16x16x32_bf16.  Operand layout of that instruction, for lane l:
+//   A (16 x 32): lane l holds A[l & 15][8 * (l >> 4) + e], e = 0..7
+//   B (32 x 16): lane l holds B[8 * (l >> 4) + e][l & 15]
+//   D (16 x 16): lane l, register q holds D[4 * (l >> 4) + q][l & 15]
+// Because the contraction index may be permuted freely (as long as A and B
+// agree), each lane's eight contraction values are eight consecutive bf16 in
+// memory: one 16-byte load.
+#include "fmhc_common.h"
+
+namespace fmhc {
+
+namespace {
+
+constexpr int kDout = 32;
+constexpr float kEps = 1e-6f;
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// K1 forward, matrix-core path (nC % 8 == 0, 16-byte aligned x / W / out).
+//
+// A workgroup owns 16*R consecutive tokens and SPLIT waves.  The nC axis is
+// cut into 64-wide chunks; wave w accumulates chunks w, w + SPLIT, ... for all
+// of the workgroup's tokens (so the waves of a workgroup read adjacent
+// 128-byte pieces of the same x rows), then the SPLIT partial results are
+// summed in LDS in a fixed order.  Per chunk and token block the MFMA is
+//   D (32 d x 16 tokens) += W[:, chunk] (A, two 16-row halves) * x[tokens, chunk]^T (B)
+// so D's layout gives every lane 4 consecutive d of one token.  The sum of
+// squares also runs on the matrix cores: the same x registers are both A and
+// B of a third MFMA, G (16 x 16) += x x^T, whose diagonal is sum_k x[t,k]^2
+// in fp32 (the bf16 products are exact).
+template <int R, int SPLIT>
+__global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __restrict__ x,
+                                                             const uint16_t* __restrict__ W,
+                                                             uint16_t* __restrict__ out,
+                                                             float* __restrict__ inv_rms,
+                                                             int64_t T, int nC) {
+  __shared__ float red_acc[SPLIT][R][8][kWave];
+  __shared__ float red_ss[SPLIT][R][16];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+  const int row = lane & 15;
+  const int grp = lane >> 4;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * (16 * R);
+
+  const uint16_t* xrow[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    int64_t t = t0 + 16 * r + row;
+    t = t < T ? t : T - 1;  // tail rows re-read the last token; their results are not stored
+    xrow[r] = x + t * nC + 8 * grp;
+  }
+  const uint16_t* w0 = W + static_cast<int64_t>(row) * nC + 8 * grp;
+  const uint16_t* w1 = W + static_cast<int64_t>(16 + row) * nC + 8 * grp;
+
+  f32x4 acc[2][R];
+  f32x4 gram[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    acc[0][r] = f32x4{0.f, 0.f, 0.f, 0.f};
+    acc[1][r] = f32x4{0.f, 0.f, 0.f, 0.f};
+    gram[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  const int nfull = nC >> 6;
+  for (int c = wave; c < nfull; c += SPLIT) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int k = c * 64 + 32 * s;
+      const bf16x8 wa = as_bf16x8(*reinterpret_cast<const u32x4*>(w0 + k));
+      const bf16x8 wb = as_bf16x8(*reinterpret_cast<const u32x4*>(w1 + k));
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const bf16x8 xb = as_bf16x8(ld_stream(reinterpret_cast<const u32x4*>(xrow[r] + k)));
+        acc[0][r] = mfma16(wa, xb, acc[0][r]);
+        acc[1][r] = mfma16(wb, xb, acc[1][r]);
+        gram[r] = mfma16(xb, xb, gram[r]);
+      }
+    }
+  }
+  // Ragged last chunk (nC % 64 != 0): 16-byte pieces past nC contribute zero.
+  if ((nC & 63) != 0 && wave == nfull % SPLIT) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int k = nfull * 64 + 32 * s;
+      const bool ok = k + 8 * grp < nC;
+      u32x4 wav = {0u, 0u, 0u, 0u}, wbv = {0u, 0u, 0u, 0u};
+      if (ok) {
+        wav = *reinterpret_cast<const u32x4*>(w0 + k);
+        wbv = *reinterpret_cast<const u32x4*>(w1 + k);
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        u32x4 xv = {0u, 0u, 0u, 0u};
+        if (ok) xv = ld_stream(reinterpret_cast<const u32x4*>(xrow[r] + k));
+        const bf16x8 xb = as_bf16x8(xv);
+        acc[0][r] = mfma16(as_bf16x8(wav), xb, acc[0][r]);
+        acc[1][r] = mfma16(as_bf16x8(wbv), xb, acc[1][r]);
+        gram[r] = mfma16(xb, xb, gram[r]);
+      }
+    }
+  }
+
+  // Diagonal G[row][row] sits in lane row + 16 * (row >> 2), register row & 3.
+  const int q_diag = row & 3;
+  const bool holds_diag = grp == (row >> 2);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const f32x4 gr = gram[r];
+    const float diag = q_diag == 0 ? gr[0] : q_diag == 1 ? gr[1] : q_diag == 2 ? gr[2] : gr[3];
+    if (holds_diag) red_ss[wave][r][row] = diag;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      red_acc[wave][r][q][lane] = acc[0][r][q];
+      red_acc[wave][r][4 + q][lane] = acc[1][r][q];
+    }
+  }
+  __syncthreads();
+
+  for (int r = wave; r < R; r += SPLIT) {
+    float a[8];
+    float s2 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a[i] = 0.f;
+#pragma unroll
+    for (int w = 0; w < SPLIT; ++w) {
+      s2 += red_ss[w][r][row];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a[i] += red_acc[w][r][i][lane];
+    }
+    const float inv = rsqrtf(s2 / static_cast<float>(nC) + kEps);
+    const int64_t t = t0 + 16 * r + row;
+    if (t < T) {
+      uint16_t* orow = out + t * kDout + 4 * grp;
+      u32x2 lo2 = {pack_bf16x2(a[0] * inv, a[1] * inv), pack_bf16x2(a[2] * inv, a[3] * inv)};
+      u32x2 hi2 = {pack_bf16x2(a[4] * inv, a[5] * inv), pack_bf16x2(a[6] * inv, a[7] * inv)};
+      st_stream(reinterpret_cast<u32x2*>(orow), lo2);
+      st_stream(reinterpret_cast<u32x2*>(orow + 16), hi2);
+      if (grp == 0) inv_rms[t] = inv;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// K1 backward dx, matrix-core path (nC % 8 == 0, 16-byte aligned x / go /
+// proj_out / grad_x).
+//
+// Each wave owns a 128-wide slice of the nC axis and walks NTB blocks of 16
+// tokens.  Per token block one MFMA per 16-row tile computes
+//   D (16 k x 16 tokens) = W^T[k tile, 0:32] (A) * go[tokens, 0:32]^T (B),
+// i.e. the whole D_out = 32 contraction in one instruction.  The eight A
+// tiles (W^T for the wave's 128 k) are loaded once per wave and stay in
+// registers.  Tile m's row i stands for
+//   k(m, i) = k_slice + 32 * (m >> 1) + 8 * (i >> 2) + 4 * (m & 1) + (i & 3)
+// which makes the two tiles 2u, 2u + 1 give each lane 8 consecutive k of its
+// token: x is read and grad_x written as one 16-byte vector per lane, and each
+// store instruction covers 64 contiguous bytes of 16 token rows.
+template <int NTB>
+__global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ x,
+                                                   const uint16_t* __restrict__ W,
+                                                   const uint16_t* __restrict__ go,
+                                                   const uint16_t* __restrict__ proj,
+                                                   const float* __restrict__ inv_rms,
+                                                   uint16_t* __restrict__ gx,
+                                                   int64_t T, int nC, int nslices) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+  const int row = lane & 15;
+  const int grp = lane >> 4;
+  const int64_t wid = static_cast<int64_t>(blockIdx.x) * 4 + wave;
+  const int slice = static_cast<int>(wid % nslices);
+  const int64_t run = wid / nslices;
+  const int64_t tb0 = run * NTB * 16;
+  if (tb0 >= T) return;
+  const int kw = slice * 128;
+
+  bf16x8 afr[8];
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    const int k = kw + 32 * (m >> 1) + 8 * (row >> 2) + 4 * (m & 1) + (row & 3);
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (k < nC) {
+      const uint16_t* wc = W + static_cast<int64_t>(8 * grp) * nC + k;
+      uint32_t e[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) e[i] = wc[static_cast<int64_t>(i) * nC];
+      v.x = e[0] | (e[1] << 16);
+      v.y = e[2] | (e[3] << 16);
+      v.z = e[4] | (e[5] << 16);
+      v.w = e[6] | (e[7] << 16);
+    }
+    afr[m] = as_bf16x8(v);
+  }
+
+  for (int tb = 0; tb < NTB; ++tb) {
+    const int64_t tbase = tb0 + 16 * tb;
+    if (tbase >= T) break;
+    const int64_t t = tbase + row;
+    const int64_t tl = t < T ? t : T - 1;
+
+    const u32x4 gv = *reinterpret_cast<const u32x4*>(go + tl * kDout + 8 * grp);
+    const u32x4 pv = *reinterpret_cast<const u32x4*>(proj + tl * kDout + 8 * grp);
+    const float inv = inv_rms[tl];
+
+    u32x4 xv[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int k = kw + 32 * u + 8 * grp;
+      xv[u] = u32x4{0u, 0u, 0u, 0u};
+      if (k < nC) xv[u] = ld_stream(reinterpret_cast<const u32x4*>(x + tl * nC + k));
+    }
+
+    float gf[8], pf[8];
+    unpack8(gv, gf);
+    unpack8(pv, pf);
+    float dot = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dot = __builtin_fmaf(gf[e], pf[e], dot);
+    dot += __shfl_xor(dot, 16, kWave);
+    dot += __shfl_xor(dot, 32, kWave);
+    const float scale = dot * (inv * inv) / static_cast<float>(nC);
+
+    const bf16x8 b = as_bf16x8(gv);
+    f32x4 acc[8];
+#pragma unroll
+    for (int m = 0; m < 8; ++m) acc[m] = mfma16(afr[m], b, f32x4{0.f, 0.f, 0.f, 0.f});
+
+    if (t < T) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int k = kw + 32 * u + 8 * grp;
+        if (k < nC) {
+          float xf[8], o[8];
+          unpack8(xv[u], xf);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            o[q] = inv * acc[2 * u][q] - scale * xf[q];
+            o[4 + q] = inv * acc[2 * u + 1][q] - scale * xf[4 + q];
+          }
+          st_stream(reinterpret_cast<u32x4*>(gx + t * nC + k), pack8(o));
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Element-wise paths for shapes or alignments the matrix-core paths do not
+// take (nC % 8 != 0, or a base pointer not 16-byte aligned).  One wave per
+// token; results agree with the matrix-core paths to fp32 summation order.
+__global__ __launch_bounds__(256) void k1_fwd_scalar(const uint16_t* __restrict__ x,
+                                                     const uint16_t* __restrict__ W,
+                                                     uint16_t* __restrict__ out,
+                                                     float* __restrict__ inv_rms,
+                                                     int64_t T, int nC) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + wave;
+  if (t >= T) return;
+  const uint16_t* xr = x + t * nC;
+  float acc[kDout];
+#pragma unroll
+  for (int d = 0; d < kDout; ++d) acc[d] = 0.f;
+  float ss = 0.f;
+  for (int k = lane; k < nC; k += kWave) {
+    const float xv = bf16_to_f32(xr[k]);
+    ss = __builtin_fmaf(xv, xv, ss);
+#pragma unroll
+    for (int d = 0; d < kDout; ++d)
+      acc[d] = __builtin_fmaf(xv, bf16_to_f32(W[static_cast<int64_t>(d) * nC + k]), acc[d]);
+  }
+  ss = group_sum<kWave>(ss);
+#pragma unroll
+  for (int d = 0; d < kDout; ++d) acc[d] = group_sum<kWave>(acc[d]);
+  const float inv = rsqrtf(ss / static_cast<float>(nC) + kEps);
+  if (lane == 0) {
+    inv_rms[t] = inv;
+#pragma unroll
+    for (int d = 0; d < kDout; ++d) out[t * kDout + d] = f32_to_bf16(acc[d] * inv);
+  }
+}
+
+__global__ __launch_bounds__(256) void k1_bwd_scalar(const uint16_t* __restrict__ x,
+                                                     const uint16_t* __restrict__ W,
+                                                     const uint16_t* __restrict__ go,
+                                                     const uint16_t* __restrict__ proj,
+                                                     const float* __restrict__ inv_rms,
+                                                     uint16_t* __restrict__ gx,
+                                                     int64_t T, int nC) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + wave;
+  if (t >= T) return;
+  float g[kDout];
+  float dot = 0.f;
+#pragma unroll
+  for (int d = 0; d < kDout; ++d) {
+    g[d] = bf16_to_f32(go[t * kDout + d]);
+    dot = __builtin_fmaf(g[d], bf16_to_f32(proj[t * kDout + d]), dot);
+  }
+  const float inv = inv_rms[t];
+  const float scale = dot * (inv * inv) / static_cast<float>(nC);
+  const uint16_t* xr = x + t * nC;
+  uint16_t* gr = gx + t * nC;
+  for (int k = lane; k < nC; k += kWave) {
+    float s = 0.f;
+#pragma unroll
+    for (int d = 0; d < kDout; ++d)
+      s = __builtin_fmaf(g[d], bf16_to_f32(W[static_cast<int64_t>(d) * nC + k]), s);
+    gr[k] = f32_to_bf16(inv * s - scale * bf16_to_f32(xr[k]));
+  }
+}
+
+constexpr int kFwdR = 4;      // token blocks of 16 per workgroup
+constexpr int kFwdSplit = 4;  // waves per workgroup (split of the nC axis)
+constexpr int kBwdNTB = 16;   // token blocks of 16 per wave
+
+bool bad_sizes(int64_t T, int64_t nC, int64_t D_out) {
+  return T < 0 || nC <= 0 || nC > (int64_t{1} << 30) || D_out != kDout;
+}
+
+}  // namespace
+}  // namespace fmhc
+
+extern "C" int fmhc_k1_fwd(const uint16_t* x_flat, const uint16_t* W, uint16_t* out,
+                           float* inv_rms, int64_t T, int64_t nC, int64_t D_out, void* stream) {
+  using namespace fmhc;
+  if (bad_sizes(T, nC, D_out)) return FMHC_ERR_INVALID_ARGUMENT;
+  if (T == 0) return FMHC_OK;
+  if (!x_flat || !W || !out || !inv_rms) return FMHC_ERR_INVALID_ARGUMENT;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int nc = static_cast<int>(nC);
+  if (nC % 8 == 0 && aligned16(x_flat) && aligned16(W) && aligned16(out)) {
+    const dim3 grid(blocks_for(T, 16 * kFwdR));
+    k1_fwd_mfma<kFwdR, kFwdSplit><<<grid, kWave * kFwdSplit, 0, s>>>(x_flat, W, out, inv_rms, T, nc);
+  } else {
+    const dim3 grid(blocks_for(T, 4));
+    k1_fwd_scalar<<<grid, 256, 0, s>>>(x_flat, W, out, inv_rms, T, nc);
+  }
+  return launch_status();
+}
+
+extern "C" int fmhc_k1_bwd_dx(const uint16_t* x_flat, const uint16_t* W, const uint16_t* grad_out,
+                              const uint16_t* proj_out, const float* inv_rms, uint16_t* grad_x,
+                              int64_t T, int64_t nC, int64_t D_out, void* stream) {
+  using namespace fmhc;
+  if (bad_sizes(T, nC, D_out)) return FMHC_ERR_INVALID_ARGUMENT;
+  if (T == 0) return FMHC_OK;
+  if (!x_flat || !W || !grad_out || !proj_out || !inv_rms || !grad_x)
+    return FMHC_ERR_INVALID_ARGUMENT;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int nc = static_cast<int>(nC);
+  if (nC % 8 == 0 && aligned16(x_flat) && aligned16(grad_out) && aligned16(proj_out) &&
+      aligned16(grad_x)) {
+    const int nslices = static_cast<int>((nC + 127) / 128);
+    const int64_t nruns = (T + 16 * kBwdNTB - 1) / (16 * kBwdNTB);
+    const dim3 grid(blocks_for(nruns * nslices, 4));
+    k1_bwd_mfma<kBwdNTB><<<grid, 256, 0, s>>>(x_flat, W, grad_out, proj_out, inv_rms, grad_x, T, nc,
+                                              nslices);
+  } else {
+    const dim3 grid(blocks_for(T, 4));
+    k1_bwd_scalar<<<grid, 256, 0, s>>>(x_flat, W, grad_out, proj_out, inv_rms, grad_x, T, nc);
+  }
+  return launch_status();
+}

@@ -1,0 +1,210 @@
+// K3: pre-map of the n = 4 residual streams into the layer input, and its
+// backward.
+//
+//   forward   out[t,c]        = bf16(sum_j h_pre[t,j] * x[t,j,c])       j = 0..3 in order
+//   backward  grad_x[t,j,c]   = bf16(h_pre[t,j] * go[t,c])
+//             grad_h_pre[t,j] = sum_c x[t,j,c] * go[t,c]                 (fp32)
+//
+// Follows src/flash_mhc/kernels.py:673-717 (forward) and :720-853 (fused
+// backward) of the reference, written for gfx950:
+//   * a group of LPT consecutive lanes owns one token; a wave64 holds
+//     64 / LPT tokens.  Each lane streams 16-byte vectors of all four stream
+//     rows, so every x row is read once and every output row written once;
+//   * the four per-token coefficients are wave-uniform when LPT == 64 and then
+//     live in SGPRs;
+//   * the backward's four reductions over C finish with an in-wave butterfly
+//     (no LDS, no atomics), so grad_h_pre is deterministic.
+#include "fmhc_common.h"
+
+namespace fmhc {
+
+namespace {
+
+constexpr int kBlock = 256;  // 4 waves per workgroup
+
+template <int LPT>
+__device__ __forceinline__ int64_t token_of_lane(int lane) {
+  constexpr int TPW = kWave / LPT;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+  const int64_t first = (static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) + wave) * TPW;
+  return LPT == kWave ? first : first + lane / LPT;
+}
+
+template <int VEC, int LPT>
+__global__ __launch_bounds__(kBlock) void k3_fwd_kernel(const uint16_t* __restrict__ x,
+                                                        const float* __restrict__ h_pre,
+                                                        uint16_t* __restrict__ out,
+                                                        int64_t T, int C) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t tok = token_of_lane<LPT>(lane);
+  if (tok >= T) return;
+  const int sub = lane % LPT;
+  const int ng = C / VEC;
+
+  const float* hp = h_pre + tok * 4;
+  const float h0 = hp[0], h1 = hp[1], h2 = hp[2], h3 = hp[3];
+  const uint16_t* x0 = x + tok * 4 * C;
+  const uint16_t* x1 = x0 + C;
+  const uint16_t* x2 = x1 + C;
+  const uint16_t* x3 = x2 + C;
+  uint16_t* orow = out + tok * C;
+
+#pragma unroll 2
+  for (int g = sub; g < ng; g += LPT) {
+    float a[VEC], b[VEC], c[VEC], d[VEC], o[VEC];
+    Lanes<VEC>::load(x0, g, a);
+    Lanes<VEC>::load(x1, g, b);
+    Lanes<VEC>::load(x2, g, c);
+    Lanes<VEC>::load(x3, g, d);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      float acc = h0 * a[e];
+      acc = __builtin_fmaf(h1, b[e], acc);
+      acc = __builtin_fmaf(h2, c[e], acc);
+      o[e] = __builtin_fmaf(h3, d[e], acc);
+    }
+    Lanes<VEC>::store(orow, g, o);
+  }
+}
+
+template <int VEC, int LPT>
+__global__ __launch_bounds__(kBlock) void k3_bwd_kernel(const uint16_t* __restrict__ x,
+                                                        const float* __restrict__ h_pre,
+                                                        const uint16_t* __restrict__ go,
+                                                        uint16_t* __restrict__ grad_x,
+                                                        float* __restrict__ grad_h_pre,
+                                                        int64_t T, int C) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t tok = token_of_lane<LPT>(lane);
+  if (tok >= T) return;
+  const int sub = lane % LPT;
+  const int ng = C / VEC;
+
+  const float* hp = h_pre + tok * 4;
+  const float h0 = hp[0], h1 = hp[1], h2 = hp[2], h3 = hp[3];
+  const uint16_t* x0 = x + tok * 4 * C;
+  const uint16_t* x1 = x0 + C;
+  const uint16_t* x2 = x1 + C;
+  const uint16_t* x3 = x2 + C;
+  const uint16_t* grow = go + tok * C;
+  uint16_t* gx0 = grad_x + tok * 4 * C;
+  uint16_t* gx1 = gx0 + C;
+  uint16_t* gx2 = gx1 + C;
+  uint16_t* gx3 = gx2 + C;
+
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll 2
+  for (int g = sub; g < ng; g += LPT) {
+    float q[VEC], a[VEC], b[VEC], c[VEC], d[VEC], o[VEC];
+    Lanes<VEC>::load(grow, g, q);
+    Lanes<VEC>::load(x0, g, a);
+    Lanes<VEC>::load(x1, g, b);
+    Lanes<VEC>::load(x2, g, c);
+    Lanes<VEC>::load(x3, g, d);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) o[e] = h0 * q[e];
+    Lanes<VEC>::store(gx0, g, o);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) o[e] = h1 * q[e];
+    Lanes<VEC>::store(gx1, g, o);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) o[e] = h2 * q[e];
+    Lanes<VEC>::store(gx2, g, o);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) o[e] = h3 * q[e];
+    Lanes<VEC>::store(gx3, g, o);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      s0 = __builtin_fmaf(a[e], q[e], s0);
+      s1 = __builtin_fmaf(b[e], q[e], s1);
+      s2 = __builtin_fmaf(c[e], q[e], s2);
+      s3 = __builtin_fmaf(d[e], q[e], s3);
+    }
+  }
+  s0 = group_sum<LPT>(s0);
+  s1 = group_sum<LPT>(s1);
+  s2 = group_sum<LPT>(s2);
+  s3 = group_sum<LPT>(s3);
+  if (sub == 0) {
+    float* dst = grad_h_pre + tok * 4;
+    dst[0] = s0;
+    dst[1] = s1;
+    dst[2] = s2;
+    dst[3] = s3;
+  }
+}
+
+// Lanes per token: a full wave for wide rows, fewer lanes (more tokens per
+// wave) when a row would leave most of a wave idle.
+template <int VEC>
+int pick_lpt(int C) {
+  const int groups = C / VEC;
+  if (groups >= 128) return 64;
+  if (groups >= 32) return 32;
+  if (groups >= 16) return 16;
+  return 8;
+}
+
+template <int VEC>
+int launch_k3_fwd(const uint16_t* x, const float* h_pre, uint16_t* out, int64_t T, int C,
+                  hipStream_t s) {
+  const int lpt = pick_lpt<VEC>(C);
+  const int64_t tokens_per_block = (kBlock / kWave) * (kWave / lpt);
+  const dim3 grid(blocks_for(T, tokens_per_block));
+  switch (lpt) {
+    case 64: k3_fwd_kernel<VEC, 64><<<grid, kBlock, 0, s>>>(x, h_pre, out, T, C); break;
+    case 32: k3_fwd_kernel<VEC, 32><<<grid, kBlock, 0, s>>>(x, h_pre, out, T, C); break;
+    case 16: k3_fwd_kernel<VEC, 16><<<grid, kBlock, 0, s>>>(x, h_pre, out, T, C); break;
+    default: k3_fwd_kernel<VEC, 8><<<grid, kBlock, 0, s>>>(x, h_pre, out, T, C); break;
+  }
+  return launch_status();
+}
+
+template <int VEC>
+int launch_k3_bwd(const uint16_t* x, const float* h_pre, const uint16_t* go, uint16_t* grad_x,
+                  float* grad_h_pre, int64_t T, int C, hipStream_t s) {
+  const int lpt = pick_lpt<VEC>(C);
+  const int64_t tokens_per_block = (kBlock / kWave) * (kWave / lpt);
+  const dim3 grid(blocks_for(T, tokens_per_block));
+  switch (lpt) {
+    case 64: k3_bwd_kernel<VEC, 64><<<grid, kBlock, 0, s>>>(x, h_pre, go, grad_x, grad_h_pre, T, C); break;
+    case 32: k3_bwd_kernel<VEC, 32><<<grid, kBlock, 0, s>>>(x, h_pre, go, grad_x, grad_h_pre, T, C); break;
+    case 16: k3_bwd_kernel<VEC, 16><<<grid, kBlock, 0, s>>>(x, h_pre, go, grad_x, grad_h_pre, T, C); break;
+    default: k3_bwd_kernel<VEC, 8><<<grid, kBlock, 0, s>>>(x, h_pre, go, grad_x, grad_h_pre, T, C); break;
+  }
+  return launch_status();
+}
+
+bool bad_sizes(int64_t T, int64_t C, int64_t n) {
+  return T < 0 || C <= 0 || C > (int64_t{1} << 30) || n != 4;
+}
+
+}  // namespace
+}  // namespace fmhc
+
+extern "C" int fmhc_k3_fwd(const uint16_t* x, const float* h_pre, uint16_t* out, int64_t T,
+                           int64_t C, int64_t n, void* stream) {
+  using namespace fmhc;
+  if (bad_sizes(T, C, n)) return FMHC_ERR_INVALID_ARGUMENT;
+  if (T == 0) return FMHC_OK;
+  if (!x || !h_pre || !out) return FMHC_ERR_INVALID_ARGUMENT;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int c = static_cast<int>(C);
+  if (C % 8 == 0 && aligned16(x) && aligned16(out))
+    return launch_k3_fwd<8>(x, h_pre, out, T, c, s);
+  return launch_k3_fwd<1>(x, h_pre, out, T, c, s);
+}
+
+extern "C" int fmhc_k3_bwd(const uint16_t* x, const float* h_pre, const uint16_t* grad_out,
+                           uint16_t* grad_x, float* grad_h_pre, int64_t T, int64_t C, int64_t n,
+                           void* stream) {
+  using namespace fmhc;
+  if (bad_sizes(T, C, n)) return FMHC_ERR_INVALID_ARGUMENT;
+  if (T == 0) return FMHC_OK;
+  if (!x || !h_pre || !grad_out || !grad_x || !grad_h_pre) return FMHC_ERR_INVALID_ARGUMENT;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int c = static_cast<int>(C);
+  if (C % 8 == 0 && aligned16(x) && aligned16(grad_out) && aligned16(grad_x))
+    return launch_k3_bwd<8>(x, h_pre, grad_out, grad_x, grad_h_pre, T, c, s);
+  return launch_k3_bwd<1>(x, h_pre, grad_out, grad_x, grad_h_pre, T, c, s);
+}

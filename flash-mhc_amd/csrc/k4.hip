@@ -1,0 +1,278 @@
+// K4: post-mixing (residual stream mix + post-weighted layer output) and its
+// backward.
+//
+//   forward   out[t,i,c]    = bf16(h_post[t,i] * lo[t,c] + sum_j H[t,i,j] * x[t,j,c])
+//   backward  grad_lo[t,c]  = bf16(sum_i h_post[t,i] * go[t,i,c])
+//             grad_hp[t,i]  = sum_c go[t,i,c] * lo[t,c]           (fp32)
+//             grad_H[t,i,j] = sum_c go[t,i,c] * x[t,j,c]          (fp32)
+//             grad_x[t,j,c] = bf16(sum_i H[t,i,j] * go[t,i,c])
+//
+// Follows src/flash_mhc/kernels.py:384-481 (forward) and :487-665 (fused
+// backward) of the reference, written for gfx950: a group of LPT consecutive
+// lanes owns one token and streams 16-byte vectors of every row it touches, so
+// each input row is read once and each output row written once per launch.
+// The backward keeps its 20 per-token partial sums in registers and finishes
+// them with an in-wave butterfly: no LDS, no atomics, deterministic.
+#include "fmhc_common.h"
+
+namespace fmhc {
+
+namespace {
+
+constexpr int kBlock = 256;  // 4 waves per workgroup
+
+template <int LPT>
+__device__ __forceinline__ int64_t token_of_lane(int lane) {
+  constexpr int TPW = kWave / LPT;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+  const int64_t first = (static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) + wave) * TPW;
+  return LPT == kWave ? first : first + lane / LPT;
+}
+
+template <int VEC, int LPT>
+__global__ __launch_bounds__(kBlock) void k4_fwd_kernel(const uint16_t* __restrict__ x,
+                                                        const uint16_t* __restrict__ lo,
+                                                        const float* __restrict__ H,
+                                                        const float* __restrict__ h_post,
+                                                        uint16_t* __restrict__ out,
+                                                        int64_t T, int C) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t tok = token_of_lane<LPT>(lane);
+  if (tok >= T) return;
+  const int sub = lane % LPT;
+  const int ng = C / VEC;
+
+  float h[4][4], p[4];
+  {
+    const float* Ht = H + tok * 16;
+    const float* pt = h_post + tok * 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      p[i] = pt[i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) h[i][j] = Ht[i * 4 + j];
+    }
+  }
+  const uint16_t* xr[4];
+  uint16_t* orow[4];
+  xr[0] = x + tok * 4 * C;
+  orow[0] = out + tok * 4 * C;
+#pragma unroll
+  for (int j = 1; j < 4; ++j) {
+    xr[j] = xr[j - 1] + C;
+    orow[j] = orow[j - 1] + C;
+  }
+  const uint16_t* lrow = lo + tok * C;
+
+#pragma unroll 2
+  for (int g = sub; g < ng; g += LPT) {
+    float l[VEC], xv[4][VEC];
+    Lanes<VEC>::load(lrow, g, l);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) Lanes<VEC>::load(xr[j], g, xv[j]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float o[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        float acc = p[i] * l[e];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc = __builtin_fmaf(h[i][j], xv[j][e], acc);
+        o[e] = acc;
+      }
+      Lanes<VEC>::store(orow[i], g, o);
+    }
+  }
+}
+
+template <int VEC, int LPT>
+__global__ __launch_bounds__(kBlock) void k4_bwd_kernel(const uint16_t* __restrict__ x,
+                                                        const uint16_t* __restrict__ lo,
+                                                        const float* __restrict__ H,
+                                                        const float* __restrict__ h_post,
+                                                        const uint16_t* __restrict__ go,
+                                                        uint16_t* __restrict__ grad_x,
+                                                        uint16_t* __restrict__ grad_lo,
+                                                        float* __restrict__ grad_H,
+                                                        float* __restrict__ grad_hp,
+                                                        int64_t T, int C) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t tok = token_of_lane<LPT>(lane);
+  if (tok >= T) return;
+  const int sub = lane % LPT;
+  const int ng = C / VEC;
+
+  float h[4][4], p[4];
+  {
+    const float* Ht = H + tok * 16;
+    const float* pt = h_post + tok * 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      p[i] = pt[i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) h[i][j] = Ht[i * 4 + j];
+    }
+  }
+  const uint16_t* xr[4];
+  const uint16_t* gr[4];
+  uint16_t* gxr[4];
+  xr[0] = x + tok * 4 * C;
+  gr[0] = go + tok * 4 * C;
+  gxr[0] = grad_x + tok * 4 * C;
+#pragma unroll
+  for (int j = 1; j < 4; ++j) {
+    xr[j] = xr[j - 1] + C;
+    gr[j] = gr[j - 1] + C;
+    gxr[j] = gxr[j - 1] + C;
+  }
+  const uint16_t* lrow = lo + tok * C;
+  uint16_t* glrow = grad_lo + tok * C;
+
+  float shp[4] = {0.f, 0.f, 0.f, 0.f};
+  float sH[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sH[i][j] = 0.f;
+
+#pragma unroll 2
+  for (int g = sub; g < ng; g += LPT) {
+    float q[4][VEC], l[VEC];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) Lanes<VEC>::load(gr[i], g, q[i]);
+    Lanes<VEC>::load(lrow, g, l);
+
+    // grad_lo and the grad_h_post partial sums.
+    {
+      float o[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        float acc = p[0] * q[0][e];
+        acc = __builtin_fmaf(p[1], q[1][e], acc);
+        acc = __builtin_fmaf(p[2], q[2][e], acc);
+        o[e] = __builtin_fmaf(p[3], q[3][e], acc);
+      }
+      Lanes<VEC>::store(glrow, g, o);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) shp[i] = __builtin_fmaf(q[i][e], l[e], shp[i]);
+    }
+
+    // One x stream at a time: grad_H partial sums and grad_x.
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float xv[VEC], o[VEC];
+      Lanes<VEC>::load(xr[j], g, xv);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) sH[i][j] = __builtin_fmaf(q[i][e], xv[e], sH[i][j]);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        float acc = h[0][j] * q[0][e];
+        acc = __builtin_fmaf(h[1][j], q[1][e], acc);
+        acc = __builtin_fmaf(h[2][j], q[2][e], acc);
+        o[e] = __builtin_fmaf(h[3][j], q[3][e], acc);
+      }
+      Lanes<VEC>::store(gxr[j], g, o);
+    }
+  }
+
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    shp[i] = group_sum<LPT>(shp[i]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sH[i][j] = group_sum<LPT>(sH[i][j]);
+  }
+  if (sub == 0) {
+    float* dH = grad_H + tok * 16;
+    float* dp = grad_hp + tok * 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      dp[i] = shp[i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) dH[i * 4 + j] = sH[i][j];
+    }
+  }
+}
+
+template <int VEC>
+int pick_lpt(int C) {
+  const int groups = C / VEC;
+  if (groups >= 128) return 64;
+  if (groups >= 32) return 32;
+  if (groups >= 16) return 16;
+  return 8;
+}
+
+template <int VEC>
+int launch_k4_fwd(const uint16_t* x, const uint16_t* lo, const float* H, const float* hp,
+                  uint16_t* out, int64_t T, int C, hipStream_t s) {
+  const int lpt = pick_lpt<VEC>(C);
+  const int64_t tokens_per_block = (kBlock / kWave) * (kWave / lpt);
+  const dim3 grid(blocks_for(T, tokens_per_block));
+  switch (lpt) {
+    case 64: k4_fwd_kernel<VEC, 64><<<grid, kBlock, 0, s>>>(x, lo, H, hp, out, T, C); break;
+    case 32: k4_fwd_kernel<VEC, 32><<<grid, kBlock, 0, s>>>(x, lo, H, hp, out, T, C); break;
+    case 16: k4_fwd_kernel<VEC, 16><<<grid, kBlock, 0, s>>>(x, lo, H, hp, out, T, C); break;
+    default: k4_fwd_kernel<VEC, 8><<<grid, kBlock, 0, s>>>(x, lo, H, hp, out, T, C); break;
+  }
+  return launch_status();
+}
+
+template <int VEC>
+int launch_k4_bwd(const uint16_t* x, const uint16_t* lo, const float* H, const float* hp,
+                  const uint16_t* go, uint16_t* gx, uint16_t* glo, float* gH, float* ghp,
+                  int64_t T, int C, hipStream_t s) {
+  const int lpt = pick_lpt<VEC>(C);
+  const int64_t tokens_per_block = (kBlock / kWave) * (kWave / lpt);
+  const dim3 grid(blocks_for(T, tokens_per_block));
+  switch (lpt) {
+    case 64: k4_bwd_kernel<VEC, 64><<<grid, kBlock, 0, s>>>(x, lo, H, hp, go, gx, glo, gH, ghp, T, C); break;
+    case 32: k4_bwd_kernel<VEC, 32><<<grid, kBlock, 0, s>>>(x, lo, H, hp, go, gx, glo, gH, ghp, T, C); break;
+    case 16: k4_bwd_kernel<VEC, 16><<<grid, kBlock, 0, s>>>(x, lo, H, hp, go, gx, glo, gH, ghp, T, C); break;
+    default: k4_bwd_kernel<VEC, 8><<<grid, kBlock, 0, s>>>(x, lo, H, hp, go, gx, glo, gH, ghp, T, C); break;
+  }
+  return launch_status();
+}
+
+bool bad_sizes(int64_t T, int64_t C, int64_t n) {
+  return T < 0 || C <= 0 || C > (int64_t{1} << 30) || n != 4;
+}
+
+}  // namespace
+}  // namespace fmhc
+
+extern "C" int fmhc_k4_fwd(const uint16_t* x, const uint16_t* lo, const float* H,
+                           const float* h_post, uint16_t* out, int64_t T, int64_t C, int64_t n,
+                           void* stream) {
+  using namespace fmhc;
+  if (bad_sizes(T, C, n)) return FMHC_ERR_INVALID_ARGUMENT;
+  if (T == 0) return FMHC_OK;
+  if (!x || !lo || !H || !h_post || !out) return FMHC_ERR_INVALID_ARGUMENT;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int c = static_cast<int>(C);
+  if (C % 8 == 0 && aligned16(x) && aligned16(lo) && aligned16(out))
+    return launch_k4_fwd<8>(x, lo, H, h_post, out, T, c, s);
+  return launch_k4_fwd<1>(x, lo, H, h_post, out, T, c, s);
+}
+
+extern "C" int fmhc_k4_bwd(const uint16_t* x, const uint16_t* lo, const float* H,
+                           const float* h_post, const uint16_t* grad_out, uint16_t* grad_x,
+                           uint16_t* grad_lo, float* grad_H, float* grad_h_post, int64_t T,
+                           int64_t C, int64_t n, void* stream) {
+  using namespace fmhc;
+  if (bad_sizes(T, C, n)) return FMHC_ERR_INVALID_ARGUMENT;
+  if (T == 0) return FMHC_OK;
+  if (!x || !lo || !H || !h_post || !grad_out || !grad_x || !grad_lo || !grad_H || !grad_h_post)
+    return FMHC_ERR_INVALID_ARGUMENT;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int c = static_cast<int>(C);
+  if (C % 8 == 0 && aligned16(x) && aligned16(lo) && aligned16(grad_out) && aligned16(grad_x) &&
+      aligned16(grad_lo))
+    return launch_k4_bwd<8>(x, lo, H, h_post, grad_out, grad_x, grad_lo, grad_H, grad_h_post, T,
+                            c, s);
+  return launch_k4_bwd<1>(x, lo, H, h_post, grad_out, grad_x, grad_lo, grad_H, grad_h_post, T, c,
+                          s);
+}

@@ -1,0 +1,201 @@
+"""mHC-lite residual wrapper with the gfx950 HIP fused path.
+
+``MHCLiteBlock`` keeps the reference's public surface
+(alint77/flash-mHC ``src/flash_mhc/block.py``): constructor arguments,
+attribute / parameter / buffer names and their registration order (hence the
+``state_dict`` keys and the RNG draws at construction), the fused-path
+predicate (``block.py:221-231``), the activation-checkpoint predicate
+(``block.py:74-80``) and the method names ``_forward_pytorch`` /
+``_forward_triton`` that callers use directly.
+
+Per layer, with x of shape (T, n, C):
+  K1  proj, inv_rms = rmsnorm-project(x.reshape(T, nC), W_all.weight)   HIP kernel
+  K2  h_pre = sigmoid(a_pre * proj[:, :n] + b), h_post = 2 sigmoid(...),
+      H_res = softmax(a_res * proj[:, 2n:] + b) @ perm, H_merged = H_res - h_post h_pre^T
+                                                                         PyTorch ops
+  K3  layer_input = sum_j h_pre[:, j] x[:, j]                             HIP kernel
+      layer_output = layer(layer_input)                                  user module
+  K4  out = H_merged @ x + h_post (x) layer_output                       HIP kernel
+
+The fused path runs for GPU bf16 inputs of shape (T, 4, C); every other input
+(other n, other dtypes, CPU tensors, extra leading dims) takes the plain
+PyTorch formulation of the same block, as in the reference.
+"""
+
+from __future__ import annotations
+
+import itertools
+import math
+from contextlib import nullcontext
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+from torch.utils.checkpoint import checkpoint as _checkpoint
+
+from . import ops as _ops
+
+
+def build_permutation_matrices(n: int) -> tuple[torch.Tensor, int]:
+    """All n x n permutation matrices, flattened: shape (n!, n*n), values {0, 1}.
+
+    Row m is the permutation number m of ``itertools.permutations(range(n))``
+    (lexicographic order), with entry ``[m, i*n + j] = 1`` iff that permutation
+    maps i to j.  Index 0 is the identity.  Same layout as the reference's
+    ``build_permutation_matrices`` (block.py:21-32).
+    """
+    if n < 1:
+        raise ValueError(f"n must be >= 1, got {n}")
+    images = torch.tensor(list(itertools.permutations(range(n))), dtype=torch.long)
+    mats = torch.zeros(images.shape[0], n, n)
+    mats.scatter_(2, images.unsqueeze(-1), 1.0)
+    return mats.reshape(images.shape[0], n * n), 0
+
+
+class MHCLiteBlock(nn.Module):
+    """mHC-lite wrapper for a residual layer mapping (T, C) -> (T, C).
+
+    Args:
+        n_streams: number of residual streams n (the fused path needs n == 4).
+        hidden_size: C.
+        layer: module applied to the pre-mixed (T, C) input.
+        triton_fused: use the fused device path when the input qualifies (the
+            name is the reference's; here the fused path is HIP, not Triton).
+        activation_checkpointing: recompute the pre-map and post-res regions
+            in backward instead of keeping their activations.
+    """
+
+    def __init__(
+        self,
+        n_streams: int,
+        hidden_size: int,
+        layer: nn.Module,
+        triton_fused: bool = True,
+        activation_checkpointing: bool = False,
+    ) -> None:
+        super().__init__()
+        self.n = n_streams
+        self.C = hidden_size
+        self.nC = n_streams * hidden_size
+        self.layer = layer
+        self.triton_fused = triton_fused
+        self.activation_checkpointing = activation_checkpointing
+
+        self.n_fact = math.factorial(n_streams)
+
+        self.alpha_pre = nn.Parameter(torch.tensor([0.01]))
+        self.alpha_post = nn.Parameter(torch.tensor([0.01]))
+        self.alpha_res = nn.Parameter(torch.tensor([0.01]))
+
+        self.W_all = nn.Linear(self.nC, 2 * n_streams + self.n_fact, bias=True)
+
+        perm_flat, self.identity_idx = build_permutation_matrices(n_streams)
+        self.register_buffer("perm_mat", perm_flat)
+
+    # -- shared pieces ------------------------------------------------------
+
+    def _use_activation_checkpointing(self, x_streams: torch.Tensor) -> bool:
+        return (
+            self.activation_checkpointing
+            and self.training
+            and torch.is_grad_enabled()
+            and x_streams.requires_grad
+        )
+
+    def _coefficients(
+        self, proj: torch.Tensor, dt: torch.dtype
+    ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        """K2: mixing coefficients from the (..., 2n + n!) projection, in dtype dt.
+
+        Same operations, in the same order and precision, as the reference's
+        block.py:93-105 (fallback) and :162-170 (fused path).
+        """
+        n = self.n
+        pre, post, res = proj.split([n, n, self.n_fact], dim=-1)
+        bias = self.W_all.bias.to(dt)
+        h_pre = torch.sigmoid(self.alpha_pre.to(dt) * pre + bias[:n])
+        h_post = 2.0 * torch.sigmoid(self.alpha_post.to(dt) * post + bias[n : 2 * n])
+        a_res = F.softmax(self.alpha_res.to(dt) * res + bias[2 * n :], dim=-1)
+        H_res = torch.matmul(a_res, self.perm_mat.to(dt)).unflatten(-1, (n, n))
+        H_merged = H_res - h_post.unsqueeze(-1) * h_pre.unsqueeze(-2)
+        return h_pre, h_post, H_merged
+
+    # -- plain PyTorch formulation (block.py:82-148) ------------------------
+
+    def _mhc_coeffs_pytorch(self, x_streams: torch.Tensor):
+        dt = x_streams.dtype
+        x_flat = x_streams.reshape(*x_streams.shape[:-2], self.nC)
+        x_norm = F.rms_norm(x_flat, (self.nC,))
+        proj = F.linear(x_norm, self.W_all.weight.to(dt), None)
+        return self._coefficients(proj, dt)
+
+    def _mhc_pre_map_pytorch(self, x_streams: torch.Tensor):
+        h_pre, h_post, H_merged = self._mhc_coeffs_pytorch(x_streams)
+        layer_input = torch.matmul(h_pre.unsqueeze(-2), x_streams).squeeze(-2)
+        return layer_input, H_merged, h_post
+
+    def _mhc_post_res_pytorch(self, x_streams, layer_output, H_merged, h_post):
+        return (
+            torch.matmul(H_merged, x_streams)
+            + h_post.unsqueeze(-1) * layer_output.unsqueeze(-2)
+        )
+
+    def _forward_pytorch(self, x_streams: torch.Tensor, **kwargs) -> torch.Tensor:
+        return self._run(
+            x_streams, self._mhc_pre_map_pytorch, self._mhc_post_res_pytorch, nullcontext(), kwargs
+        )
+
+    # -- fused HIP path (block.py:150-219) ------------------------------------
+
+    def _mhc_coeffs_triton(self, x_streams: torch.Tensor):
+        dt = x_streams.dtype
+        T = x_streams.shape[0]
+        proj, _inv_rms = torch.ops.flash_mhc.fused_rmsnorm_project(
+            x_streams.reshape(T, self.nC), self.W_all.weight.to(dt)
+        )
+        return self._coefficients(proj, dt)
+
+    def _mhc_pre_map_triton(self, x_streams: torch.Tensor):
+        h_pre, h_post, H_merged = self._mhc_coeffs_triton(x_streams)
+        layer_input = torch.ops.flash_mhc.fused_pre_map(x_streams, h_pre.float())
+        return layer_input, H_merged.float(), h_post.float()
+
+    def _mhc_post_res_triton(self, x_streams, layer_output, H_merged, h_post):
+        return torch.ops.flash_mhc.fused_post_res(x_streams, layer_output, H_merged, h_post)
+
+    def _forward_triton(self, x_streams: torch.Tensor, **kwargs) -> torch.Tensor:
+        """Fused path: K1/K3/K4 on the HIP kernels (K2 in PyTorch)."""
+        ctx = nullcontext() if self.training else _ops.disable_autotune_temporarily()
+        return self._run(x_streams, self._mhc_pre_map_triton, self._mhc_post_res_triton, ctx, kwargs)
+
+    # -- common driver ------------------------------------------------------
+
+    def _run(self, x_streams, pre_map, post_res, ctx, kwargs) -> torch.Tensor:
+        use_ckpt = self._use_activation_checkpointing(x_streams)
+        with ctx:
+            if use_ckpt:
+                layer_input, H_merged, h_post = _checkpoint(
+                    pre_map, x_streams, use_reentrant=False
+                )
+            else:
+                layer_input, H_merged, h_post = pre_map(x_streams)
+
+            layer_output = self.layer(layer_input, **kwargs)
+
+            if use_ckpt:
+                return _checkpoint(
+                    post_res, x_streams, layer_output, H_merged, h_post, use_reentrant=False
+                )
+            return post_res(x_streams, layer_output, H_merged, h_post)
+
+    def forward(self, x_streams: torch.Tensor, **kwargs) -> torch.Tensor:
+        use_fused = (
+            self.triton_fused
+            and x_streams.is_cuda
+            and x_streams.dtype == torch.bfloat16
+            and x_streams.dim() == 3
+            and self.n == 4
+        )
+        if use_fused:
+            return self._forward_triton(x_streams, **kwargs)
+        return self._forward_pytorch(x_streams, **kwargs)

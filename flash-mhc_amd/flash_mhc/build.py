@@ -1,0 +1,95 @@
+"""Build the gfx950 HIP extension ``_lib/libflash_mhc_hip.so`` in-tree.
+
+Usage: ``python -m flash_mhc.build`` (run from ``flash-mhc_amd/``) or
+``flash_mhc.build.build()``.  hipcc cross-compiles for gfx950 without a GPU.
+
+Every HIP source is compiled with ``-Xclang -target-feature -Xclang
+-packed-fp32-ops`` so the compiler never emits packed fp32 VALU instructions
+(v_pk_add/mul/fma_f32); the host pass prints a harmless "not a recognized
+feature" warning for it.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+ROOT = PKG_DIR.parent  # flash-mhc_amd/
+CSRC = ROOT / "csrc"
+INCLUDE = ROOT.parent / "include"
+BUILD_DIR = ROOT / "_build"
+LIB_DIR = PKG_DIR / "_lib"
+LIB_NAME = "libflash_mhc_hip.so"
+LIB_PATH = LIB_DIR / LIB_NAME
+
+SOURCES = ("k1.hip", "k3.hip", "k4.hip", "abi.hip")
+
+ARCH = "gfx950"
+
+COMMON_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    "-Wno-unused-function",
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+]
+
+
+def hipcc() -> str:
+    exe = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(exe).exists():
+        raise RuntimeError("hipcc not found; the HIP toolchain (ROCm) is required to build flash_mhc")
+    return exe
+
+
+def _run(cmd: list[str], verbose: bool) -> None:
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(
+            f"command failed ({proc.returncode}): {' '.join(cmd)}\n{proc.stdout}\n{proc.stderr}"
+        )
+    if verbose:
+        # Drop the host pass's warning about the device-only target feature.
+        noise = "packed-fp32-ops' is not a recognized feature"
+        for line in (proc.stdout + proc.stderr).splitlines():
+            if noise not in line and line.strip():
+                print(line)
+
+
+def build(verbose: bool = False, extra_flags: list[str] | None = None, out: Path | None = None) -> Path:
+    """Compile every HIP source and link the shared library. Returns its path."""
+    cc = hipcc()
+    BUILD_DIR.mkdir(parents=True, exist_ok=True)
+    out = Path(out) if out is not None else LIB_PATH
+    out.parent.mkdir(parents=True, exist_ok=True)
+    flags = COMMON_FLAGS + [f"-I{INCLUDE}"] + list(extra_flags or [])
+
+    def compile_one(src: str) -> Path:
+        obj = BUILD_DIR / (Path(src).stem + ".o")
+        _run([cc, *flags, "-c", str(CSRC / src), "-o", str(obj)], verbose)
+        return obj
+
+    jobs = min(len(SOURCES), max(1, (os.cpu_count() or 1)))
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(compile_one, SOURCES))
+    tmp = out.with_suffix(".so.tmp")
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)], verbose)
+    os.replace(tmp, out)
+    return out
+
+
+if __name__ == "__main__":
+    path = build(verbose="-v" in sys.argv)
+    print(path)

@@ -1,0 +1,223 @@
+"""Launchers for the gfx950 HIP kernels (drop-in for the reference's Triton
+``kernels.py``).
+
+Each function validates its tensors, allocates any output that was not passed
+in, and enqueues one kernel through the C ABI on torch's current stream of
+the tensors' device.  Nothing here falls back to another implementation: a
+missing extension or a bad argument raises.
+
+Reference counterparts (alint77/flash-mHC):
+  k1_fwd     <- src/flash_mhc/kernels.py:250-303  _fused_rmsnorm_project_fwd_kernel
+  k1_bwd_dx  <- src/flash_mhc/kernels.py:306-376  _fused_rmsnorm_project_bwd_dx_kernel
+  k3_fwd     <- src/flash_mhc/kernels.py:673-717  _fused_pre_map_fwd_kernel
+  k3_bwd     <- src/flash_mhc/kernels.py:720-853  _fused_pre_map_bwd_fused_kernel_n4
+  k4_fwd     <- src/flash_mhc/kernels.py:384-481  _fused_post_res_fwd_kernel_n4
+  k4_bwd     <- src/flash_mhc/kernels.py:487-665  _fused_post_res_bwd_fused_kernel_n4
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _abi
+
+N_STREAMS = 4
+D_OUT = 32  # 2n + n! at n = 4
+
+_BF16 = torch.bfloat16
+_F32 = torch.float32
+
+
+def _require(t: torch.Tensor, name: str, dtype: torch.dtype, shape: tuple[int, ...], device) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.device != device:
+        raise ValueError(f"{name} is on {t.device}, expected {device}")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} must have shape {tuple(shape)}, got {tuple(t.shape)}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def _device_of(x: torch.Tensor) -> torch.device:
+    if not isinstance(x, torch.Tensor):
+        raise TypeError("expected a torch.Tensor")
+    if x.device.type != "cuda":
+        raise ValueError(f"flash_mhc HIP kernels need a GPU tensor, got device {x.device}")
+    return x.device
+
+
+class _OnDevice:
+    """Make ``device`` current for the launch (cheap when it already is)."""
+
+    __slots__ = ("idx", "prev")
+
+    def __init__(self, device: torch.device):
+        self.idx = device.index if device.index is not None else torch.cuda.current_device()
+        self.prev = None
+
+    def __enter__(self):
+        cur = torch.cuda.current_device()
+        if cur != self.idx:
+            self.prev = cur
+            torch.cuda.set_device(self.idx)
+
+    def __exit__(self, *exc):
+        if self.prev is not None:
+            torch.cuda.set_device(self.prev)
+
+
+def k1_fwd(x_flat: torch.Tensor, W: torch.Tensor, out: torch.Tensor | None = None,
+           inv_rms: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """proj (T, 32) bf16 and inv_rms (T,) fp32 from x_flat (T, nC) bf16, W (32, nC) bf16."""
+    dev = _device_of(x_flat)
+    if x_flat.dim() != 2:
+        raise ValueError(f"x_flat must be 2-D (T, nC), got shape {tuple(x_flat.shape)}")
+    T, nC = x_flat.shape
+    _require(x_flat, "x_flat", _BF16, (T, nC), dev)
+    if W.dim() != 2 or W.shape[0] != D_OUT:
+        raise ValueError(f"W must have shape ({D_OUT}, nC); got {tuple(W.shape)}")
+    _require(W, "W", _BF16, (D_OUT, nC), dev)
+    if out is None:
+        out = torch.empty((T, D_OUT), device=dev, dtype=_BF16)
+    if inv_rms is None:
+        inv_rms = torch.empty((T,), device=dev, dtype=_F32)
+    _require(out, "out", _BF16, (T, D_OUT), dev)
+    _require(inv_rms, "inv_rms", _F32, (T,), dev)
+    lib = _abi.load()
+    with _OnDevice(dev):
+        st = lib.fmhc_k1_fwd(x_flat.data_ptr(), W.data_ptr(), out.data_ptr(), inv_rms.data_ptr(),
+                             T, nC, D_OUT, _abi.stream_of(x_flat))
+    _abi.check(st, "k1_fwd")
+    return out, inv_rms
+
+
+def k1_bwd_dx(grad_out: torch.Tensor, x_flat: torch.Tensor, W: torch.Tensor,
+              proj_out: torch.Tensor, inv_rms: torch.Tensor,
+              grad_x: torch.Tensor | None = None) -> torch.Tensor:
+    """grad of x_flat for K1, from the stored bf16 projection and inv_rms."""
+    dev = _device_of(x_flat)
+    if x_flat.dim() != 2:
+        raise ValueError(f"x_flat must be 2-D (T, nC), got shape {tuple(x_flat.shape)}")
+    T, nC = x_flat.shape
+    _require(x_flat, "x_flat", _BF16, (T, nC), dev)
+    _require(W, "W", _BF16, (D_OUT, nC), dev)
+    _require(grad_out, "grad_out", _BF16, (T, D_OUT), dev)
+    _require(proj_out, "proj_out", _BF16, (T, D_OUT), dev)
+    _require(inv_rms, "inv_rms", _F32, (T,), dev)
+    if grad_x is None:
+        grad_x = torch.empty_like(x_flat)
+    _require(grad_x, "grad_x", _BF16, (T, nC), dev)
+    lib = _abi.load()
+    with _OnDevice(dev):
+        st = lib.fmhc_k1_bwd_dx(x_flat.data_ptr(), W.data_ptr(), grad_out.data_ptr(),
+                                proj_out.data_ptr(), inv_rms.data_ptr(), grad_x.data_ptr(),
+                                T, nC, D_OUT, _abi.stream_of(x_flat))
+    _abi.check(st, "k1_bwd_dx")
+    return grad_x
+
+
+def _streams_shape(x: torch.Tensor) -> tuple[int, int, int]:
+    if x.dim() != 3:
+        raise ValueError(f"x_streams must be 3-D (T, n, C), got shape {tuple(x.shape)}")
+    T, n, C = x.shape
+    if n != N_STREAMS:
+        raise ValueError(f"flash_mhc HIP kernels support n={N_STREAMS} only, got n={n}")
+    return T, n, C
+
+
+def k3_fwd(x_streams: torch.Tensor, h_pre: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """layer_input (T, C) bf16 = sum_j h_pre[:, j] * x_streams[:, j, :]."""
+    dev = _device_of(x_streams)
+    T, n, C = _streams_shape(x_streams)
+    _require(x_streams, "x_streams", _BF16, (T, n, C), dev)
+    _require(h_pre, "h_pre", _F32, (T, n), dev)
+    if out is None:
+        out = torch.empty((T, C), device=dev, dtype=_BF16)
+    _require(out, "out", _BF16, (T, C), dev)
+    lib = _abi.load()
+    with _OnDevice(dev):
+        st = lib.fmhc_k3_fwd(x_streams.data_ptr(), h_pre.data_ptr(), out.data_ptr(), T, C, n,
+                             _abi.stream_of(x_streams))
+    _abi.check(st, "k3_fwd")
+    return out
+
+
+def k3_bwd(grad_out: torch.Tensor, x_streams: torch.Tensor, h_pre: torch.Tensor,
+           grad_x: torch.Tensor | None = None,
+           grad_h_pre: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """(grad_x (T, n, C) bf16, grad_h_pre (T, n) fp32) of K3."""
+    dev = _device_of(x_streams)
+    T, n, C = _streams_shape(x_streams)
+    _require(x_streams, "x_streams", _BF16, (T, n, C), dev)
+    _require(h_pre, "h_pre", _F32, (T, n), dev)
+    _require(grad_out, "grad_out", _BF16, (T, C), dev)
+    if grad_x is None:
+        grad_x = torch.empty_like(x_streams)
+    if grad_h_pre is None:
+        grad_h_pre = torch.empty((T, n), device=dev, dtype=_F32)
+    _require(grad_x, "grad_x", _BF16, (T, n, C), dev)
+    _require(grad_h_pre, "grad_h_pre", _F32, (T, n), dev)
+    lib = _abi.load()
+    with _OnDevice(dev):
+        st = lib.fmhc_k3_bwd(x_streams.data_ptr(), h_pre.data_ptr(), grad_out.data_ptr(),
+                             grad_x.data_ptr(), grad_h_pre.data_ptr(), T, C, n,
+                             _abi.stream_of(x_streams))
+    _abi.check(st, "k3_bwd")
+    return grad_x, grad_h_pre
+
+
+def k4_fwd(x_streams: torch.Tensor, layer_output: torch.Tensor, H_merged: torch.Tensor,
+           h_post: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """out (T, n, C) bf16 = H_merged @ x_streams + h_post (x) layer_output."""
+    dev = _device_of(x_streams)
+    T, n, C = _streams_shape(x_streams)
+    _require(x_streams, "x_streams", _BF16, (T, n, C), dev)
+    _require(layer_output, "layer_output", _BF16, (T, C), dev)
+    _require(H_merged, "H_merged", _F32, (T, n, n), dev)
+    _require(h_post, "h_post", _F32, (T, n), dev)
+    if out is None:
+        out = torch.empty_like(x_streams)
+    _require(out, "out", _BF16, (T, n, C), dev)
+    lib = _abi.load()
+    with _OnDevice(dev):
+        st = lib.fmhc_k4_fwd(x_streams.data_ptr(), layer_output.data_ptr(), H_merged.data_ptr(),
+                             h_post.data_ptr(), out.data_ptr(), T, C, n, _abi.stream_of(x_streams))
+    _abi.check(st, "k4_fwd")
+    return out
+
+
+def k4_bwd(grad_out: torch.Tensor, x_streams: torch.Tensor, layer_output: torch.Tensor,
+           H_merged: torch.Tensor, h_post: torch.Tensor,
+           grad_x: torch.Tensor | None = None, grad_layer_output: torch.Tensor | None = None,
+           grad_H: torch.Tensor | None = None, grad_h_post: torch.Tensor | None = None):
+    """(grad_x, grad_layer_output, grad_H_merged, grad_h_post) of K4."""
+    dev = _device_of(x_streams)
+    T, n, C = _streams_shape(x_streams)
+    _require(x_streams, "x_streams", _BF16, (T, n, C), dev)
+    _require(layer_output, "layer_output", _BF16, (T, C), dev)
+    _require(H_merged, "H_merged", _F32, (T, n, n), dev)
+    _require(h_post, "h_post", _F32, (T, n), dev)
+    _require(grad_out, "grad_out", _BF16, (T, n, C), dev)
+    if grad_x is None:
+        grad_x = torch.empty_like(x_streams)
+    if grad_layer_output is None:
+        grad_layer_output = torch.empty((T, C), device=dev, dtype=_BF16)
+    if grad_H is None:
+        grad_H = torch.empty((T, n, n), device=dev, dtype=_F32)
+    if grad_h_post is None:
+        grad_h_post = torch.empty((T, n), device=dev, dtype=_F32)
+    _require(grad_x, "grad_x", _BF16, (T, n, C), dev)
+    _require(grad_layer_output, "grad_layer_output", _BF16, (T, C), dev)
+    _require(grad_H, "grad_H", _F32, (T, n, n), dev)
+    _require(grad_h_post, "grad_h_post", _F32, (T, n), dev)
+    lib = _abi.load()
+    with _OnDevice(dev):
+        st = lib.fmhc_k4_bwd(x_streams.data_ptr(), layer_output.data_ptr(), H_merged.data_ptr(),
+                             h_post.data_ptr(), grad_out.data_ptr(), grad_x.data_ptr(),
+                             grad_layer_output.data_ptr(), grad_H.data_ptr(), grad_h_post.data_ptr(),
+                             T, C, n, _abi.stream_of(x_streams))
+    _abi.check(st, "k4_bwd")
+    return grad_x, grad_layer_output, grad_H, grad_h_post

@@ -1,0 +1,225 @@
+"""torch.library custom ops for the mHC-lite fused path, backed by gfx950 HIP.
+
+The op namespace, names, schemas, FakeTensor behaviour and autograd formulas
+are those of the reference (alint77/flash-mHC ``src/flash_mhc/ops.py``), so
+``torch.ops.flash_mhc.*`` callers and ``torch.compile`` (which sees the ops as
+opaque through their fakes) work unchanged.  Only the device implementation
+differs: each "CUDA"-key impl validates its inputs and launches one HIP kernel
+through the C ABI (:mod:`flash_mhc.kernels`).  There is no other backend: on a
+tensor that is not on a GPU, or without the built extension, the ops raise.
+
+Reference map:
+  schemas                              ops.py:22-41
+  fakes                                ops.py:145-202
+  device impls                         ops.py:205-667
+  autograd (setup_context + backward)  ops.py:670-714
+  disable_autotune_temporarily         ops.py:44-58
+"""
+
+from __future__ import annotations
+
+import threading
+from contextlib import contextmanager
+
+import torch
+import torch.library
+
+from . import kernels as _k
+
+_lib = torch.library.Library("flash_mhc", "DEF")
+
+_lib.define(
+    "fused_rmsnorm_project(Tensor x_flat, Tensor W) -> (Tensor out, Tensor inv_rms)"
+)
+_lib.define(
+    "fused_rmsnorm_project_bwd_dx(Tensor grad_out, Tensor x_flat, Tensor W, Tensor proj_out, Tensor inv_rms) -> Tensor grad_x"
+)
+
+_lib.define("fused_pre_map(Tensor x_streams, Tensor h_pre) -> Tensor out")
+_lib.define(
+    "fused_pre_map_backward(Tensor grad_out, Tensor x_streams, Tensor h_pre) -> (Tensor grad_x, Tensor grad_h_pre)"
+)
+
+_lib.define(
+    "fused_post_res(Tensor x_streams, Tensor layer_output, Tensor H_merged, Tensor h_post) -> Tensor out"
+)
+_lib.define(
+    "fused_post_res_backward(Tensor grad_out, Tensor x_streams, Tensor layer_output, Tensor H_merged, Tensor h_post) -> (Tensor grad_x, Tensor grad_layer_output, Tensor grad_H_merged, Tensor grad_h_post)"
+)
+
+
+# ---------------------------------------------------------------------------
+# Launch-configuration control.  The reference switches between Triton
+# autotuning and fixed launch parameters (ops.py:44-63); the HIP kernels have
+# one fixed gfx950 configuration per shape class, so the context manager only
+# tracks its nesting depth (MHCLiteBlock enters it in eval mode).
+
+_AUTOTUNE_CONTROL = threading.local()
+
+
+def _autotune_disable_depth() -> int:
+    return int(getattr(_AUTOTUNE_CONTROL, "disable_depth", 0))
+
+
+@contextmanager
+def disable_autotune_temporarily():
+    """Kept for API compatibility; launch configurations are fixed."""
+    _AUTOTUNE_CONTROL.disable_depth = _autotune_disable_depth() + 1
+    try:
+        yield
+    finally:
+        _AUTOTUNE_CONTROL.disable_depth = max(0, _autotune_disable_depth() - 1)
+
+
+# ---------------------------------------------------------------------------
+# Fake (meta) implementations: output shapes/dtypes only (ops.py:145-202).
+
+@torch.library.register_fake("flash_mhc::fused_rmsnorm_project")
+def _fused_rmsnorm_project_fake(x_flat: torch.Tensor, W: torch.Tensor):
+    T = x_flat.shape[0]
+    D_out = W.shape[0]
+    out = torch.empty((T, D_out), device=x_flat.device, dtype=x_flat.dtype)
+    inv_rms = torch.empty((T,), device=x_flat.device, dtype=torch.float32)
+    return out, inv_rms
+
+
+@torch.library.register_fake("flash_mhc::fused_rmsnorm_project_bwd_dx")
+def _fused_rmsnorm_project_bwd_dx_fake(grad_out, x_flat, W, proj_out, inv_rms):
+    return torch.empty_like(x_flat)
+
+
+@torch.library.register_fake("flash_mhc::fused_pre_map")
+def _fused_pre_map_fake(x_streams: torch.Tensor, h_pre: torch.Tensor):
+    T, _, C = x_streams.shape
+    return torch.empty((T, C), device=x_streams.device, dtype=x_streams.dtype)
+
+
+@torch.library.register_fake("flash_mhc::fused_pre_map_backward")
+def _fused_pre_map_backward_fake(grad_out, x_streams, h_pre):
+    grad_x = torch.empty_like(x_streams)
+    grad_h_pre = torch.empty_like(h_pre, dtype=torch.float32)
+    return grad_x, grad_h_pre
+
+
+@torch.library.register_fake("flash_mhc::fused_post_res")
+def _fused_post_res_fake(x_streams, layer_output, H_merged, h_post):
+    return torch.empty_like(x_streams)
+
+
+@torch.library.register_fake("flash_mhc::fused_post_res_backward")
+def _fused_post_res_backward_fake(grad_out, x_streams, layer_output, H_merged, h_post):
+    grad_x = torch.empty_like(x_streams)
+    grad_layer_output = torch.empty_like(layer_output)
+    grad_H_merged = torch.empty_like(H_merged, dtype=torch.float32)
+    grad_h_post = torch.empty_like(h_post, dtype=torch.float32)
+    return grad_x, grad_layer_output, grad_H_merged, grad_h_post
+
+
+# ---------------------------------------------------------------------------
+# Device implementations (GPU tensors -> HIP kernels).
+
+
+def _check_n4(x_streams: torch.Tensor, message: str) -> None:
+    # Same errors as the reference (ops.py:352-353, 424-425, 506-507, 581-582).
+    if x_streams.dim() != 3:
+        raise ValueError(f"x_streams must have shape (T, n, C), got {tuple(x_streams.shape)}")
+    if x_streams.shape[1] != 4:
+        raise ValueError(message)
+
+
+def _coeff(t: torch.Tensor) -> torch.Tensor:
+    # The reference kernels upcast whatever coefficient dtype they receive.
+    return t.to(torch.float32).contiguous()
+
+
+@torch.library.impl(_lib, "fused_rmsnorm_project", "CUDA")
+def _fused_rmsnorm_project_cuda(x_flat: torch.Tensor, W: torch.Tensor):
+    return _k.k1_fwd(x_flat.contiguous(), W.contiguous())
+
+
+@torch.library.impl(_lib, "fused_rmsnorm_project_bwd_dx", "CUDA")
+def _fused_rmsnorm_project_bwd_dx_cuda(grad_out, x_flat, W, proj_out, inv_rms):
+    return _k.k1_bwd_dx(grad_out.contiguous(), x_flat.contiguous(), W.contiguous(),
+                        proj_out.contiguous(), inv_rms.contiguous())
+
+
+@torch.library.impl(_lib, "fused_pre_map", "CUDA")
+def _fused_pre_map_cuda(x_streams: torch.Tensor, h_pre: torch.Tensor):
+    _check_n4(x_streams, "flash_mhc::fused_pre_map currently supports n=4 only")
+    return _k.k3_fwd(x_streams.contiguous(), _coeff(h_pre))
+
+
+@torch.library.impl(_lib, "fused_pre_map_backward", "CUDA")
+def _fused_pre_map_backward_cuda(grad_out, x_streams, h_pre):
+    _check_n4(x_streams, "flash_mhc::fused_pre_map_backward supports n=4 only")
+    return _k.k3_bwd(grad_out.contiguous(), x_streams.contiguous(), _coeff(h_pre))
+
+
+@torch.library.impl(_lib, "fused_post_res", "CUDA")
+def _fused_post_res_cuda(x_streams, layer_output, H_merged, h_post):
+    _check_n4(x_streams, "flash_mhc::fused_post_res currently supports n=4 only")
+    return _k.k4_fwd(x_streams.contiguous(), layer_output.contiguous(), _coeff(H_merged),
+                     _coeff(h_post))
+
+
+@torch.library.impl(_lib, "fused_post_res_backward", "CUDA")
+def _fused_post_res_backward_cuda(grad_out, x_streams, layer_output, H_merged, h_post):
+    _check_n4(x_streams, "flash_mhc::fused_post_res_backward supports n=4 only")
+    return _k.k4_bwd(grad_out.contiguous(), x_streams.contiguous(), layer_output.contiguous(),
+                     _coeff(H_merged), _coeff(h_post))
+
+
+# ---------------------------------------------------------------------------
+# Autograd (ops.py:670-714).  The formulas are the reference's; each op saves
+# only the tensors its backward reads (the reference also saves the K3/K4
+# outputs, which its backward never uses).
+
+
+def _setup_k1(ctx, inputs, output):
+    x_flat, W = inputs
+    out, inv_rms = output
+    ctx.save_for_backward(x_flat, W, out, inv_rms)
+
+
+def _fused_rmsnorm_project_backward(ctx, grad_out, grad_inv_rms):
+    # inv_rms is treated as non-differentiable, as in the reference.
+    x_flat, W, proj_out, inv_rms = ctx.saved_tensors
+    grad_x = torch.ops.flash_mhc.fused_rmsnorm_project_bwd_dx(
+        grad_out, x_flat, W, proj_out, inv_rms
+    )
+    grad_out_scaled = (grad_out * inv_rms[:, None]).to(x_flat.dtype)
+    grad_W = torch.matmul(grad_out_scaled.transpose(0, 1).contiguous(), x_flat)
+    return grad_x, grad_W
+
+
+def _setup_inputs(ctx, inputs, output):
+    ctx.save_for_backward(*inputs)
+
+
+def _fused_pre_map_backward(ctx, grad_out):
+    x_streams, h_pre = ctx.saved_tensors
+    return torch.ops.flash_mhc.fused_pre_map_backward(grad_out, x_streams, h_pre)
+
+
+def _fused_post_res_backward(ctx, grad_out):
+    x_streams, layer_output, H_merged, h_post = ctx.saved_tensors
+    return torch.ops.flash_mhc.fused_post_res_backward(
+        grad_out, x_streams, layer_output, H_merged, h_post
+    )
+
+
+torch.library.register_autograd(
+    "flash_mhc::fused_rmsnorm_project",
+    _fused_rmsnorm_project_backward,
+    setup_context=_setup_k1,
+)
+torch.library.register_autograd(
+    "flash_mhc::fused_pre_map",
+    _fused_pre_map_backward,
+    setup_context=_setup_inputs,
+)
+torch.library.register_autograd(
+    "flash_mhc::fused_post_res",
+    _fused_post_res_backward,
+    setup_context=_setup_inputs,
+)

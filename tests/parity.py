@@ -1,0 +1,87 @@
+"""Parity tolerances for the bf16 / fp32 outputs of the HIP kernels.
+
+Every check compares a device result ``o`` with the oracle value ``R``
+computed in float64 from the *same* bf16/fp32 inputs, and with
+``S = sum |terms|`` of the same formula.
+
+bf16 outputs (the north-star rule: equal to the fp32 value rounded to bf16
+within 1 bf16 ulp):
+    |o - R| <= ulp_bf16(R) + 4 * sqrt(n) * 2^-24 * S
+The second term is the probabilistic bound of an n-term fp32 sum in any
+order (Higham's sqrt(n) rule with a 4-sigma margin).  It only matters where
+the terms cancel (|R| << S), i.e. where "1 ulp of the fp32 reference" is
+itself ill-defined.
+
+fp32 outputs (reductions): |o - R| <= 4 * sqrt(n) * 2^-24 * S + 2^-23 * |R|.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+U32 = 2.0 ** -24
+
+
+def bf16_ulp(R: torch.Tensor) -> torch.Tensor:
+    """Spacing of bf16 numbers at |R| (normal range; 2^-133 below it)."""
+    _, e = torch.frexp(R.abs().clamp_min(2.0 ** -126))
+    return torch.ldexp(torch.ones_like(R), (e - 8).to(torch.int32))
+
+
+def _stats(err: torch.Tensor, tol: torch.Tensor) -> str:
+    ratio = err / tol
+    idx = int(torch.argmax(ratio))
+    return (f"max err {float(err.max()):.3e}, worst err/tol {float(ratio.flatten()[idx]):.3f} "
+            f"at flat index {idx}")
+
+
+def check_bf16(name: str, out: torch.Tensor, R: torch.Tensor, S: torch.Tensor, n_terms: int) -> dict:
+    o = out.detach().to("cpu", torch.float64)
+    assert o.shape == R.shape, f"{name}: shape {tuple(o.shape)} != {tuple(R.shape)}"
+    assert out.dtype == torch.bfloat16, f"{name}: dtype {out.dtype}"
+    err = (o - R).abs()
+    tol = bf16_ulp(R) + 4.0 * math.sqrt(n_terms) * U32 * S
+    bad = ~(err <= tol)  # also catches NaN
+    assert not bool(bad.any()), f"{name}: {int(bad.sum())} of {err.numel()} elements out of tolerance; {_stats(err, tol)}"
+    exact = (o == R.to(torch.bfloat16).double()).double().mean().item()
+    return {"max_err": float(err.max()) if err.numel() else 0.0, "frac_equal_rn": exact}
+
+
+def check_fp32(name: str, out: torch.Tensor, R: torch.Tensor, S: torch.Tensor, n_terms: int) -> dict:
+    o = out.detach().to("cpu", torch.float64)
+    assert o.shape == R.shape, f"{name}: shape {tuple(o.shape)} != {tuple(R.shape)}"
+    assert out.dtype == torch.float32, f"{name}: dtype {out.dtype}"
+    err = (o - R).abs()
+    tol = 4.0 * math.sqrt(n_terms) * U32 * S + 2.0 * U32 * R.abs() + 1e-30
+    bad = ~(err <= tol)
+    assert not bool(bad.any()), f"{name}: {int(bad.sum())} of {err.numel()} elements out of tolerance; {_stats(err, tol)}"
+    return {"max_err": float(err.max()) if err.numel() else 0.0}
+
+
+def check_rel(name: str, out: torch.Tensor, R: torch.Tensor, rtol: float) -> None:
+    """|o - R| <= rtol * |R| elementwise (positive quantities such as inv_rms)."""
+    o = out.detach().to("cpu", torch.float64)
+    err = (o - R).abs()
+    tol = rtol * R.abs()
+    bad = ~(err <= tol)
+    assert not bool(bad.any()), f"{name}: {int(bad.sum())} elements out of tolerance; {_stats(err, tol)}"
+
+
+def block_close(name: str, out: torch.Tensor, ref: torch.Tensor, rtol: float = 2e-2, floor: float = 2e-2) -> dict:
+    """Block-level check of a bf16 pipeline against an fp32/fp64 reference:
+    |o - ref| <= rtol * |ref| + floor * rms(ref) elementwise.  The bf16 fused
+    path rounds the K2 coefficients to bf16 (block.py:163-169 of the
+    reference), so a relative bound with an absolute floor is the meaningful
+    rule there; the per-kernel checks above are the tight ones."""
+    o = out.detach().to("cpu", torch.float64)
+    r = ref.detach().to("cpu", torch.float64)
+    assert o.shape == r.shape, f"{name}: shape {tuple(o.shape)} != {tuple(r.shape)}"
+    rms = float(r.pow(2).mean().sqrt()) if r.numel() else 0.0
+    err = (o - r).abs()
+    tol = rtol * r.abs() + floor * rms + 1e-30
+    bad = ~(err <= tol)
+    assert not bool(bad.any()), f"{name}: {int(bad.sum())} of {err.numel()} out of tolerance; {_stats(err, tol)}; rms(ref)={rms:.3e}"
+    rel = float(err.norm() / max(r.norm(), 1e-30))
+    return {"rel_l2": rel}
