@@ -63,6 +63,11 @@ class MHCLiteBlock(nn.Module):
             name is the reference's; here the fused path is HIP, not Triton).
         activation_checkpointing: recompute the pre-map and post-res regions
             in backward instead of keeping their activations.
+        rmsnorm_weight: give the RMSNorm over the n*C stream a learnable
+            per-channel weight ``rms_weight`` (initialised to ones).  Off by
+            default, which is the reference's block (no RMSNorm weight) with
+            an identical state_dict.  The fused path folds it into the
+            projection: rmsnorm(x) * g @ W^T == rmsnorm(x) @ (W * g)^T.
     """
 
     def __init__(
@@ -72,6 +77,7 @@ class MHCLiteBlock(nn.Module):
         layer: nn.Module,
         triton_fused: bool = True,
         activation_checkpointing: bool = False,
+        rmsnorm_weight: bool = False,
     ) -> None:
         super().__init__()
         self.n = n_streams
@@ -91,6 +97,11 @@ class MHCLiteBlock(nn.Module):
 
         perm_flat, self.identity_idx = build_permutation_matrices(n_streams)
         self.register_buffer("perm_mat", perm_flat)
+
+        if rmsnorm_weight:
+            self.rms_weight = nn.Parameter(torch.ones(self.nC))
+        else:
+            self.rms_weight = None
 
     # -- shared pieces ------------------------------------------------------
 
@@ -125,7 +136,8 @@ class MHCLiteBlock(nn.Module):
     def _mhc_coeffs_pytorch(self, x_streams: torch.Tensor):
         dt = x_streams.dtype
         x_flat = x_streams.reshape(*x_streams.shape[:-2], self.nC)
-        x_norm = F.rms_norm(x_flat, (self.nC,))
+        g = None if self.rms_weight is None else self.rms_weight.to(dt)
+        x_norm = F.rms_norm(x_flat, (self.nC,), weight=g)
         proj = F.linear(x_norm, self.W_all.weight.to(dt), None)
         return self._coefficients(proj, dt)
 
@@ -150,8 +162,12 @@ class MHCLiteBlock(nn.Module):
     def _mhc_coeffs_triton(self, x_streams: torch.Tensor):
         dt = x_streams.dtype
         T = x_streams.shape[0]
+        if self.rms_weight is None:
+            W = self.W_all.weight.to(dt)
+        else:
+            W = (self.W_all.weight.float() * self.rms_weight.float()).to(dt)
         proj, _inv_rms = torch.ops.flash_mhc.fused_rmsnorm_project(
-            x_streams.reshape(T, self.nC), self.W_all.weight.to(dt)
+            x_streams.reshape(T, self.nC), W
         )
         return self._coefficients(proj, dt)
 

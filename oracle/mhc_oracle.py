@@ -181,34 +181,53 @@ def k4_torch(x_streams, layer_output, H_merged, h_post):
 # K2 coefficient math and the whole block (block.py:82-148, :150-177)
 
 
-def coefficients(proj, bias, alpha_pre, alpha_post, alpha_res, perm, n: int):
-    """(h_pre, h_post, H_merged) from the (.., 2n+n!) projection, in proj's dtype."""
+def coefficients(proj, bias, alpha_pre, alpha_post, alpha_res, perm, n: int, taps: dict | None = None):
+    """(h_pre, h_post, H_merged, H_res) from the (.., 2n+n!) projection, in proj's dtype.
+
+    If ``taps`` is a dict, the logits z = alpha * proj_part + bias and the
+    projection parts are stored in it (tests use them to bound the rounding
+    error of the alpha gradients, which are sums over all tokens)."""
     dt = proj.dtype
     nf = math.factorial(n)
     pre, post, res = proj[..., :n], proj[..., n : 2 * n], proj[..., 2 * n : 2 * n + nf]
     b = bias.to(dt)
-    h_pre = torch.sigmoid(alpha_pre.to(dt) * pre + b[:n])
-    h_post = 2.0 * torch.sigmoid(alpha_post.to(dt) * post + b[n : 2 * n])
-    a_res = torch.softmax(alpha_res.to(dt) * res + b[2 * n :], dim=-1)
+    z_pre = alpha_pre.to(dt) * pre + b[:n]
+    z_post = alpha_post.to(dt) * post + b[n : 2 * n]
+    z_res = alpha_res.to(dt) * res + b[2 * n :]
+    if taps is not None:
+        for name, z, part in (("pre", z_pre, pre), ("post", z_post, post), ("res", z_res, res)):
+            if z.requires_grad:
+                z.retain_grad()
+            taps["z_" + name] = z
+            taps["p_" + name] = part
+    h_pre = torch.sigmoid(z_pre)
+    h_post = 2.0 * torch.sigmoid(z_post)
+    a_res = torch.softmax(z_res, dim=-1)
+    if taps is not None:
+        if a_res.requires_grad:
+            a_res.retain_grad()
+        taps["a_res"] = a_res
     H_res = (a_res @ perm.to(dt)).reshape(*a_res.shape[:-1], n, n)
     H_merged = H_res - h_post[..., :, None] * h_pre[..., None, :]
     return h_pre, h_post, H_merged, H_res
 
 
-def block_forward(x_streams, params: dict, layer, n: int):
+def block_forward(x_streams, params: dict, layer, n: int, taps: dict | None = None):
     """The block's plain-PyTorch formulation (block.py:82-148).
 
-    params: W (2n+n!, nC), b, alpha_pre, alpha_post, alpha_res, perm."""
+    params: W (2n+n!, nC), b, alpha_pre, alpha_post, alpha_res, perm, and
+    optionally g (nC,), an RMSNorm weight (block option, absent in the reference)."""
     dt = x_streams.dtype
     nC = x_streams.shape[-1] * n
     x_flat = x_streams.reshape(*x_streams.shape[:-2], nC)
     # F.rms_norm with eps=None uses finfo(float32).eps for fp32 and bf16
     # (bf16 is upcast), and finfo(float64).eps for fp64.
-    x_norm = F.rms_norm(x_flat, (nC,))
+    g = params.get("g")
+    x_norm = F.rms_norm(x_flat, (nC,), weight=None if g is None else g.to(dt))
     proj = x_norm @ params["W"].to(dt).T
     h_pre, h_post, H_merged, _ = coefficients(
         proj, params["b"], params["alpha_pre"], params["alpha_post"], params["alpha_res"],
-        params["perm"], n,
+        params["perm"], n, taps,
     )
     layer_input = (h_pre.unsqueeze(-1) * x_streams).sum(dim=-2)
     layer_output = layer(layer_input)

@@ -1,0 +1,75 @@
+"""Test-only CPU kernels for the flash_mhc ops, computed by the oracle.
+
+The product registers device ("CUDA"-key) implementations only.  To test the
+op *contract* without a GPU (schemas, fakes, autograd registration,
+torch.library.opcheck, torch.compile tracing), these helpers temporarily
+register CPU kernels that evaluate the oracle's float64 formulas and round
+once to the op's output dtype.  The registration lives in a context manager
+and is removed on exit; GPU tensors never dispatch to it.
+"""
+
+from __future__ import annotations
+
+from contextlib import contextmanager
+
+import torch
+
+from oracle import mhc_oracle as O
+
+BF16 = torch.bfloat16
+
+
+def _k1(x_flat, W):
+    R, _, inv = O.k1_fwd(x_flat, W)
+    return R.to(x_flat.dtype), inv.to(torch.float32)
+
+
+def _k1_bwd_dx(grad_out, x_flat, W, proj_out, inv_rms):
+    R, _ = O.k1_bwd_dx(grad_out, x_flat, W, proj_out, inv_rms)
+    return R.to(x_flat.dtype)
+
+
+def _k3(x, h):
+    if x.shape[1] != 4:
+        raise ValueError("flash_mhc::fused_pre_map currently supports n=4 only")
+    R, _ = O.k3_fwd(x, h)
+    return R.to(x.dtype)
+
+
+def _k3_bwd(go, x, h):
+    gx, _, gh, _ = O.k3_bwd(go, x, h)
+    return gx.to(x.dtype), gh.to(torch.float32)
+
+
+def _k4(x, lo, H, hp):
+    R, _ = O.k4_fwd(x, lo, H, hp)
+    return R.to(x.dtype)
+
+
+def _k4_bwd(go, x, lo, H, hp):
+    r = O.k4_bwd(go, x, lo, H, hp)
+    return (r["grad_x"][0].to(x.dtype), r["grad_lo"][0].to(lo.dtype),
+            r["grad_H"][0].to(torch.float32), r["grad_hp"][0].to(torch.float32))
+
+
+IMPLS = {
+    "fused_rmsnorm_project": _k1,
+    "fused_rmsnorm_project_bwd_dx": _k1_bwd_dx,
+    "fused_pre_map": _k3,
+    "fused_pre_map_backward": _k3_bwd,
+    "fused_post_res": _k4,
+    "fused_post_res_backward": _k4_bwd,
+}
+
+
+@contextmanager
+def oracle_cpu_kernels():
+    import flash_mhc  # noqa: F401  # the op schemas must exist first
+
+    lib = torch.library.Library("flash_mhc", "IMPL")
+    try:
+        for name, fn in IMPLS.items():
+            lib.impl(name, fn, "CPU")
+        yield
+    finally:
+        lib._destroy()

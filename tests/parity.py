@@ -69,19 +69,26 @@ def check_rel(name: str, out: torch.Tensor, R: torch.Tensor, rtol: float) -> Non
     assert not bool(bad.any()), f"{name}: {int(bad.sum())} elements out of tolerance; {_stats(err, tol)}"
 
 
-def block_close(name: str, out: torch.Tensor, ref: torch.Tensor, rtol: float = 2e-2, floor: float = 2e-2) -> dict:
-    """Block-level check of a bf16 pipeline against an fp32/fp64 reference:
-    |o - ref| <= rtol * |ref| + floor * rms(ref) elementwise.  The bf16 fused
-    path rounds the K2 coefficients to bf16 (block.py:163-169 of the
-    reference), so a relative bound with an absolute floor is the meaningful
-    rule there; the per-kernel checks above are the tight ones."""
+def block_close(name: str, out: torch.Tensor, ref: torch.Tensor, rtol: float = 2e-2, atol: float = 5e-2) -> dict:
+    """Block-level check of the bf16 fused pipeline against an fp32 reference:
+        |o - ref| <= rtol * |ref| + atol * rms_t(ref)
+    elementwise, where rms_t is the RMS of the reference over token t (dim 0).
+    rtol/atol default to the reference's own end-to-end forward tolerances
+    (tests/test_correctness.py:284; 5e-2 / 1e-1 for gradients, :296, :317),
+    with the absolute term scaled by each token's magnitude so that tokens
+    scaled x100 are held to the same relative standard.  The bf16 pipeline
+    rounds the K2 coefficients to bf16 by design (block.py:163-169 of the
+    reference); the per-kernel checks above are the tight ones."""
     o = out.detach().to("cpu", torch.float64)
     r = ref.detach().to("cpu", torch.float64)
     assert o.shape == r.shape, f"{name}: shape {tuple(o.shape)} != {tuple(r.shape)}"
-    rms = float(r.pow(2).mean().sqrt()) if r.numel() else 0.0
+    if r.dim() >= 2:
+        rms_t = r.reshape(r.shape[0], -1).pow(2).mean(dim=1).sqrt().reshape(-1, *([1] * (r.dim() - 1)))
+    else:
+        rms_t = r.pow(2).mean().sqrt()
     err = (o - r).abs()
-    tol = rtol * r.abs() + floor * rms + 1e-30
+    tol = rtol * r.abs() + atol * rms_t + 1e-30
     bad = ~(err <= tol)
-    assert not bool(bad.any()), f"{name}: {int(bad.sum())} of {err.numel()} out of tolerance; {_stats(err, tol)}; rms(ref)={rms:.3e}"
-    rel = float(err.norm() / max(r.norm(), 1e-30))
-    return {"rel_l2": rel}
+    assert not bool(bad.any()), f"{name}: {int(bad.sum())} of {err.numel()} out of tolerance; {_stats(err, tol)}"
+    rel = float(err.norm() / max(float(r.norm()), 1e-30))
+    return {"rel_l2": rel, "max_err_over_tol": float((err / tol).max()) if err.numel() else 0.0}

@@ -1,0 +1,214 @@
+"""CPU tests of the flash_mhc op boundary (torch.library contract).
+
+The schema strings, fake-tensor shapes and autograd behaviour must be the
+reference's (src/flash_mhc/ops.py:22-41, :145-202, :670-714).  Device work is
+replaced here by the oracle's CPU kernels (tests/oracle_cpu_ops.py) so the
+contract is exercised without a GPU; GPU parity is in test_gpu_*.py.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+from torch._subclasses.fake_tensor import FakeTensorMode
+
+import flash_mhc
+from flash_mhc import kernels as K
+from flash_mhc import ops
+from oracle import mhc_oracle as O
+from oracle_cpu_ops import oracle_cpu_kernels
+
+BF16 = torch.bfloat16
+
+# Verbatim from the reference (ops.py:24-41).
+REFERENCE_SCHEMAS = {
+    "fused_rmsnorm_project": "fused_rmsnorm_project(Tensor x_flat, Tensor W) -> (Tensor out, Tensor inv_rms)",
+    "fused_rmsnorm_project_bwd_dx": "fused_rmsnorm_project_bwd_dx(Tensor grad_out, Tensor x_flat, Tensor W, Tensor proj_out, Tensor inv_rms) -> Tensor grad_x",
+    "fused_pre_map": "fused_pre_map(Tensor x_streams, Tensor h_pre) -> Tensor out",
+    "fused_pre_map_backward": "fused_pre_map_backward(Tensor grad_out, Tensor x_streams, Tensor h_pre) -> (Tensor grad_x, Tensor grad_h_pre)",
+    "fused_post_res": "fused_post_res(Tensor x_streams, Tensor layer_output, Tensor H_merged, Tensor h_post) -> Tensor out",
+    "fused_post_res_backward": "fused_post_res_backward(Tensor grad_out, Tensor x_streams, Tensor layer_output, Tensor H_merged, Tensor h_post) -> (Tensor grad_x, Tensor grad_layer_output, Tensor grad_H_merged, Tensor grad_h_post)",
+}
+
+
+def rnd(shape, seed, scale=1.0, dtype=BF16):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * scale).to(dtype)
+
+
+@pytest.mark.parametrize("name", sorted(REFERENCE_SCHEMAS))
+def test_schema_matches_reference(name):
+    op = getattr(torch.ops.flash_mhc, name).default
+    assert str(op._schema) == "flash_mhc::" + REFERENCE_SCHEMAS[name]
+
+
+def test_only_device_kernels_registered():
+    """No CPU implementation ships: the device path cannot silently fall back."""
+    for name in REFERENCE_SCHEMAS:
+        qual = f"flash_mhc::{name}"
+        assert torch._C._dispatch_has_kernel_for_dispatch_key(qual, "CUDA")
+        assert not torch._C._dispatch_has_kernel_for_dispatch_key(qual, "CPU")
+    with pytest.raises(NotImplementedError):
+        torch.ops.flash_mhc.fused_pre_map(rnd((2, 4, 8), 0), torch.zeros(2, 4))
+
+
+def test_fakes():
+    with FakeTensorMode():
+        T, C = 7, 24
+        x = torch.empty(T, 4, C, dtype=BF16)
+        xf = torch.empty(T, 4 * C, dtype=BF16)
+        W = torch.empty(32, 4 * C, dtype=BF16)
+        out, inv = torch.ops.flash_mhc.fused_rmsnorm_project(xf, W)
+        assert out.shape == (T, 32) and out.dtype == BF16 and inv.shape == (T,) and inv.dtype == torch.float32
+        gx = torch.ops.flash_mhc.fused_rmsnorm_project_bwd_dx(out, xf, W, out, inv)
+        assert gx.shape == xf.shape and gx.dtype == BF16
+        h = torch.empty(T, 4, dtype=BF16)
+        li = torch.ops.flash_mhc.fused_pre_map(x, h)
+        assert li.shape == (T, C) and li.dtype == BF16
+        gx, gh = torch.ops.flash_mhc.fused_pre_map_backward(li, x, h)
+        assert gx.shape == x.shape and gh.shape == (T, 4) and gh.dtype == torch.float32
+        lo = torch.empty(T, C, dtype=BF16)
+        H = torch.empty(T, 4, 4)
+        hp = torch.empty(T, 4)
+        o = torch.ops.flash_mhc.fused_post_res(x, lo, H, hp)
+        assert o.shape == x.shape and o.dtype == BF16
+        g = torch.ops.flash_mhc.fused_post_res_backward(o, x, lo, H, hp)
+        assert [t.shape for t in g] == [x.shape, lo.shape, H.shape, hp.shape]
+        assert [t.dtype for t in g] == [BF16, BF16, torch.float32, torch.float32]
+
+
+@pytest.mark.parametrize(
+    "fn,args,msg",
+    [
+        (ops._fused_pre_map_cuda, lambda: (rnd((2, 3, 8), 1), torch.zeros(2, 3)),
+         "flash_mhc::fused_pre_map currently supports n=4 only"),
+        (ops._fused_pre_map_backward_cuda, lambda: (rnd((2, 8), 1), rnd((2, 3, 8), 1), torch.zeros(2, 3)),
+         "flash_mhc::fused_pre_map_backward supports n=4 only"),
+        (ops._fused_post_res_cuda, lambda: (rnd((2, 5, 8), 1), rnd((2, 8), 1), torch.zeros(2, 5, 5), torch.zeros(2, 5)),
+         "flash_mhc::fused_post_res currently supports n=4 only"),
+        (ops._fused_post_res_backward_cuda,
+         lambda: (rnd((2, 5, 8), 1), rnd((2, 5, 8), 1), rnd((2, 8), 1), torch.zeros(2, 5, 5), torch.zeros(2, 5)),
+         "flash_mhc::fused_post_res_backward supports n=4 only"),
+    ],
+)
+def test_n_not_4_errors_match_reference(fn, args, msg):
+    with pytest.raises(ValueError, match=msg):
+        fn(*args())
+
+
+def test_launchers_reject_host_tensors_and_bad_args():
+    x = rnd((4, 4, 8), 2)
+    with pytest.raises(ValueError, match="GPU tensor"):
+        K.k3_fwd(x, torch.zeros(4, 4))
+    with pytest.raises(ValueError, match="GPU tensor"):
+        K.k1_fwd(x.view(4, 32), rnd((32, 32), 3))
+    with pytest.raises(TypeError):
+        K.k3_fwd("not a tensor", None)
+
+
+def test_disable_autotune_context_nests():
+    assert ops._autotune_disable_depth() == 0
+    with ops.disable_autotune_temporarily():
+        with ops.disable_autotune_temporarily():
+            assert ops._autotune_disable_depth() == 2
+        assert ops._autotune_disable_depth() == 1
+    assert ops._autotune_disable_depth() == 0
+
+
+# ---------------------------------------------------------------------------
+# With the oracle standing in for the device kernels
+
+
+@pytest.fixture
+def cpu_kernels():
+    with oracle_cpu_kernels():
+        yield
+
+
+def _samples():
+    T, C = 6, 16
+    x = rnd((T, 4, C), 10)
+    xf = x.reshape(T, 4 * C)
+    W = rnd((32, 4 * C), 11, 0.05)
+    h = torch.rand(T, 4, generator=torch.Generator().manual_seed(12))
+    lo = rnd((T, C), 13)
+    H = rnd((T, 4, 4), 14, dtype=torch.float32)
+    hp = rnd((T, 4), 15, dtype=torch.float32)
+    return T, C, x, xf, W, h, lo, H, hp
+
+
+def test_opcheck_all_ops(cpu_kernels):
+    T, C, x, xf, W, h, lo, H, hp = _samples()
+    proj, inv = torch.ops.flash_mhc.fused_rmsnorm_project(xf, W)
+    cases = [
+        (torch.ops.flash_mhc.fused_rmsnorm_project.default, (xf.clone().requires_grad_(True), W.clone().requires_grad_(True))),
+        (torch.ops.flash_mhc.fused_rmsnorm_project_bwd_dx.default, (rnd((T, 32), 16), xf, W, proj, inv)),
+        (torch.ops.flash_mhc.fused_pre_map.default, (x.clone().requires_grad_(True), h.clone().requires_grad_(True))),
+        (torch.ops.flash_mhc.fused_pre_map_backward.default, (rnd((T, C), 17), x, h)),
+        (torch.ops.flash_mhc.fused_post_res.default,
+         (x.clone().requires_grad_(True), lo.clone().requires_grad_(True), H.clone().requires_grad_(True), hp.clone().requires_grad_(True))),
+        (torch.ops.flash_mhc.fused_post_res_backward.default, (rnd((T, 4, C), 18), x, lo, H, hp)),
+    ]
+    for op, args in cases:
+        torch.library.opcheck(op, args)
+
+
+def test_autograd_formulas(cpu_kernels):
+    """Gradients through the ops equal the oracle's backward values."""
+    T, C, x, xf, W, h, lo, H, hp = _samples()
+    xs = x.clone().requires_grad_(True)
+    hs = h.clone().requires_grad_(True)
+    go3 = rnd((T, C), 20)
+    torch.ops.flash_mhc.fused_pre_map(xs, hs).backward(go3)
+    gx, _, gh, _ = O.k3_bwd(go3, x, h)
+    assert torch.equal(xs.grad, gx.to(BF16))
+    torch.testing.assert_close(hs.grad, gh.float())
+
+    xs = xf.clone().requires_grad_(True)
+    Ws = W.clone().requires_grad_(True)
+    proj, inv = torch.ops.flash_mhc.fused_rmsnorm_project(xs, Ws)
+    go1 = rnd((T, 32), 21)
+    proj.backward(go1)
+    gx, _ = O.k1_bwd_dx(go1, xf, W, proj.detach(), inv)
+    gW, _ = O.k1_grad_W(go1, xf, inv)
+    assert torch.equal(xs.grad, gx.to(BF16))
+    torch.testing.assert_close(Ws.grad.double(), gW, rtol=1e-2, atol=1e-2)
+
+
+def _block(seed=0, C=16):
+    torch.manual_seed(seed)
+    layer = torch.nn.Sequential(torch.nn.Linear(C, C, bias=False), torch.nn.GELU())
+    return flash_mhc.MHCLiteBlock(4, C, layer).to(BF16)
+
+
+def test_compile_fullgraph_fused_block(cpu_kernels):
+    """The fused block traces under torch.compile(fullgraph=True) with no graph
+    breaks, and compiled forward + backward equal eager."""
+    blk = _block()
+    x = rnd((8, 4, 16), 30)
+    xe = x.clone().requires_grad_(True)
+    out_e = blk._forward_triton(xe)
+    out_e.float().sum().backward()
+    ge = {n: p.grad.clone() for n, p in blk.named_parameters()}
+    blk.zero_grad()
+    compiled = torch.compile(blk._forward_triton, fullgraph=True, backend="aot_eager")
+    xc = x.clone().requires_grad_(True)
+    out_c = compiled(xc)
+    out_c.float().sum().backward()
+    assert torch.equal(out_c, out_e)
+    assert torch.equal(xc.grad, xe.grad)
+    for n, p in blk.named_parameters():
+        assert torch.equal(p.grad, ge[n]), n
+
+
+def test_fused_block_matches_plain_block_on_cpu(cpu_kernels):
+    """The fused composition (K1 project-then-normalise, K2 in bf16, K3, K4)
+    agrees with the block's plain formulation to bf16 accuracy."""
+    from parity import block_close
+
+    blk = _block(C=32)
+    x = rnd((64, 4, 32), 31)
+    with torch.no_grad():
+        a = blk._forward_triton(x)
+        b = blk.float()._forward_pytorch(x.float())
+    block_close("fused vs plain", a, b)
