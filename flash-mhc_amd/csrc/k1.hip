@@ -44,6 +44,12 @@ __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
 // squares also runs on the matrix cores: the same x registers are both A and
 // B of a third MFMA, G (16 x 16) += x x^T, whose diagonal is sum_k x[t,k]^2
 // in fp32 (the bf16 products are exact).
+template <int R>
+struct FwdFrag {
+  u32x4 wa[2], wb[2];  // W rows 0-15 / 16-31, two 32-wide k steps
+  u32x4 xv[2][R];      // x of the R token blocks, two k steps
+};
+
 template <int R, int SPLIT>
 __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __restrict__ x,
                                                              const uint16_t* __restrict__ W,
@@ -78,43 +84,75 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
     gram[r] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
+  // Full 64-wide chunks.  Wave w takes the chunks at positions w, w + SPLIT,
+  // ... of a per-workgroup rotation of the chunk order (rotating spreads the
+  // concurrent reads of all workgroups over the DRAM channels instead of every
+  // workgroup hitting the same column of its 8 KiB-strided rows), and
+  // double-buffers: the next chunk's fragments are loaded while the MFMAs of
+  // the current one run.  x uses ordinary loads here: each load instruction
+  // covers half of a 128-byte line and the other half follows one
+  // instruction later, which the nontemporal hint would evict in between.
   const int nfull = nC >> 6;
-  for (int c = wave; c < nfull; c += SPLIT) {
+  const int rot = nfull > 0 ? static_cast<int>(blockIdx.x % static_cast<unsigned>(nfull)) : 0;
+  FwdFrag<R> f0, f1;
+  auto chunk_at = [&](int p) { return p + rot < nfull ? p + rot : p + rot - nfull; };
+  auto load = [&](FwdFrag<R>& f, int p) {
+    const int k = chunk_at(p) * 64;
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      const int k = c * 64 + 32 * s;
-      const bf16x8 wa = as_bf16x8(*reinterpret_cast<const u32x4*>(w0 + k));
-      const bf16x8 wb = as_bf16x8(*reinterpret_cast<const u32x4*>(w1 + k));
+      f.wa[s] = *reinterpret_cast<const u32x4*>(w0 + k + 32 * s);
+      f.wb[s] = *reinterpret_cast<const u32x4*>(w1 + k + 32 * s);
+#pragma unroll
+      for (int r = 0; r < R; ++r) f.xv[s][r] = *reinterpret_cast<const u32x4*>(xrow[r] + k + 32 * s);
+    }
+  };
+  auto compute = [&](const FwdFrag<R>& f) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const bf16x8 xb = as_bf16x8(ld_stream(reinterpret_cast<const u32x4*>(xrow[r] + k)));
-        acc[0][r] = mfma16(wa, xb, acc[0][r]);
-        acc[1][r] = mfma16(wb, xb, acc[1][r]);
+        const bf16x8 xb = as_bf16x8(f.xv[s][r]);
+        acc[0][r] = mfma16(as_bf16x8(f.wa[s]), xb, acc[0][r]);
+        acc[1][r] = mfma16(as_bf16x8(f.wb[s]), xb, acc[1][r]);
         gram[r] = mfma16(xb, xb, gram[r]);
       }
     }
+  };
+  // n chunks for this wave, two per trip.  Both prefetches are issued on every
+  // path (a clamped index re-reads a cached chunk that is never computed), so
+  // the compiler keeps them ahead of the MFMAs; an odd count ends with f0.
+  const int n = nfull > wave ? (nfull - wave + SPLIT - 1) / SPLIT : 0;
+  auto pos = [&](int i) { return wave + SPLIT * (i < n ? i : n - 1); };
+  if (n > 0) {
+    load(f0, pos(0));
+    int i = 0;
+    for (; i + 1 < n; i += 2) {
+      load(f1, pos(i + 1));
+      __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the MFMAs
+      compute(f0);
+      load(f0, pos(i + 2));
+      __builtin_amdgcn_sched_barrier(0);
+      compute(f1);
+    }
+    if (i < n) compute(f0);
   }
   // Ragged last chunk (nC % 64 != 0): 16-byte pieces past nC contribute zero.
   if ((nC & 63) != 0 && wave == nfull % SPLIT) {
+    const int k = nfull * 64;
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      const int k = nfull * 64 + 32 * s;
-      const bool ok = k + 8 * grp < nC;
-      u32x4 wav = {0u, 0u, 0u, 0u}, wbv = {0u, 0u, 0u, 0u};
-      if (ok) {
-        wav = *reinterpret_cast<const u32x4*>(w0 + k);
-        wbv = *reinterpret_cast<const u32x4*>(w1 + k);
-      }
+      const bool ok = k + 32 * s + 8 * grp < nC;
+      f0.wa[s] = f0.wb[s] = u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        u32x4 xv = {0u, 0u, 0u, 0u};
-        if (ok) xv = ld_stream(reinterpret_cast<const u32x4*>(xrow[r] + k));
-        const bf16x8 xb = as_bf16x8(xv);
-        acc[0][r] = mfma16(as_bf16x8(wav), xb, acc[0][r]);
-        acc[1][r] = mfma16(as_bf16x8(wbv), xb, acc[1][r]);
-        gram[r] = mfma16(xb, xb, gram[r]);
+      for (int r = 0; r < R; ++r) f0.xv[s][r] = u32x4{0u, 0u, 0u, 0u};
+      if (ok) {
+        f0.wa[s] = *reinterpret_cast<const u32x4*>(w0 + k + 32 * s);
+        f0.wb[s] = *reinterpret_cast<const u32x4*>(w1 + k + 32 * s);
+#pragma unroll
+        for (int r = 0; r < R; ++r) f0.xv[s][r] = *reinterpret_cast<const u32x4*>(xrow[r] + k + 32 * s);
       }
     }
+    compute(f0);
   }
 
   // Diagonal G[row][row] sits in lane row + 16 * (row >> 2), register row & 3.
@@ -158,19 +196,26 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
 }
 
 // ---------------------------------------------------------------------------
-// K1 backward dx, matrix-core path (nC % 8 == 0, 16-byte aligned x / go /
-// proj_out / grad_x).
+// K1 backward dx, matrix-core path (nC % 8 == 0, 16-byte aligned x / W / go /
+// proj_out / inv_rms / grad_x).
 //
 // Each wave owns a 128-wide slice of the nC axis and walks NTB blocks of 16
-// tokens.  Per token block one MFMA per 16-row tile computes
-//   D (16 k x 16 tokens) = W^T[k tile, 0:32] (A) * go[tokens, 0:32]^T (B),
-// i.e. the whole D_out = 32 contraction in one instruction.  The eight A
-// tiles (W^T for the wave's 128 k) are loaded once per wave and stay in
-// registers.  Tile m's row i stands for
-//   k(m, i) = k_slice + 32 * (m >> 1) + 8 * (i >> 2) + 4 * (m & 1) + (i & 3)
-// which makes the two tiles 2u, 2u + 1 give each lane 8 consecutive k of its
-// token: x is read and grad_x written as one 16-byte vector per lane, and each
-// store instruction covers 64 contiguous bytes of 16 token rows.
+// tokens (strided by the number of runs, see below).  Per token block, eight MFMAs (tiles m = 0..7) compute
+//   D_m (16 tokens x 16 columns) = go[tokens, 0:32] (A) * W[0:32, cols_m] (B)
+// i.e. the whole D_out = 32 contraction in one instruction per tile, where
+// column j of tile m stands for k = k_slice + 8 * j + m.  With D's layout
+// (lane l, register q holds D[4 * (l >> 4) + q][l & 15]) every lane then owns
+// 8 consecutive k (tiles m = 0..7) of 4 tokens (q = 0..3): x is read and
+// grad_x written as one 16-byte vector per lane and token, and each memory
+// instruction covers 4 token rows x 256 contiguous bytes (whole cache lines).
+// The B tiles depend only on the slice, so each wave builds them once: eight
+// 16-byte loads of W rows and an 8 x 8 bf16 transpose in registers.
+struct BwdFrag {
+  u32x4 gv, pv;   // go / proj_out row of token tbase + col, d = 8 * grp .. + 8
+  float inv[4];   // inv_rms of tokens tbase + 4 * grp + q
+  u32x4 xv[4];    // x of those tokens, k = kl .. kl + 8
+};
+
 template <int NTB>
 __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ x,
                                                    const uint16_t* __restrict__ W,
@@ -181,83 +226,109 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
                                                    int64_t T, int nC, int nslices) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
-  const int row = lane & 15;
-  const int grp = lane >> 4;
+  const int col = lane & 15;  // A row (token) for the loads of go, B/D column
+  const int grp = lane >> 4;  // 8-wide d group of A/B; 4-token group of D
   const int64_t wid = static_cast<int64_t>(blockIdx.x) * 4 + wave;
   const int slice = static_cast<int>(wid % nslices);
   const int64_t run = wid / nslices;
-  const int64_t tb0 = run * NTB * 16;
-  if (tb0 >= T) return;
-  const int kw = slice * 128;
+  // Token blocks run, run + nruns, run + 2 * nruns, ...: the waves resident at
+  // one time work on neighbouring blocks, so the concurrent reads and writes
+  // cover contiguous memory instead of addresses a power-of-two apart.
+  const int64_t nblocks = (T + 15) / 16;
+  const int64_t nruns = (nblocks + NTB - 1) / NTB;
+  if (run >= nruns || run >= nblocks) return;
+  const int kl = slice * 128 + 8 * col;  // this lane's 8 consecutive k
+  const bool kok = kl < nC;              // nC % 8 == 0: all 8 valid or none
 
-  bf16x8 afr[8];
+  // B tiles: bfr[m] holds W[8 * grp + e][kl + m], e = 0..7.
+  bf16x8 bfr[8];
+  {
+    u32x4 rows[8];
 #pragma unroll
-  for (int m = 0; m < 8; ++m) {
-    const int k = kw + 32 * (m >> 1) + 8 * (row >> 2) + 4 * (m & 1) + (row & 3);
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if (k < nC) {
-      const uint16_t* wc = W + static_cast<int64_t>(8 * grp) * nC + k;
-      uint32_t e[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) e[i] = wc[static_cast<int64_t>(i) * nC];
-      v.x = e[0] | (e[1] << 16);
-      v.y = e[2] | (e[3] << 16);
-      v.z = e[4] | (e[5] << 16);
-      v.w = e[6] | (e[7] << 16);
+    for (int e = 0; e < 8; ++e) {
+      rows[e] = u32x4{0u, 0u, 0u, 0u};
+      if (kok) rows[e] = *reinterpret_cast<const u32x4*>(W + static_cast<int64_t>(8 * grp + e) * nC + kl);
     }
-    afr[m] = as_bf16x8(v);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      uint32_t h[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t w = rows[e][m >> 1];
+        h[e] = (m & 1) ? (w >> 16) : (w & 0xffffu);
+      }
+      const u32x4 v = {h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+      bfr[m] = as_bf16x8(v);
+    }
   }
 
-  for (int tb = 0; tb < NTB; ++tb) {
-    const int64_t tbase = tb0 + 16 * tb;
-    if (tbase >= T) break;
-    const int64_t t = tbase + row;
-    const int64_t tl = t < T ? t : T - 1;
-
-    const u32x4 gv = *reinterpret_cast<const u32x4*>(go + tl * kDout + 8 * grp);
-    const u32x4 pv = *reinterpret_cast<const u32x4*>(proj + tl * kDout + 8 * grp);
-    const float inv = inv_rms[tl];
-
-    u32x4 xv[4];
+  // Token blocks of this wave, two per trip with double-buffered fragments:
+  // the next block's go / proj_out / inv_rms / x are in flight while the
+  // current block computes (same structure as the forward kernel).
+  const int64_t left = (nblocks - run + nruns - 1) / nruns;
+  const int nb = static_cast<int>(left < NTB ? left : NTB);
+  auto pos = [&](int i) { return i < nb ? i : nb - 1; };
+  auto load = [&](BwdFrag& f, int tb) {
+    const int64_t tbase = (run + static_cast<int64_t>(tb) * nruns) * 16;
+    const int64_t ta = tbase + col < T ? tbase + col : T - 1;
+    f.gv = *reinterpret_cast<const u32x4*>(go + ta * kDout + 8 * grp);
+    f.pv = *reinterpret_cast<const u32x4*>(proj + ta * kDout + 8 * grp);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int k = kw + 32 * u + 8 * grp;
-      xv[u] = u32x4{0u, 0u, 0u, 0u};
-      if (k < nC) xv[u] = ld_stream(reinterpret_cast<const u32x4*>(x + tl * nC + k));
+    for (int q = 0; q < 4; ++q) {
+      const int64_t t = tbase + 4 * grp + q;
+      const int64_t tl = t < T ? t : T - 1;
+      f.inv[q] = inv_rms[tl];
+      f.xv[q] = u32x4{0u, 0u, 0u, 0u};
+      if (kok) f.xv[q] = ld_stream(reinterpret_cast<const u32x4*>(x + tl * nC + kl));
     }
-
+  };
+  auto compute = [&](const BwdFrag& f, int tb) {
+    const int64_t tbase = (run + static_cast<int64_t>(tb) * nruns) * 16;
+    // dot(go, proj_out) of token tbase + col, over the four 8-wide d groups.
     float gf[8], pf[8];
-    unpack8(gv, gf);
-    unpack8(pv, pf);
+    unpack8(f.gv, gf);
+    unpack8(f.pv, pf);
     float dot = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) dot = __builtin_fmaf(gf[e], pf[e], dot);
     dot += __shfl_xor(dot, 16, kWave);
     dot += __shfl_xor(dot, 32, kWave);
-    const float scale = dot * (inv * inv) / static_cast<float>(nC);
-
-    const bf16x8 b = as_bf16x8(gv);
+    float scale[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float d = __shfl(dot, 4 * grp + q, kWave);  // token tbase + 4 * grp + q
+      scale[q] = d * (f.inv[q] * f.inv[q]) / static_cast<float>(nC);
+    }
     f32x4 acc[8];
+    const bf16x8 a = as_bf16x8(f.gv);
 #pragma unroll
-    for (int m = 0; m < 8; ++m) acc[m] = mfma16(afr[m], b, f32x4{0.f, 0.f, 0.f, 0.f});
-
-    if (t < T) {
+    for (int m = 0; m < 8; ++m) acc[m] = mfma16(a, bfr[m], f32x4{0.f, 0.f, 0.f, 0.f});
+    if (kok) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int k = kw + 32 * u + 8 * grp;
-        if (k < nC) {
+      for (int q = 0; q < 4; ++q) {
+        const int64_t t = tbase + 4 * grp + q;
+        if (t < T) {
           float xf[8], o[8];
-          unpack8(xv[u], xf);
+          unpack8(f.xv[q], xf);
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            o[q] = inv * acc[2 * u][q] - scale * xf[q];
-            o[4 + q] = inv * acc[2 * u + 1][q] - scale * xf[4 + q];
-          }
-          st_stream(reinterpret_cast<u32x4*>(gx + t * nC + k), pack8(o));
+          for (int m = 0; m < 8; ++m) o[m] = f.inv[q] * acc[m][q] - scale[q] * xf[m];
+          st_stream(reinterpret_cast<u32x4*>(gx + t * nC + kl), pack8(o));
         }
       }
     }
+  };
+  BwdFrag f0, f1;
+  load(f0, 0);
+  int i = 0;
+  for (; i + 1 < nb; i += 2) {
+    load(f1, pos(i + 1));
+    __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the compute
+    compute(f0, i);
+    load(f0, pos(i + 2));
+    __builtin_amdgcn_sched_barrier(0);
+    compute(f1, i + 1);
   }
+  if (i < nb) compute(f0, i);
 }
 
 // ---------------------------------------------------------------------------
@@ -327,7 +398,7 @@ __global__ __launch_bounds__(256) void k1_bwd_scalar(const uint16_t* __restrict_
   }
 }
 
-constexpr int kFwdR = 4;      // token blocks of 16 per workgroup
+constexpr int kFwdR = 8;      // token blocks of 16 per workgroup
 constexpr int kFwdSplit = 4;  // waves per workgroup (split of the nC axis)
 constexpr int kBwdNTB = 16;   // token blocks of 16 per wave
 
@@ -366,8 +437,8 @@ extern "C" int fmhc_k1_bwd_dx(const uint16_t* x_flat, const uint16_t* W, const u
     return FMHC_ERR_INVALID_ARGUMENT;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int nc = static_cast<int>(nC);
-  if (nC % 8 == 0 && aligned16(x_flat) && aligned16(grad_out) && aligned16(proj_out) &&
-      aligned16(grad_x)) {
+  if (nC % 8 == 0 && aligned16(x_flat) && aligned16(W) && aligned16(grad_out) &&
+      aligned16(proj_out) && aligned16(grad_x)) {
     const int nslices = static_cast<int>((nC + 127) / 128);
     const int64_t nruns = (T + 16 * kBwdNTB - 1) / (16 * kBwdNTB);
     const dim3 grid(blocks_for(nruns * nslices, 4));
