@@ -87,14 +87,20 @@ __device__ __forceinline__ u32x4 pack8(const float f[8]) {
 
 // Element group moved by one lane per step: VEC = 8 (one 16-byte vector) or
 // VEC = 1 (one bf16 scalar).  `idx` counts groups, so the element offset is
-// idx * VEC.
+// idx * VEC.  raw() issues the load and keeps the packed bf16 bits; unpack()
+// widens them to fp32; load() does both.
 template <int VEC>
 struct Lanes;
 
 template <>
 struct Lanes<8> {
+  using Raw = u32x4;
+  __device__ static __forceinline__ Raw raw(const uint16_t* __restrict__ row, int idx) {
+    return ld_stream(reinterpret_cast<const u32x4*>(row) + idx);
+  }
+  __device__ static __forceinline__ void unpack(const Raw v, float f[8]) { unpack8(v, f); }
   __device__ static __forceinline__ void load(const uint16_t* __restrict__ row, int idx, float f[8]) {
-    unpack8(ld_stream(reinterpret_cast<const u32x4*>(row) + idx), f);
+    unpack8(raw(row, idx), f);
   }
   __device__ static __forceinline__ void store(uint16_t* __restrict__ row, int idx, const float f[8]) {
     st_stream(reinterpret_cast<u32x4*>(row) + idx, pack8(f));
@@ -103,8 +109,11 @@ struct Lanes<8> {
 
 template <>
 struct Lanes<1> {
+  using Raw = uint32_t;
+  __device__ static __forceinline__ Raw raw(const uint16_t* __restrict__ row, int idx) { return row[idx]; }
+  __device__ static __forceinline__ void unpack(const Raw v, float f[1]) { f[0] = __uint_as_float(v << 16); }
   __device__ static __forceinline__ void load(const uint16_t* __restrict__ row, int idx, float f[1]) {
-    f[0] = bf16_to_f32(row[idx]);
+    unpack(raw(row, idx), f);
   }
   __device__ static __forceinline__ void store(uint16_t* __restrict__ row, int idx, const float f[1]) {
     row[idx] = f32_to_bf16(f[0]);
