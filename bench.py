@@ -115,22 +115,43 @@ def make_step(inp: dict, T: int, C: int):
     }
 
 
-def copy_ceiling_gbps(nbytes: int = 1 << 30, iters: int = 20) -> float:
-    """HBM GB/s of torch's device copy (read + write) of an nbytes buffer."""
-    src = torch.empty(nbytes // 2, dtype=torch.bfloat16, device="cuda").normal_()
-    dst = torch.empty_like(src)
-    for _ in range(3):
-        dst.copy_(src)
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    s.record()
-    for _ in range(iters):
-        dst.copy_(src)
-    e.record()
-    torch.cuda.synchronize()
-    ms = s.elapsed_time(e) / iters
-    del src, dst
-    return 2 * nbytes / (ms * 1e-3) / 1e9
+def read_write_split(T: int, n: int, C: int, D: int) -> dict[str, tuple[int, int]]:
+    """(bytes read, bytes written) per launch; sums to bytes_model."""
+    bf, f4 = 2, 4
+    nC = n * C
+    return {
+        "k1_fwd": (bf * T * nC + bf * D * nC, bf * T * D + f4 * T),
+        "k1_bwd_dx": (bf * T * nC + bf * D * nC + 2 * bf * T * D + f4 * T, bf * T * nC),
+        "k3_fwd": (bf * T * nC + f4 * T * n, bf * T * C),
+        "k3_bwd": (bf * T * nC + f4 * T * n + bf * T * C, bf * T * nC + f4 * T * n),
+        "k4_fwd": (bf * T * nC + bf * T * C + f4 * T * n * n + f4 * T * n, bf * T * nC),
+        "k4_bwd": (2 * bf * T * nC + bf * T * C + f4 * T * n * n + f4 * T * n,
+                   bf * T * nC + bf * T * C + f4 * T * n * n + f4 * T * n),
+    }
+
+
+def stream_ceilings(nbytes: int = 1 << 30, iters: int = 10) -> dict[str, float]:
+    """Measured HBM GB/s of 16-byte streaming read / write / copy (fmhc_stream_probe)."""
+    from flash_mhc import _abi
+
+    lib = _abi.load()
+    a = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
+    b = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    out = {}
+    for name, kind, moved in (("read", 0, nbytes), ("write", 1, nbytes), ("copy", 2, 2 * nbytes)):
+        run = lambda: _abi.check(lib.fmhc_stream_probe(kind, a.data_ptr(), b.data_ptr(), nbytes, st), "stream_probe")  # noqa: E731
+        for _ in range(3):
+            run()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(iters):
+            run()
+        e1.record()
+        torch.cuda.synchronize()
+        out[name] = round(moved / (e0.elapsed_time(e1) / iters * 1e-3) / 1e9, 1)
+    del a, b
+    return out
 
 
 def cpu_baseline(C: int, tokens: int, iters: int = 3) -> dict:
@@ -280,7 +301,13 @@ def main() -> None:
         except (OSError, ValueError):
             traffic = None
 
-    ceiling = copy_ceiling_gbps()
+    ceil = stream_ceilings()
+    split = read_write_split(T, n, C, D)
+    for name in KERNELS:
+        rd, wr = split[name]
+        mix = (rd + wr) / (rd / ceil["read"] + wr / ceil["write"])
+        per[name]["mix_ceiling_GBps"] = round(mix, 1)
+        per[name]["frac_of_mix_ceiling"] = round(per[name]["GBps"] / mix, 4)
     line = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -302,7 +329,7 @@ def main() -> None:
         "frac_of_peak": round(value / PEAK_GBPS, 4),
         "tokens_per_s": round(T / (ms_per_step * 1e-3), 1),
         "sum_kernel_ms": round(sum_kernel_ms, 4),
-        "copy_ceiling_GBps": round(ceiling, 1),
+        "ceilings_GBps": ceil,
         "kernels": per,
         "roofline": {
             "kernel": dom,

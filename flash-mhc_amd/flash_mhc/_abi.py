@@ -23,7 +23,7 @@ LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libflash_mhc_hip.so"
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 
-# name -> argtypes, following include/flash_mhc_hip.h
+# name -> argtypes, following include/flash_mhc_hip.h and include/flash_mhc_probe.h
 SIGNATURES: dict[str, list] = {
     "fmhc_k1_fwd": [_P, _P, _P, _P, _I64, _I64, _I64, _P],
     "fmhc_k1_bwd_dx": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
@@ -32,6 +32,7 @@ SIGNATURES: dict[str, list] = {
     "fmhc_k4_fwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
     "fmhc_k4_bwd": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
     "fmhc_error_string": [ctypes.c_int],
+    "fmhc_stream_probe": [ctypes.c_int, _P, _P, _I64, _P],
     "fmhc_abi_version": [],
 }
 RESTYPES = {"fmhc_error_string": ctypes.c_char_p}
