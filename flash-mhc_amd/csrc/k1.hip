@@ -26,6 +26,7 @@ constexpr int kDout = 32;
 constexpr float kEps = 1e-6f;
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -216,13 +217,24 @@ struct BwdFrag {
   u32x4 xv[4];    // x of those tokens, k = kl .. kl + 8
 };
 
-template <int NTB>
+// With DW = true the same pass also accumulates the weight gradient
+//   grad_W[d, k] = sum_t bf16(go[t,d] * inv_rms[t]) * x[t,k]
+// (ops.py:683-684 of the reference computes it as a separate matmul that reads
+// x a second time).  The lane's x registers for one token block (4 tokens x 8
+// consecutive k) are exactly the A operand of v_mfma_f32_16x16x16_bf16 with
+// the contraction over tokens, so tile m of dW^T is
+//   D (16 k x 16 d) += x[tokens, k_slice + 8 * i + m]^T (A) * G[tokens, 16 h + j] (B)
+// with G = bf16(go * inv_rms).  G reaches the B layout through a 1 KiB
+// wave-private LDS tile.  Each wave writes its fp32 partial dW for its slice;
+// k1_dw_reduce sums the partials of all runs in a fixed order.
+template <int NTB, bool DW>
 __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ x,
                                                    const uint16_t* __restrict__ W,
                                                    const uint16_t* __restrict__ go,
                                                    const uint16_t* __restrict__ proj,
                                                    const float* __restrict__ inv_rms,
                                                    uint16_t* __restrict__ gx,
+                                                   float* __restrict__ dw_partial,
                                                    int64_t T, int nC, int nslices) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
@@ -239,6 +251,11 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
   if (run >= nruns || run >= nblocks) return;
   const int kl = slice * 128 + 8 * col;  // this lane's 8 consecutive k
   const bool kok = kl < nC;              // nC % 8 == 0: all 8 valid or none
+
+  __shared__ uint32_t gtile[DW ? 4 : 1][16 * 16];  // wave-private 16 tokens x 32 d bf16
+  f32x4 dacc[DW ? 8 : 1][2];
+#pragma unroll
+  for (int m = 0; m < (DW ? 8 : 1); ++m) dacc[m][0] = dacc[m][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // B tiles: bfr[m] holds W[8 * grp + e][kl + m], e = 0..7.
   bf16x8 bfr[8];
@@ -316,6 +333,51 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
         }
       }
     }
+    if constexpr (DW) {
+      // go block -> LDS (lane (col, grp) holds go[tbase + col][8 grp .. + 8]),
+      // then B operands G[tbase + 4 grp + q][16 h + col], q = 0..3, h = 0..1.
+      uint32_t* tile = gtile[wave];
+      *reinterpret_cast<u32x4*>(tile + col * 16 + grp * 4) = f.gv;
+      // Same-wave LDS operations are performed in order: no wait is needed
+      // between the write above and the reads below.
+      const uint16_t* t16 = reinterpret_cast<const uint16_t*>(tile);
+      uint32_t graw[2][4];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) graw[h][q] = t16[(4 * grp + q) * 32 + 16 * h + col];
+      __builtin_amdgcn_sched_barrier(0);  // issue all eight reads before converting
+      uint32_t bh[2][2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        float gq[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int64_t t = tbase + 4 * grp + q;
+          const float g = __uint_as_float(graw[h][q] << 16);
+          gq[q] = t < T ? g * f.inv[q] : 0.f;  // tail tokens contribute nothing
+        }
+        bh[h][0] = pack_bf16x2(gq[0], gq[1]);
+        bh[h][1] = pack_bf16x2(gq[2], gq[3]);
+      }
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        // A: element m of the 4 tokens' x vectors.
+        uint32_t e[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t w = f.xv[q][m >> 1];
+          e[q] = (m & 1) ? (w >> 16) : (w & 0xffffu);
+        }
+        const u32x2 av = {e[0] | (e[1] << 16), e[2] | (e[3] << 16)};
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const u32x2 bv = {bh[h][0], bh[h][1]};
+          dacc[m][h] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+              __builtin_bit_cast(bf16x4, av), __builtin_bit_cast(bf16x4, bv), dacc[m][h], 0, 0, 0);
+        }
+      }
+    }
   };
   BwdFrag f0, f1;
   load(f0, 0);
@@ -329,6 +391,64 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
     compute(f1, i + 1);
   }
   if (i < nb) compute(f0, i);
+
+  if constexpr (DW) {
+    // Partial layout [run][slice][m][h][r][lane]: one 256-byte row per store.
+    float* dst = dw_partial + (run * nslices + slice) * (8 * 2 * 4 * kWave);
+#pragma unroll
+    for (int m = 0; m < 8; ++m)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dst[((m * 2 + h) * 4 + r) * kWave + lane] = dacc[m][h][r];
+  }
+}
+
+// Sums the per-run partials of k1_bwd_mfma<NTB, true> in run order and writes
+// grad_W (32, nC) bf16.  Thread i owns partial element i of every run:
+// i = (((slice * 8 + m) * 2 + h) * 4 + r) * 64 + lane, which stands for
+// d = 16 h + (lane & 15), k = 128 slice + 8 (4 (lane >> 4) + r) + m.
+__global__ __launch_bounds__(256) void k1_dw_reduce(const float* __restrict__ partial,
+                                                    uint16_t* __restrict__ dW, int64_t nruns,
+                                                    int nslices, int nC) {
+  const int64_t per_run = static_cast<int64_t>(nslices) * (8 * 2 * 4 * kWave);
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= per_run) return;
+  float acc = 0.f;
+  for (int64_t r = 0; r < nruns; ++r) acc += partial[r * per_run + i];
+  const int lane = static_cast<int>(i % kWave);
+  const int rr = static_cast<int>((i / kWave) % 4);
+  const int h = static_cast<int>((i / (4 * kWave)) % 2);
+  const int m = static_cast<int>((i / (8 * kWave)) % 8);
+  const int slice = static_cast<int>(i / (64 * kWave));
+  const int d = 16 * h + (lane & 15);
+  const int k = 128 * slice + 8 * (4 * (lane >> 4) + rr) + m;
+  if (k < nC) dW[static_cast<int64_t>(d) * nC + k] = f32_to_bf16(acc);
+}
+
+// grad_W of an empty batch (a kernel, not a memset, so the call can be captured
+// in a graph).
+__global__ __launch_bounds__(256) void k1_dw_zero(uint16_t* __restrict__ dW, int nC) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i < static_cast<int64_t>(kDout) * nC) dW[i] = 0;
+}
+
+// Element-wise weight gradient for shapes the matrix-core path does not take:
+// one thread per (d, k), tokens summed in order.
+__global__ __launch_bounds__(256) void k1_dw_scalar(const uint16_t* __restrict__ x,
+                                                    const uint16_t* __restrict__ go,
+                                                    const float* __restrict__ inv_rms,
+                                                    uint16_t* __restrict__ dW, int64_t T, int nC) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= static_cast<int64_t>(kDout) * nC) return;
+  const int d = static_cast<int>(i / nC);
+  const int k = static_cast<int>(i % nC);
+  float acc = 0.f;
+  for (int64_t t = 0; t < T; ++t) {
+    const float g = bf16_to_f32(f32_to_bf16(bf16_to_f32(go[t * kDout + d]) * inv_rms[t]));
+    acc = __builtin_fmaf(g, bf16_to_f32(x[t * nC + k]), acc);
+  }
+  dW[i] = f32_to_bf16(acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -400,7 +520,8 @@ __global__ __launch_bounds__(256) void k1_bwd_scalar(const uint16_t* __restrict_
 
 constexpr int kFwdR = 8;      // token blocks of 16 per workgroup
 constexpr int kFwdSplit = 4;  // waves per workgroup (split of the nC axis)
-constexpr int kBwdNTB = 16;   // token blocks of 16 per wave
+constexpr int kBwdNTB = 16;   // token blocks of 16 per wave (dx only)
+constexpr int kBwdDwNTB = 64; // token blocks of 16 per wave when grad_W is fused
 
 bool bad_sizes(int64_t T, int64_t nC, int64_t D_out) {
   return T < 0 || nC <= 0 || nC > (int64_t{1} << 30) || D_out != kDout;
@@ -442,11 +563,64 @@ extern "C" int fmhc_k1_bwd_dx(const uint16_t* x_flat, const uint16_t* W, const u
     const int nslices = static_cast<int>((nC + 127) / 128);
     const int64_t nruns = (T + 16 * kBwdNTB - 1) / (16 * kBwdNTB);
     const dim3 grid(blocks_for(nruns * nslices, 4));
-    k1_bwd_mfma<kBwdNTB><<<grid, 256, 0, s>>>(x_flat, W, grad_out, proj_out, inv_rms, grad_x, T, nc,
-                                              nslices);
+    k1_bwd_mfma<kBwdNTB, false><<<grid, 256, 0, s>>>(x_flat, W, grad_out, proj_out, inv_rms, grad_x,
+                                                     nullptr, T, nc, nslices);
   } else {
     const dim3 grid(blocks_for(T, 4));
     k1_bwd_scalar<<<grid, 256, 0, s>>>(x_flat, W, grad_out, proj_out, inv_rms, grad_x, T, nc);
   }
+  return launch_status();
+}
+
+namespace fmhc {
+namespace {
+bool k1_bwd_fused_path(const void* x, const void* W, const void* go, const void* proj, const void* gx,
+                       int64_t nC) {
+  return nC % 8 == 0 && aligned16(x) && aligned16(W) && aligned16(go) && aligned16(proj) &&
+         aligned16(gx);
+}
+int64_t k1_bwd_runs(int64_t T) { return (T + 16 * kBwdDwNTB - 1) / (16 * kBwdDwNTB); }
+}  // namespace
+}  // namespace fmhc
+
+extern "C" int64_t fmhc_k1_bwd_workspace_bytes(int64_t T, int64_t nC) {
+  using namespace fmhc;
+  if (T <= 0 || nC <= 0 || nC % 8 != 0) return 0;
+  const int64_t nslices = (nC + 127) / 128;
+  return k1_bwd_runs(T) * nslices * (8 * 2 * 4 * kWave) * static_cast<int64_t>(sizeof(float));
+}
+
+extern "C" int fmhc_k1_bwd(const uint16_t* x_flat, const uint16_t* W, const uint16_t* grad_out,
+                           const uint16_t* proj_out, const float* inv_rms, uint16_t* grad_x,
+                           uint16_t* grad_W, void* workspace, int64_t workspace_bytes, int64_t T,
+                           int64_t nC, int64_t D_out, void* stream) {
+  using namespace fmhc;
+  if (bad_sizes(T, nC, D_out)) return FMHC_ERR_INVALID_ARGUMENT;
+  if (!grad_W) return FMHC_ERR_INVALID_ARGUMENT;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int nc = static_cast<int>(nC);
+  if (T == 0) {  // grad_W of an empty batch is zero
+    k1_dw_zero<<<dim3(blocks_for(static_cast<int64_t>(kDout) * nC, 256)), 256, 0, s>>>(grad_W, nC);
+    return launch_status();
+  }
+  if (!x_flat || !W || !grad_out || !proj_out || !inv_rms || !grad_x) return FMHC_ERR_INVALID_ARGUMENT;
+  if (k1_bwd_fused_path(x_flat, W, grad_out, proj_out, grad_x, nC)) {
+    const int64_t need = fmhc_k1_bwd_workspace_bytes(T, nC);
+    if (!workspace || workspace_bytes < need || !aligned16(workspace)) return FMHC_ERR_INVALID_ARGUMENT;
+    const int nslices = static_cast<int>((nC + 127) / 128);
+    const int64_t nruns = k1_bwd_runs(T);
+    float* partial = static_cast<float*>(workspace);
+    k1_bwd_mfma<kBwdDwNTB, true><<<dim3(blocks_for(nruns * nslices, 4)), 256, 0, s>>>(
+        x_flat, W, grad_out, proj_out, inv_rms, grad_x, partial, T, nc, nslices);
+    const int st = launch_status();
+    if (st != FMHC_OK) return st;
+    const int64_t per_run = static_cast<int64_t>(nslices) * (8 * 2 * 4 * kWave);
+    k1_dw_reduce<<<dim3(blocks_for(per_run, 256)), 256, 0, s>>>(partial, grad_W, nruns, nslices, nc);
+    return launch_status();
+  }
+  const int st = fmhc_k1_bwd_dx(x_flat, W, grad_out, proj_out, inv_rms, grad_x, T, nC, D_out, stream);
+  if (st != FMHC_OK) return st;
+  k1_dw_scalar<<<dim3(blocks_for(static_cast<int64_t>(kDout) * nC, 256)), 256, 0, s>>>(
+      x_flat, grad_out, inv_rms, grad_W, T, nc);
   return launch_status();
 }

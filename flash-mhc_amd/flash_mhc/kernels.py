@@ -9,6 +9,7 @@ missing extension or a bad argument raises.
 Reference counterparts (alint77/flash-mHC):
   k1_fwd     <- src/flash_mhc/kernels.py:250-303  _fused_rmsnorm_project_fwd_kernel
   k1_bwd_dx  <- src/flash_mhc/kernels.py:306-376  _fused_rmsnorm_project_bwd_dx_kernel
+  k1_bwd     <- the above plus the grad_W matmul of src/flash_mhc/ops.py:683-684, fused
   k3_fwd     <- src/flash_mhc/kernels.py:673-717  _fused_pre_map_fwd_kernel
   k3_bwd     <- src/flash_mhc/kernels.py:720-853  _fused_pre_map_bwd_fused_kernel_n4
   k4_fwd     <- src/flash_mhc/kernels.py:384-481  _fused_post_res_fwd_kernel_n4
@@ -117,6 +118,38 @@ def k1_bwd_dx(grad_out: torch.Tensor, x_flat: torch.Tensor, W: torch.Tensor,
                                 T, nC, D_OUT, _abi.stream_of(x_flat))
     _abi.check(st, "k1_bwd_dx")
     return grad_x
+
+
+def k1_bwd(grad_out: torch.Tensor, x_flat: torch.Tensor, W: torch.Tensor,
+           proj_out: torch.Tensor, inv_rms: torch.Tensor,
+           grad_x: torch.Tensor | None = None,
+           grad_W: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """(grad_x, grad_W) of K1 in one pass over x; grad_W is (32, nC) bf16 and
+    equals bf16(bf16(grad_out * inv_rms)^T @ x_flat) up to fp32 summation order."""
+    dev = _device_of(x_flat)
+    if x_flat.dim() != 2:
+        raise ValueError(f"x_flat must be 2-D (T, nC), got shape {tuple(x_flat.shape)}")
+    T, nC = x_flat.shape
+    _require(x_flat, "x_flat", _BF16, (T, nC), dev)
+    _require(W, "W", _BF16, (D_OUT, nC), dev)
+    _require(grad_out, "grad_out", _BF16, (T, D_OUT), dev)
+    _require(proj_out, "proj_out", _BF16, (T, D_OUT), dev)
+    _require(inv_rms, "inv_rms", _F32, (T,), dev)
+    if grad_x is None:
+        grad_x = torch.empty_like(x_flat)
+    if grad_W is None:
+        grad_W = torch.empty((D_OUT, nC), device=dev, dtype=_BF16)
+    _require(grad_x, "grad_x", _BF16, (T, nC), dev)
+    _require(grad_W, "grad_W", _BF16, (D_OUT, nC), dev)
+    lib = _abi.load()
+    nbytes = int(lib.fmhc_k1_bwd_workspace_bytes(T, nC))
+    ws = torch.empty((max(nbytes, 16),), device=dev, dtype=torch.uint8)
+    with _OnDevice(dev):
+        st = lib.fmhc_k1_bwd(x_flat.data_ptr(), W.data_ptr(), grad_out.data_ptr(), proj_out.data_ptr(),
+                             inv_rms.data_ptr(), grad_x.data_ptr(), grad_W.data_ptr(), ws.data_ptr(),
+                             ws.numel(), T, nC, D_OUT, _abi.stream_of(x_flat))
+    _abi.check(st, "k1_bwd")
+    return grad_x, grad_W
 
 
 def _streams_shape(x: torch.Tensor) -> tuple[int, int, int]:

@@ -14,10 +14,15 @@ Reference map:
   device impls                         ops.py:205-667
   autograd (setup_context + backward)  ops.py:670-714
   disable_autotune_temporarily         ops.py:44-58
+
+Addition: fused_rmsnorm_project_bwd (grad_x and grad_W of K1 in one pass over
+x); the K1 autograd rule uses it unless FLASH_MHC_FUSED_DW=0, in which case it
+runs the reference's two-step rule (bwd_dx, then a matmul for grad_W).
 """
 
 from __future__ import annotations
 
+import os
 import threading
 from contextlib import contextmanager
 
@@ -33,6 +38,12 @@ _lib.define(
 )
 _lib.define(
     "fused_rmsnorm_project_bwd_dx(Tensor grad_out, Tensor x_flat, Tensor W, Tensor proj_out, Tensor inv_rms) -> Tensor grad_x"
+)
+
+# Not in the reference: K1's x- and W-gradient in one pass over x (the
+# reference's autograd rule computes grad_W with a second matmul over x).
+_lib.define(
+    "fused_rmsnorm_project_bwd(Tensor grad_out, Tensor x_flat, Tensor W, Tensor proj_out, Tensor inv_rms) -> (Tensor grad_x, Tensor grad_W)"
 )
 
 _lib.define("fused_pre_map(Tensor x_streams, Tensor h_pre) -> Tensor out")
@@ -86,6 +97,11 @@ def _fused_rmsnorm_project_fake(x_flat: torch.Tensor, W: torch.Tensor):
 @torch.library.register_fake("flash_mhc::fused_rmsnorm_project_bwd_dx")
 def _fused_rmsnorm_project_bwd_dx_fake(grad_out, x_flat, W, proj_out, inv_rms):
     return torch.empty_like(x_flat)
+
+
+@torch.library.register_fake("flash_mhc::fused_rmsnorm_project_bwd")
+def _fused_rmsnorm_project_bwd_fake(grad_out, x_flat, W, proj_out, inv_rms):
+    return torch.empty_like(x_flat), torch.empty_like(W, dtype=x_flat.dtype)
 
 
 @torch.library.register_fake("flash_mhc::fused_pre_map")
@@ -143,6 +159,12 @@ def _fused_rmsnorm_project_bwd_dx_cuda(grad_out, x_flat, W, proj_out, inv_rms):
                         proj_out.contiguous(), inv_rms.contiguous())
 
 
+@torch.library.impl(_lib, "fused_rmsnorm_project_bwd", "CUDA")
+def _fused_rmsnorm_project_bwd_cuda(grad_out, x_flat, W, proj_out, inv_rms):
+    return _k.k1_bwd(grad_out.contiguous(), x_flat.contiguous(), W.to(x_flat.dtype).contiguous(),
+                     proj_out.contiguous(), inv_rms.contiguous())
+
+
 @torch.library.impl(_lib, "fused_pre_map", "CUDA")
 def _fused_pre_map_cuda(x_streams: torch.Tensor, h_pre: torch.Tensor):
     _check_n4(x_streams, "flash_mhc::fused_pre_map currently supports n=4 only")
@@ -181,9 +203,20 @@ def _setup_k1(ctx, inputs, output):
     ctx.save_for_backward(x_flat, W, out, inv_rms)
 
 
+def _fused_dw_enabled() -> bool:
+    v = os.getenv("FLASH_MHC_FUSED_DW", "1").strip().lower()
+    return v not in {"0", "false", "off", "no"}
+
+
 def _fused_rmsnorm_project_backward(ctx, grad_out, grad_inv_rms):
     # inv_rms is treated as non-differentiable, as in the reference.
     x_flat, W, proj_out, inv_rms = ctx.saved_tensors
+    if _fused_dw_enabled():
+        # Same gradients as the two-step rule below, computed in one pass over x.
+        grad_x, grad_W = torch.ops.flash_mhc.fused_rmsnorm_project_bwd(
+            grad_out, x_flat, W, proj_out, inv_rms
+        )
+        return grad_x, grad_W
     grad_x = torch.ops.flash_mhc.fused_rmsnorm_project_bwd_dx(
         grad_out, x_flat, W, proj_out, inv_rms
     )

@@ -56,6 +56,23 @@ int fmhc_k1_bwd_dx(const uint16_t* x_flat, const uint16_t* W, const uint16_t* gr
                    const uint16_t* proj_out, const float* inv_rms, uint16_t* grad_x,
                    int64_t T, int64_t nC, int64_t D_out, void* stream);
 
+/* K1 backward, grad of x_flat and of W in one pass over x:
+ *   grad_x as fmhc_k1_bwd_dx;
+ *   grad_W[d,k] = bf16(sum_t bf16(go[t,d] * inv_rms[t]) * x[t,k])   (fp32 accumulation)
+ * grad_W (D_out, nC) bf16.  `workspace` is device memory of at least
+ * fmhc_k1_bwd_workspace_bytes(T, nC) bytes, 16-byte aligned, for per-wave
+ * partial sums (summed in a fixed order: results are deterministic).
+ * Replaces: src/flash_mhc/ops.py:678-685 (_fused_rmsnorm_project_backward:
+ *           the bwd_dx launch plus the grad_W torch.matmul, which reads x again). */
+int fmhc_k1_bwd(const uint16_t* x_flat, const uint16_t* W, const uint16_t* grad_out,
+                const uint16_t* proj_out, const float* inv_rms, uint16_t* grad_x, uint16_t* grad_W,
+                void* workspace, int64_t workspace_bytes, int64_t T, int64_t nC, int64_t D_out,
+                void* stream);
+
+/* Workspace bytes fmhc_k1_bwd needs for (T, nC); 0 when none is needed.
+ * No counterpart in the reference. */
+int64_t fmhc_k1_bwd_workspace_bytes(int64_t T, int64_t nC);
+
 /* K3 forward: out[t,c] = bf16(sum_j h_pre[t,j] * x[t,j,c]), j = 0..3 in order.
  * x (T, n, C) bf16; h_pre (T, n) fp32; out (T, C) bf16.
  * Replaces: src/flash_mhc/ops.py:347-414 (_fused_pre_map_cuda) launching

@@ -29,6 +29,12 @@ def _k1_bwd_dx(grad_out, x_flat, W, proj_out, inv_rms):
     return R.to(x_flat.dtype)
 
 
+def _k1_bwd(grad_out, x_flat, W, proj_out, inv_rms):
+    gx, _ = O.k1_bwd_dx(grad_out, x_flat, W, proj_out, inv_rms)
+    gW, _ = O.k1_grad_W(grad_out, x_flat, inv_rms)
+    return gx.to(x_flat.dtype), gW.to(x_flat.dtype)
+
+
 def _k3(x, h):
     if x.shape[1] != 4:
         raise ValueError("flash_mhc::fused_pre_map currently supports n=4 only")
@@ -55,6 +61,7 @@ def _k4_bwd(go, x, lo, H, hp):
 IMPLS = {
     "fused_rmsnorm_project": _k1,
     "fused_rmsnorm_project_bwd_dx": _k1_bwd_dx,
+    "fused_rmsnorm_project_bwd": _k1_bwd,
     "fused_pre_map": _k3,
     "fused_pre_map_backward": _k3_bwd,
     "fused_post_res": _k4,

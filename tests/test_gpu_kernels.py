@@ -117,6 +117,50 @@ def test_k1_bwd_dx_misaligned():
     check_bf16("k1 grad_x (misaligned)", gx, R, S, 64)
 
 
+@pytest.mark.parametrize("T,C", [(2048, 256), (257, 1024), (1, 4096), (1500, 1024), (333, 100), (31, 24), (17, 25)])
+def test_k1_bwd_fused_dw(T, C):
+    """grad_x and grad_W in one pass: grad_x as the dx kernel, grad_W against
+    the oracle's bf16(bf16(go * inv_rms)^T @ x) with n = T terms."""
+    x, W = _k1_inputs(T, C, seed=200 + T + C, stress=True)
+    go = randn((T, 32), seed=201 + T)
+    xd, Wd = x.to(DEV), W.to(DEV)
+    proj, inv = K.k1_fwd(xd, Wd)
+    gx, gW = K.k1_bwd(go.to(DEV), xd, Wd, proj, inv)
+    gx_ref = K.k1_bwd_dx(go.to(DEV), xd, Wd, proj, inv)
+    torch.cuda.synchronize()
+    R, S = O.k1_bwd_dx(go, x, W, proj.cpu(), inv.cpu())
+    check_bf16("k1 fused grad_x", gx, R, S, 64)
+    assert torch.equal(gx, gx_ref)  # same arithmetic as the dx-only kernel
+    R, S = O.k1_grad_W(go, x, inv.cpu())
+    check_bf16("k1 fused grad_W", gW, R, S, T)
+
+
+def test_k1_bwd_fused_dw_misaligned_and_empty():
+    T, C = 300, 256
+    x, W = _k1_inputs(T, C, seed=210)
+    go = randn((T, 32), seed=211)
+    proj, inv = K.k1_fwd(x.to(DEV), W.to(DEV))
+    gx, gW = K.k1_bwd(misaligned(go), misaligned(x), W.to(DEV), misaligned(proj.cpu()), inv)
+    R, S = O.k1_grad_W(go, x, inv.cpu())
+    check_bf16("k1 fused grad_W (element-wise path)", gW, R, S, T)
+    e = torch.empty((0, 4 * C), dtype=torch.bfloat16, device=DEV)
+    gx0, gW0 = K.k1_bwd(torch.empty((0, 32), dtype=torch.bfloat16, device=DEV), e, W.to(DEV),
+                        torch.empty((0, 32), dtype=torch.bfloat16, device=DEV),
+                        torch.empty((0,), device=DEV))
+    assert gx0.shape == (0, 4 * C) and torch.count_nonzero(gW0) == 0
+
+
+def test_k1_bwd_fused_dw_deterministic():
+    T, C = 4096, 1024
+    x, W = _k1_inputs(T, C, seed=220)
+    go = randn((T, 32), seed=221)
+    xd, Wd = x.to(DEV), W.to(DEV)
+    proj, inv = K.k1_fwd(xd, Wd)
+    a = K.k1_bwd(go.to(DEV), xd, Wd, proj, inv)
+    b = K.k1_bwd(go.to(DEV), xd, Wd, proj, inv)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
 # ---------------------------------------------------------------------------
 # K3
 

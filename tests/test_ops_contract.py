@@ -42,6 +42,20 @@ def test_schema_matches_reference(name):
     assert str(op._schema) == "flash_mhc::" + REFERENCE_SCHEMAS[name]
 
 
+def test_fused_backward_op_contract():
+    op = torch.ops.flash_mhc.fused_rmsnorm_project_bwd.default
+    assert str(op._schema) == ("flash_mhc::fused_rmsnorm_project_bwd(Tensor grad_out, Tensor x_flat, "
+                               "Tensor W, Tensor proj_out, Tensor inv_rms) -> (Tensor grad_x, Tensor grad_W)")
+    assert torch._C._dispatch_has_kernel_for_dispatch_key("flash_mhc::fused_rmsnorm_project_bwd", "CUDA")
+    assert not torch._C._dispatch_has_kernel_for_dispatch_key("flash_mhc::fused_rmsnorm_project_bwd", "CPU")
+    with FakeTensorMode():
+        xf = torch.empty(7, 96, dtype=BF16)
+        W = torch.empty(32, 96, dtype=BF16)
+        g = torch.empty(7, 32, dtype=BF16)
+        gx, gW = torch.ops.flash_mhc.fused_rmsnorm_project_bwd(g, xf, W, g, torch.empty(7))
+        assert gx.shape == xf.shape and gx.dtype == BF16 and gW.shape == W.shape and gW.dtype == BF16
+
+
 def test_only_device_kernels_registered():
     """No CPU implementation ships: the device path cannot silently fall back."""
     for name in REFERENCE_SCHEMAS:
@@ -143,6 +157,7 @@ def test_opcheck_all_ops(cpu_kernels):
     cases = [
         (torch.ops.flash_mhc.fused_rmsnorm_project.default, (xf.clone().requires_grad_(True), W.clone().requires_grad_(True))),
         (torch.ops.flash_mhc.fused_rmsnorm_project_bwd_dx.default, (rnd((T, 32), 16), xf, W, proj, inv)),
+        (torch.ops.flash_mhc.fused_rmsnorm_project_bwd.default, (rnd((T, 32), 16), xf, W, proj, inv)),
         (torch.ops.flash_mhc.fused_pre_map.default, (x.clone().requires_grad_(True), h.clone().requires_grad_(True))),
         (torch.ops.flash_mhc.fused_pre_map_backward.default, (rnd((T, C), 17), x, h)),
         (torch.ops.flash_mhc.fused_post_res.default,
@@ -151,6 +166,23 @@ def test_opcheck_all_ops(cpu_kernels):
     ]
     for op, args in cases:
         torch.library.opcheck(op, args)
+
+
+@pytest.mark.parametrize("fused", ["1", "0"])
+def test_k1_autograd_rules_agree(cpu_kernels, monkeypatch, fused):
+    """The fused K1 backward op and the reference's two-step rule give the
+    same gradients (bf16 rounding of grad_W aside)."""
+    monkeypatch.setenv("FLASH_MHC_FUSED_DW", fused)
+    T, C, x, xf, W, h, lo, H, hp = _samples()
+    xs = xf.clone().requires_grad_(True)
+    Ws = W.clone().requires_grad_(True)
+    proj, inv = torch.ops.flash_mhc.fused_rmsnorm_project(xs, Ws)
+    go1 = rnd((T, 32), 21)
+    proj.backward(go1)
+    gx, _ = O.k1_bwd_dx(go1, xf, W, proj.detach(), inv)
+    gW, _ = O.k1_grad_W(go1, xf, inv)
+    assert torch.equal(xs.grad, gx.to(BF16))
+    torch.testing.assert_close(Ws.grad.double(), gW, rtol=1e-2, atol=1e-2)
 
 
 def test_autograd_formulas(cpu_kernels):
