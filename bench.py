@@ -115,6 +115,43 @@ def make_step(inp: dict, T: int, C: int):
     }
 
 
+def k1_backward_paths(inp: dict, T: int, C: int, iters: int = 20) -> dict:
+    """K1's full backward (grad_x and grad_W): the fused kernel vs the
+    reference's two-step rule (bwd_dx kernel + torch.matmul for grad_W,
+    ops.py:680-684).  Algorithmic bytes: bwd_dx's plus the bf16 grad_W write."""
+    from flash_mhc import kernels as K
+
+    n, D = 4, 32
+    nC = n * C
+    x, W, go = inp["x"].view(T, nC), inp["W"], inp["go1"]
+    proj, inv = K.k1_fwd(x, W)
+    gx = torch.empty_like(x)
+    gW = torch.empty((D, nC), dtype=torch.bfloat16, device=x.device)
+
+    def fused():
+        K.k1_bwd(go, x, W, proj, inv, gx, gW)
+
+    def two_step():
+        K.k1_bwd_dx(go, x, W, proj, inv, gx)
+        torch.matmul((go * inv[:, None]).to(x.dtype).t().contiguous(), x)
+
+    out = {}
+    nbytes = bytes_model(T, n, C, D)["k1_bwd_dx"] + 2 * D * nC
+    for name, fn in (("fused", fused), ("two_step", two_step)):
+        for _ in range(3):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(iters):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / iters * 1e3
+        out[name] = {"avg_us": round(us, 2), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
+    out["bytes"] = nbytes
+    return out
+
+
 def read_write_split(T: int, n: int, C: int, D: int) -> dict[str, tuple[int, int]]:
     """(bytes read, bytes written) per launch; sums to bytes_model."""
     bf, f4 = 2, 4
@@ -301,6 +338,7 @@ def main() -> None:
         except (OSError, ValueError):
             traffic = None
 
+    k1_full_bwd = k1_backward_paths(inp, T, C)
     ceil = stream_ceilings()
     split = read_write_split(T, n, C, D)
     for name in KERNELS:
@@ -330,6 +368,7 @@ def main() -> None:
         "tokens_per_s": round(T / (ms_per_step * 1e-3), 1),
         "sum_kernel_ms": round(sum_kernel_ms, 4),
         "ceilings_GBps": ceil,
+        "k1_backward_with_grad_W": k1_full_bwd,
         "kernels": per,
         "roofline": {
             "kernel": dom,

@@ -227,7 +227,7 @@ struct BwdFrag {
 // with G = bf16(go * inv_rms).  G reaches the B layout through a 1 KiB
 // wave-private LDS tile.  Each wave writes its fp32 partial dW for its slice;
 // k1_dw_reduce sums the partials of all runs in a fixed order.
-template <int NTB, bool DW>
+template <int NTB, bool DW, bool FULLK>
 __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ x,
                                                    const uint16_t* __restrict__ W,
                                                    const uint16_t* __restrict__ go,
@@ -240,6 +240,10 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
   const int col = lane & 15;  // A row (token) for the loads of go, B/D column
   const int grp = lane >> 4;  // 8-wide d group of A/B; 4-token group of D
+  // Wave -> (k slice, run): the four waves of a workgroup take four
+  // consecutive slices (1 KiB of each x row) of the same run.  (Giving them
+  // one slice and four runs, to sum their grad_W partials in LDS, measured
+  // 8% slower.)
   const int64_t wid = static_cast<int64_t>(blockIdx.x) * 4 + wave;
   const int slice = static_cast<int>(wid % nslices);
   const int64_t run = wid / nslices;
@@ -247,10 +251,14 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
   // one time work on neighbouring blocks, so the concurrent reads and writes
   // cover contiguous memory instead of addresses a power-of-two apart.
   const int64_t nblocks = (T + 15) / 16;
-  const int64_t nruns = (nblocks + NTB - 1) / NTB;
-  if (run >= nruns || run >= nblocks) return;
+  const int64_t nruns = (nblocks + NTB - 1) / NTB;  // <= nblocks
+  if (run >= nruns) return;
   const int kl = slice * 128 + 8 * col;  // this lane's 8 consecutive k
-  const bool kok = kl < nC;              // nC % 8 == 0: all 8 valid or none
+  const bool kok = FULLK || kl < nC;     // nC % 8 == 0: all 8 valid or none
+  // Addresses are a wave-uniform block base plus a 32-bit per-lane byte offset
+  // (16 rows of x span 32 * nC bytes < 2^32, checked by the caller).
+  const uint32_t row_bytes = 2u * static_cast<uint32_t>(nC);
+  const uint32_t kbytes = 2u * static_cast<uint32_t>(kl);
 
   __shared__ uint32_t gtile[DW ? 4 : 1][16 * 16];  // wave-private 16 tokens x 32 d bf16
   f32x4 dacc[DW ? 8 : 1][2];
@@ -285,22 +293,30 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
   const int64_t left = (nblocks - run + nruns - 1) / nruns;
   const int nb = static_cast<int>(left < NTB ? left : NTB);
   auto pos = [&](int i) { return i < nb ? i : nb - 1; };
+  auto block_base = [&](int tb) { return (run + static_cast<int64_t>(tb) * nruns) * 16; };
+  // Valid rows of the block starting at tbase (16 except in the last block).
+  auto block_rows = [&](int64_t tbase) { return static_cast<int>(T - tbase < 16 ? T - tbase : 16); };
   auto load = [&](BwdFrag& f, int tb) {
-    const int64_t tbase = (run + static_cast<int64_t>(tb) * nruns) * 16;
-    const int64_t ta = tbase + col < T ? tbase + col : T - 1;
-    f.gv = *reinterpret_cast<const u32x4*>(go + ta * kDout + 8 * grp);
-    f.pv = *reinterpret_cast<const u32x4*>(proj + ta * kDout + 8 * grp);
+    const int64_t tbase = block_base(tb);
+    const int last = block_rows(tbase) - 1;  // rows past the end re-read the last one
+    const int rg = col < last ? col : last;
+    const uint32_t goff = static_cast<uint32_t>(rg) * (2u * kDout) + 16u * static_cast<uint32_t>(grp);
+    f.gv = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(go + tbase * kDout) + goff);
+    f.pv = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(proj + tbase * kDout) + goff);
+    const char* ib = reinterpret_cast<const char*>(inv_rms + tbase);
+    const char* xb = reinterpret_cast<const char*>(x + tbase * nC);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int64_t t = tbase + 4 * grp + q;
-      const int64_t tl = t < T ? t : T - 1;
-      f.inv[q] = inv_rms[tl];
+      const int r0 = 4 * grp + q;
+      const uint32_t r = static_cast<uint32_t>(r0 < last ? r0 : last);
+      f.inv[q] = *reinterpret_cast<const float*>(ib + 4u * r);
       f.xv[q] = u32x4{0u, 0u, 0u, 0u};
-      if (kok) f.xv[q] = ld_stream(reinterpret_cast<const u32x4*>(x + tl * nC + kl));
+      if (kok) f.xv[q] = ld_stream(reinterpret_cast<const u32x4*>(xb + (r * row_bytes + kbytes)));
     }
   };
   auto compute = [&](const BwdFrag& f, int tb) {
-    const int64_t tbase = (run + static_cast<int64_t>(tb) * nruns) * 16;
+    const int64_t tbase = block_base(tb);
+    const int rows = block_rows(tbase);
     // dot(go, proj_out) of token tbase + col, over the four 8-wide d groups.
     float gf[8], pf[8];
     unpack8(f.gv, gf);
@@ -321,15 +337,16 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
 #pragma unroll
     for (int m = 0; m < 8; ++m) acc[m] = mfma16(a, bfr[m], f32x4{0.f, 0.f, 0.f, 0.f});
     if (kok) {
+      char* gxb = reinterpret_cast<char*>(gx + tbase * nC);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int64_t t = tbase + 4 * grp + q;
-        if (t < T) {
+        const int r = 4 * grp + q;
+        if (r < rows) {
           float xf[8], o[8];
           unpack8(f.xv[q], xf);
 #pragma unroll
           for (int m = 0; m < 8; ++m) o[m] = f.inv[q] * acc[m][q] - scale[q] * xf[m];
-          st_stream(reinterpret_cast<u32x4*>(gx + t * nC + kl), pack8(o));
+          st_stream(reinterpret_cast<u32x4*>(gxb + (static_cast<uint32_t>(r) * row_bytes + kbytes)), pack8(o));
         }
       }
     }
@@ -353,9 +370,8 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
         float gq[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const int64_t t = tbase + 4 * grp + q;
           const float g = __uint_as_float(graw[h][q] << 16);
-          gq[q] = t < T ? g * f.inv[q] : 0.f;  // tail tokens contribute nothing
+          gq[q] = 4 * grp + q < rows ? g * f.inv[q] : 0.f;  // rows past the end contribute nothing
         }
         bh[h][0] = pack_bf16x2(gq[0], gq[1]);
         bh[h][1] = pack_bf16x2(gq[2], gq[3]);
@@ -404,26 +420,42 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
   }
 }
 
-// Sums the per-run partials of k1_bwd_mfma<NTB, true> in run order and writes
-// grad_W (32, nC) bf16.  Thread i owns partial element i of every run:
-// i = (((slice * 8 + m) * 2 + h) * 4 + r) * 64 + lane, which stands for
-// d = 16 h + (lane & 15), k = 128 slice + 8 (4 (lane >> 4) + r) + m.
+// Sums the per-run partials of k1_bwd_mfma<NTB, true, ...> in run order and
+// writes grad_W (32, nC) bf16.  Partial element
+// i = (((slice * 8 + m) * 2 + h) * 4 + r) * 64 + lane stands for
+// d = 16 h + (lane & 15), k = 128 slice + 8 (4 (lane >> 4) + r) + m; each
+// thread sums four consecutive elements (16-byte loads, four parts per trip).
 __global__ __launch_bounds__(256) void k1_dw_reduce(const float* __restrict__ partial,
-                                                    uint16_t* __restrict__ dW, int64_t nruns,
+                                                    uint16_t* __restrict__ dW, int64_t nparts,
                                                     int nslices, int nC) {
-  const int64_t per_run = static_cast<int64_t>(nslices) * (8 * 2 * 4 * kWave);
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (i >= per_run) return;
-  float acc = 0.f;
-  for (int64_t r = 0; r < nruns; ++r) acc += partial[r * per_run + i];
-  const int lane = static_cast<int>(i % kWave);
-  const int rr = static_cast<int>((i / kWave) % 4);
-  const int h = static_cast<int>((i / (4 * kWave)) % 2);
-  const int m = static_cast<int>((i / (8 * kWave)) % 8);
-  const int slice = static_cast<int>(i / (64 * kWave));
-  const int d = 16 * h + (lane & 15);
-  const int k = 128 * slice + 8 * (4 * (lane >> 4) + rr) + m;
-  if (k < nC) dW[static_cast<int64_t>(d) * nC + k] = f32_to_bf16(acc);
+  const int64_t per_part = static_cast<int64_t>(nslices) * (8 * 2 * 4 * kWave);
+  const int64_t i0 = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
+  if (i0 >= per_part) return;
+  const f32x4* src = reinterpret_cast<const f32x4*>(partial + i0);
+  const int64_t stride = per_part / 4;  // in 16-byte vectors
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  int64_t p = 0;
+  for (; p + 4 <= nparts; p += 4) {
+    const f32x4 v0 = src[(p + 0) * stride], v1 = src[(p + 1) * stride];
+    const f32x4 v2 = src[(p + 2) * stride], v3 = src[(p + 3) * stride];
+    acc += v0;
+    acc += v1;
+    acc += v2;
+    acc += v3;
+  }
+  for (; p < nparts; ++p) acc += src[p * stride];
+  const int lane0 = static_cast<int>(i0 % kWave);  // multiple of 4
+  const int rr = static_cast<int>((i0 / kWave) % 4);
+  const int h = static_cast<int>((i0 / (4 * kWave)) % 2);
+  const int m = static_cast<int>((i0 / (8 * kWave)) % 8);
+  const int slice = static_cast<int>(i0 / (64 * kWave));
+  const int k = 128 * slice + 8 * (4 * (lane0 >> 4) + rr) + m;
+  if (k >= nC) return;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int d = 16 * h + ((lane0 + e) & 15);
+    dW[static_cast<int64_t>(d) * nC + k] = f32_to_bf16(acc[e]);
+  }
 }
 
 // grad_W of an empty batch (a kernel, not a memset, so the call can be captured
@@ -527,6 +559,23 @@ bool bad_sizes(int64_t T, int64_t nC, int64_t D_out) {
   return T < 0 || nC <= 0 || nC > (int64_t{1} << 30) || D_out != kDout;
 }
 
+// The backward MFMA kernel addresses 16 rows of x with 32-bit byte offsets.
+bool k1_bwd_mfma_path(const void* x, const void* W, const void* go, const void* proj, const void* gx,
+                      int64_t nC) {
+  return nC % 8 == 0 && nC <= (int64_t{1} << 26) && aligned16(x) && aligned16(W) && aligned16(go) &&
+         aligned16(proj) && aligned16(gx);
+}
+
+template <int NTB, bool DW>
+void launch_k1_bwd_mfma(dim3 grid, hipStream_t s, const uint16_t* x, const uint16_t* W,
+                        const uint16_t* go, const uint16_t* proj, const float* inv_rms, uint16_t* gx,
+                        float* partial, int64_t T, int nC, int nslices) {
+  if (nC % 128 == 0)
+    k1_bwd_mfma<NTB, DW, true><<<grid, 256, 0, s>>>(x, W, go, proj, inv_rms, gx, partial, T, nC, nslices);
+  else
+    k1_bwd_mfma<NTB, DW, false><<<grid, 256, 0, s>>>(x, W, go, proj, inv_rms, gx, partial, T, nC, nslices);
+}
+
 }  // namespace
 }  // namespace fmhc
 
@@ -558,13 +607,11 @@ extern "C" int fmhc_k1_bwd_dx(const uint16_t* x_flat, const uint16_t* W, const u
     return FMHC_ERR_INVALID_ARGUMENT;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int nc = static_cast<int>(nC);
-  if (nC % 8 == 0 && aligned16(x_flat) && aligned16(W) && aligned16(grad_out) &&
-      aligned16(proj_out) && aligned16(grad_x)) {
+  if (k1_bwd_mfma_path(x_flat, W, grad_out, proj_out, grad_x, nC)) {
     const int nslices = static_cast<int>((nC + 127) / 128);
     const int64_t nruns = (T + 16 * kBwdNTB - 1) / (16 * kBwdNTB);
-    const dim3 grid(blocks_for(nruns * nslices, 4));
-    k1_bwd_mfma<kBwdNTB, false><<<grid, 256, 0, s>>>(x_flat, W, grad_out, proj_out, inv_rms, grad_x,
-                                                     nullptr, T, nc, nslices);
+    launch_k1_bwd_mfma<kBwdNTB, false>(dim3(blocks_for(nruns * nslices, 4)), s, x_flat, W, grad_out,
+                                       proj_out, inv_rms, grad_x, nullptr, T, nc, nslices);
   } else {
     const dim3 grid(blocks_for(T, 4));
     k1_bwd_scalar<<<grid, 256, 0, s>>>(x_flat, W, grad_out, proj_out, inv_rms, grad_x, T, nc);
@@ -574,18 +621,13 @@ extern "C" int fmhc_k1_bwd_dx(const uint16_t* x_flat, const uint16_t* W, const u
 
 namespace fmhc {
 namespace {
-bool k1_bwd_fused_path(const void* x, const void* W, const void* go, const void* proj, const void* gx,
-                       int64_t nC) {
-  return nC % 8 == 0 && aligned16(x) && aligned16(W) && aligned16(go) && aligned16(proj) &&
-         aligned16(gx);
-}
-int64_t k1_bwd_runs(int64_t T) { return (T + 16 * kBwdDwNTB - 1) / (16 * kBwdDwNTB); }
+int64_t k1_bwd_runs(int64_t T) { return ((T + 15) / 16 + kBwdDwNTB - 1) / kBwdDwNTB; }
 }  // namespace
 }  // namespace fmhc
 
 extern "C" int64_t fmhc_k1_bwd_workspace_bytes(int64_t T, int64_t nC) {
   using namespace fmhc;
-  if (T <= 0 || nC <= 0 || nC % 8 != 0) return 0;
+  if (T <= 0 || nC <= 0 || nC % 8 != 0 || nC > (int64_t{1} << 26)) return 0;  // no MFMA path: no workspace
   const int64_t nslices = (nC + 127) / 128;
   return k1_bwd_runs(T) * nslices * (8 * 2 * 4 * kWave) * static_cast<int64_t>(sizeof(float));
 }
@@ -604,18 +646,18 @@ extern "C" int fmhc_k1_bwd(const uint16_t* x_flat, const uint16_t* W, const uint
     return launch_status();
   }
   if (!x_flat || !W || !grad_out || !proj_out || !inv_rms || !grad_x) return FMHC_ERR_INVALID_ARGUMENT;
-  if (k1_bwd_fused_path(x_flat, W, grad_out, proj_out, grad_x, nC)) {
+  if (k1_bwd_mfma_path(x_flat, W, grad_out, proj_out, grad_x, nC)) {
     const int64_t need = fmhc_k1_bwd_workspace_bytes(T, nC);
     if (!workspace || workspace_bytes < need || !aligned16(workspace)) return FMHC_ERR_INVALID_ARGUMENT;
     const int nslices = static_cast<int>((nC + 127) / 128);
     const int64_t nruns = k1_bwd_runs(T);
     float* partial = static_cast<float*>(workspace);
-    k1_bwd_mfma<kBwdDwNTB, true><<<dim3(blocks_for(nruns * nslices, 4)), 256, 0, s>>>(
-        x_flat, W, grad_out, proj_out, inv_rms, grad_x, partial, T, nc, nslices);
+    launch_k1_bwd_mfma<kBwdDwNTB, true>(dim3(blocks_for(nruns * nslices, 4)), s, x_flat, W, grad_out,
+                                        proj_out, inv_rms, grad_x, partial, T, nc, nslices);
     const int st = launch_status();
     if (st != FMHC_OK) return st;
-    const int64_t per_run = static_cast<int64_t>(nslices) * (8 * 2 * 4 * kWave);
-    k1_dw_reduce<<<dim3(blocks_for(per_run, 256)), 256, 0, s>>>(partial, grad_W, nruns, nslices, nc);
+    const int64_t per_part = static_cast<int64_t>(nslices) * (8 * 2 * 4 * kWave);
+    k1_dw_reduce<<<dim3(blocks_for(per_part / 4, 256)), 256, 0, s>>>(partial, grad_W, nruns, nslices, nc);
     return launch_status();
   }
   const int st = fmhc_k1_bwd_dx(x_flat, W, grad_out, proj_out, inv_rms, grad_x, T, nC, D_out, stream);

@@ -44,6 +44,12 @@ COMMON_FLAGS = [
     "-packed-fp32-ops",
 ]
 
+# Per-source flags.  k1.hip: let the MFMA accumulators live in ordinary VGPRs
+# (gfx950 allows VGPR srcC/dst).  Without it the compiler keeps the backward's
+# loop-carried weight-gradient accumulators in VGPRs and copies them to and
+# from AGPRs around every MFMA, which doubles the kernel's register footprint.
+SOURCE_FLAGS = {"k1.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
 
 def hipcc() -> str:
     exe = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
@@ -78,7 +84,7 @@ def build(verbose: bool = False, extra_flags: list[str] | None = None, out: Path
 
     def compile_one(src: str) -> Path:
         obj = BUILD_DIR / (Path(src).stem + ".o")
-        _run([cc, *flags, "-c", str(CSRC / src), "-o", str(obj)], verbose)
+        _run([cc, *flags, *SOURCE_FLAGS.get(src, []), "-c", str(CSRC / src), "-o", str(obj)], verbose)
         return obj
 
     jobs = min(len(SOURCES), max(1, (os.cpu_count() or 1)))

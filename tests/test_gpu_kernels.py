@@ -117,10 +117,13 @@ def test_k1_bwd_dx_misaligned():
     check_bf16("k1 grad_x (misaligned)", gx, R, S, 64)
 
 
-@pytest.mark.parametrize("T,C", [(2048, 256), (257, 1024), (1, 4096), (1500, 1024), (333, 100), (31, 24), (17, 25)])
+@pytest.mark.parametrize(
+    "T,C", [(2048, 256), (257, 1024), (1, 4096), (1500, 1024), (20000, 256), (333, 100), (31, 24), (17, 25)]
+)
 def test_k1_bwd_fused_dw(T, C):
     """grad_x and grad_W in one pass: grad_x as the dx kernel, grad_W against
-    the oracle's bf16(bf16(go * inv_rms)^T @ x) with n = T terms."""
+    the oracle's bf16(bf16(go * inv_rms)^T @ x) with n = T terms.  T = 20000
+    spans several workgroups along T, the last one with idle waves."""
     x, W = _k1_inputs(T, C, seed=200 + T + C, stress=True)
     go = randn((T, 32), seed=201 + T)
     xd, Wd = x.to(DEV), W.to(DEV)
