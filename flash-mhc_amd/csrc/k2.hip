@@ -1,0 +1,337 @@
+// K2: the mHC-lite coefficient math of the fused path (block.py:161-170 of
+// alint77/flash-mHC), forward and backward, one thread per token.
+//
+// The reference evaluates K2 as a chain of PyTorch ops on bf16 tensors: every
+// op computes in fp32 from bf16 inputs and rounds its output to bf16 (RNE), and
+// autograd does the same for each backward op.  These kernels run the same
+// chain with the same rounding points (rb() below wherever the reference
+// produces a bf16 tensor) and the same fp32 operation order, with
+// floating-point contraction off so that no two roundings merge into an FMA.
+// Per token (p = proj row (32,), a_* = bf16(alpha_*), b = bf16(bias)):
+//   h_pre  = rb(sigmoid(rb(rb(a_pre  * p[0:4])  + b[0:4])))
+//   h_post = rb(2 * rb(sigmoid(rb(rb(a_post * p[4:8])  + b[4:8]))))
+//   a      = rb(softmax(rb(rb(a_res  * p[8:32]) + b[8:32])))
+//   H_res  = rb(a @ perm),  H_merged = rb(H_res - rb(h_post (x) h_pre))
+// The outputs are the fp32 casts the fused path hands to K3 / K4
+// (block.py:176-177).  The backward follows PyTorch's GPU kernels, whose bf16
+// sigmoid and softmax backward round intermediate products as well.  The backward also produces per-block partial sums of
+// the alpha and bias gradients (sums over tokens), which k2_param_reduce adds
+// in a fixed order.
+
+#include <hip/hip_runtime.h>
+
+#include "flash_mhc_hip.h"
+#include "fmhc_common.h"
+
+namespace fmhc {
+namespace {
+
+constexpr int kN = 4;
+constexpr int kNF = 24;             // n! for n = 4
+constexpr int kDk = 2 * kN + kNF;   // 32 projection columns
+constexpr int kNPar = 3 + kDk;      // alpha_pre, alpha_post, alpha_res, bias[32]
+constexpr int kK2Threads = 256;
+
+__device__ __forceinline__ float rb(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+
+// perm (24 x 16) rounded to bf16 (the reference multiplies by perm_mat.to(bf16)),
+// staged in LDS once per block; every lane then reads the same rows (broadcast).
+__device__ __forceinline__ void stage_perm(const float* __restrict__ perm, f32x4 sperm[kNF * 4]) {
+  float* s = reinterpret_cast<float*>(sperm);
+  for (int i = threadIdx.x; i < kNF * kN * kN; i += kK2Threads) s[i] = rb(perm[i]);
+  __syncthreads();
+}
+
+__device__ __forceinline__ float sigmoid_f32(float z) {
+#pragma clang fp contract(off)
+  const float d = 1.f + expf(-z);
+  return 1.f / d;
+}
+
+template <bool VEC>
+__device__ __forceinline__ void load_proj(const uint16_t* __restrict__ row, float p[kDk]) {
+  if constexpr (VEC) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) unpack8(reinterpret_cast<const u32x4*>(row)[i], p + 8 * i);
+  } else {
+#pragma unroll
+    for (int i = 0; i < kDk; ++i) p[i] = bf16_to_f32(row[i]);
+  }
+}
+
+// Forward chain of one token.  Fills the values the backward reuses.
+struct K2Fwd {
+  float hp[kN], hq[kN], sq[kN];  // h_pre, h_post, sigmoid of the post logits
+  float a[kNF];                  // softmax weights
+};
+
+__device__ __forceinline__ void k2_chain(const float p[kDk], float ap, float apo, float ar,
+                                         const float* __restrict__ bias, K2Fwd& f) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int j = 0; j < kN; ++j) {
+    const float z = rb(rb(ap * p[j]) + rb(bias[j]));
+    f.hp[j] = rb(sigmoid_f32(z));
+  }
+#pragma unroll
+  for (int j = 0; j < kN; ++j) {
+    const float z = rb(rb(apo * p[kN + j]) + rb(bias[kN + j]));
+    f.sq[j] = rb(sigmoid_f32(z));
+    f.hq[j] = rb(2.f * f.sq[j]);
+  }
+  float z[kNF];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int m = 0; m < kNF; ++m) {
+    z[m] = rb(rb(ar * p[2 * kN + m]) + rb(bias[2 * kN + m]));
+    mx = fmaxf(mx, z[m]);
+  }
+  float sum = 0.f;
+#pragma unroll
+  for (int m = 0; m < kNF; ++m) {
+    z[m] = expf(z[m] - mx);
+    sum = sum + z[m];
+  }
+#pragma unroll
+  for (int m = 0; m < kNF; ++m) f.a[m] = rb(z[m] / sum);
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(kK2Threads) void k2_fwd_kernel(
+    const uint16_t* __restrict__ proj, const float* __restrict__ alpha_pre,
+    const float* __restrict__ alpha_post, const float* __restrict__ alpha_res,
+    const float* __restrict__ bias, const float* __restrict__ perm, float* __restrict__ h_pre,
+    float* __restrict__ h_post, float* __restrict__ H, int64_t T) {
+#pragma clang fp contract(off)
+  __shared__ f32x4 sperm[kNF * 4];
+  stage_perm(perm, sperm);
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * kK2Threads + threadIdx.x;
+  if (t >= T) return;
+  float p[kDk];
+  load_proj<VEC>(proj + t * kDk, p);
+  K2Fwd f;
+  k2_chain(p, rb(alpha_pre[0]), rb(alpha_post[0]), rb(alpha_res[0]), bias, f);
+  f32x4 hp = {f.hp[0], f.hp[1], f.hp[2], f.hp[3]};
+  f32x4 hq = {f.hq[0], f.hq[1], f.hq[2], f.hq[3]};
+  reinterpret_cast<f32x4*>(h_pre)[t] = hp;
+  reinterpret_cast<f32x4*>(h_post)[t] = hq;
+  // H_res[ij] = sum over m in order of a[m] perm[m, ij] (m outer: one LDS row per step).
+  float acc[kN * kN];
+#pragma unroll
+  for (int ij = 0; ij < kN * kN; ++ij) acc[ij] = 0.f;
+#pragma unroll
+  for (int m = 0; m < kNF; ++m)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const f32x4 pm = sperm[m * 4 + q];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[4 * q + e] = acc[4 * q + e] + f.a[m] * pm[e];
+    }
+#pragma unroll
+  for (int i = 0; i < kN; ++i) {
+    f32x4 row;
+#pragma unroll
+    for (int j = 0; j < kN; ++j) row[j] = rb(rb(acc[i * kN + j]) - rb(f.hq[i] * f.hp[j]));
+    reinterpret_cast<f32x4*>(H)[t * kN + i] = row;
+  }
+}
+
+// Backward of one token (autograd's rounding points on the GPU; gradients of
+// the fp32 outputs are first rounded to bf16, as the .float() casts' backward
+// does).
+// Writes grad_proj and accumulates this token's terms of the 35 parameter
+// gradients into par[]: sum_j rb(gz_pre p_pre), sum_j rb(gz_post p_post),
+// sum_m rb(gz_res p_res), and the 32 logit gradients (the bias terms).
+template <bool VEC>
+__global__ __launch_bounds__(kK2Threads) void k2_bwd_kernel(
+    const uint16_t* __restrict__ proj, const float* __restrict__ alpha_pre,
+    const float* __restrict__ alpha_post, const float* __restrict__ alpha_res,
+    const float* __restrict__ bias, const float* __restrict__ perm,
+    const float* __restrict__ g_hpre, const float* __restrict__ g_hpost,
+    const float* __restrict__ g_H, uint16_t* __restrict__ grad_proj,
+    float* __restrict__ partial, int64_t T) {
+#pragma clang fp contract(off)
+  __shared__ f32x4 sperm[kNF * 4];
+  stage_perm(perm, sperm);
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * kK2Threads + threadIdx.x;
+  float par[kNPar];
+#pragma unroll
+  for (int k = 0; k < kNPar; ++k) par[k] = 0.f;
+
+  if (t < T) {
+    float p[kDk];
+    load_proj<VEC>(proj + t * kDk, p);
+    const float ap = rb(alpha_pre[0]), apo = rb(alpha_post[0]), ar = rb(alpha_res[0]);
+    K2Fwd f;
+    k2_chain(p, ap, apo, ar, bias, f);
+
+    float gH[kN * kN], ghp[kN], ghq[kN];
+#pragma unroll
+    for (int ij = 0; ij < kN * kN; ++ij) gH[ij] = g_H ? rb(g_H[t * kN * kN + ij]) : 0.f;
+    // H_merged = H_res - outer(h_post, h_pre): the outer product's gradient
+    // is -gH; its two factors get the sums over the other index.
+#pragma unroll
+    for (int i = 0; i < kN; ++i) {
+      float s = 0.f;
+#pragma unroll
+      for (int j = 0; j < kN; ++j) s = s + rb(-gH[i * kN + j] * f.hp[j]);
+      ghq[i] = rb((g_hpost ? rb(g_hpost[t * kN + i]) : 0.f) + rb(s));
+    }
+#pragma unroll
+    for (int j = 0; j < kN; ++j) {
+      float s = 0.f;
+#pragma unroll
+      for (int i = 0; i < kN; ++i) s = s + rb(-gH[i * kN + j] * f.hq[i]);
+      ghp[j] = rb((g_hpre ? rb(g_hpre[t * kN + j]) : 0.f) + rb(s));
+    }
+    // H_res = a @ perm, then the softmax backward as PyTorch's GPU kernel
+    // rounds it for bf16: gy = rb(g a), gz = rb(gy - a sum(gy)).
+    float gy[kNF];
+    float s = 0.f;
+#pragma unroll
+    for (int m = 0; m < kNF; ++m) {
+      float acc = 0.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 pm = sperm[m * 4 + q];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc = acc + gH[4 * q + e] * pm[e];
+      }
+      gy[m] = rb(rb(acc) * f.a[m]);
+      s = s + gy[m];
+    }
+    float gz[kDk];
+#pragma unroll
+    for (int m = 0; m < kNF; ++m) gz[2 * kN + m] = rb(gy[m] - f.a[m] * s);
+    // Sigmoid backward, grad (1 - y) y with every step rounded to bf16 as
+    // PyTorch's GPU kernel does for bf16; h_post = 2 sigmoid gives the factor 2 first.
+#pragma unroll
+    for (int j = 0; j < kN; ++j) {
+      gz[j] = rb(rb(ghp[j] * rb(1.f - f.hp[j])) * f.hp[j]);
+      const float gs = rb(ghq[j] * 2.f);
+      gz[kN + j] = rb(rb(gs * rb(1.f - f.sq[j])) * f.sq[j]);
+    }
+    float gp[kDk];
+#pragma unroll
+    for (int k = 0; k < kDk; ++k) {
+      const float a = k < kN ? ap : (k < 2 * kN ? apo : ar);
+      gp[k] = rb(gz[k] * a);
+      par[k < kN ? 0 : (k < 2 * kN ? 1 : 2)] += rb(gz[k] * p[k]);
+      par[3 + k] = gz[k];
+    }
+    uint16_t* row = grad_proj + t * kDk;
+    if constexpr (VEC) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) reinterpret_cast<u32x4*>(row)[i] = pack8(gp + 8 * i);
+    } else {
+#pragma unroll
+      for (int k = 0; k < kDk; ++k) row[k] = f32_to_bf16(gp[k]);
+    }
+  }
+
+  // Block partial sums: in-wave butterfly, then the four waves in order.
+  __shared__ float red[kK2Threads / kWave][kNPar];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+#pragma unroll
+  for (int k = 0; k < kNPar; ++k) {
+    float v = par[k];
+#pragma unroll
+    for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    if (lane == 0) red[wave][k] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x < kNPar) {
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < kK2Threads / kWave; ++w) v += red[w][threadIdx.x];
+    partial[static_cast<int64_t>(blockIdx.x) * kNPar + threadIdx.x] = v;
+  }
+}
+
+// One wave per parameter gradient: lanes take blocks lane, lane + 64, ...,
+// then a butterfly; the result is rounded to bf16 (the reference sums a bf16
+// tensor) and stored as the fp32 parameter's gradient.
+__global__ __launch_bounds__(kWave) void k2_param_reduce(const float* __restrict__ partial,
+                                                         int64_t nblocks, float* __restrict__ g_ap,
+                                                         float* __restrict__ g_apo,
+                                                         float* __restrict__ g_ar,
+                                                         float* __restrict__ g_bias) {
+  const int k = blockIdx.x;  // 0 .. kNPar - 1
+  float v = 0.f;
+  for (int64_t b = threadIdx.x; b < nblocks; b += kWave) v += partial[b * kNPar + k];
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  if (threadIdx.x == 0) {
+    float* dst = k == 0 ? g_ap : (k == 1 ? g_apo : (k == 2 ? g_ar : g_bias + (k - 3)));
+    *dst = rb(v);
+  }
+}
+
+bool k2_bad(int64_t T, int64_t n) { return T < 0 || n != kN; }
+int64_t k2_blocks(int64_t T) { return (T + kK2Threads - 1) / kK2Threads; }
+
+}  // namespace
+}  // namespace fmhc
+
+extern "C" int fmhc_k2_fwd(const uint16_t* proj, const float* alpha_pre, const float* alpha_post,
+                           const float* alpha_res, const float* bias, const float* perm,
+                           float* h_pre, float* h_post, float* H_merged, int64_t T, int64_t n,
+                           void* stream) {
+  using namespace fmhc;
+  if (k2_bad(T, n)) return FMHC_ERR_INVALID_ARGUMENT;
+  if (T == 0) return FMHC_OK;
+  if (!proj || !alpha_pre || !alpha_post || !alpha_res || !bias || !perm || !h_pre || !h_post || !H_merged)
+    return FMHC_ERR_INVALID_ARGUMENT;
+  if (!aligned16(h_pre) || !aligned16(h_post) || !aligned16(H_merged)) return FMHC_ERR_INVALID_ARGUMENT;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<unsigned>(k2_blocks(T)));
+  if (aligned16(proj))
+    k2_fwd_kernel<true><<<grid, kK2Threads, 0, s>>>(proj, alpha_pre, alpha_post, alpha_res, bias, perm,
+                                                    h_pre, h_post, H_merged, T);
+  else
+    k2_fwd_kernel<false><<<grid, kK2Threads, 0, s>>>(proj, alpha_pre, alpha_post, alpha_res, bias, perm,
+                                                     h_pre, h_post, H_merged, T);
+  return launch_status();
+}
+
+extern "C" int64_t fmhc_k2_bwd_workspace_bytes(int64_t T) {
+  using namespace fmhc;
+  if (T <= 0) return 0;
+  return k2_blocks(T) * kNPar * static_cast<int64_t>(sizeof(float));
+}
+
+extern "C" int fmhc_k2_bwd(const uint16_t* proj, const float* alpha_pre, const float* alpha_post,
+                           const float* alpha_res, const float* bias, const float* perm,
+                           const float* grad_h_pre, const float* grad_h_post,
+                           const float* grad_H_merged, uint16_t* grad_proj, float* grad_alpha_pre,
+                           float* grad_alpha_post, float* grad_alpha_res, float* grad_bias,
+                           void* workspace, int64_t workspace_bytes, int64_t T, int64_t n,
+                           void* stream) {
+  using namespace fmhc;
+  if (k2_bad(T, n)) return FMHC_ERR_INVALID_ARGUMENT;
+  if (!grad_alpha_pre || !grad_alpha_post || !grad_alpha_res || !grad_bias) return FMHC_ERR_INVALID_ARGUMENT;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t nblocks = k2_blocks(T);
+  float* partial = static_cast<float*>(workspace);
+  if (T > 0) {
+    if (!proj || !alpha_pre || !alpha_post || !alpha_res || !bias || !perm || !grad_proj)
+      return FMHC_ERR_INVALID_ARGUMENT;
+    if (!workspace || workspace_bytes < fmhc_k2_bwd_workspace_bytes(T)) return FMHC_ERR_INVALID_ARGUMENT;
+    const dim3 grid(static_cast<unsigned>(nblocks));
+    if (aligned16(proj) && aligned16(grad_proj))
+      k2_bwd_kernel<true><<<grid, kK2Threads, 0, s>>>(proj, alpha_pre, alpha_post, alpha_res, bias, perm,
+                                                      grad_h_pre, grad_h_post, grad_H_merged, grad_proj,
+                                                      partial, T);
+    else
+      k2_bwd_kernel<false><<<grid, kK2Threads, 0, s>>>(proj, alpha_pre, alpha_post, alpha_res, bias, perm,
+                                                       grad_h_pre, grad_h_post, grad_H_merged, grad_proj,
+                                                       partial, T);
+    const int st = launch_status();
+    if (st != FMHC_OK) return st;
+  }
+  // T == 0: the reduce writes zero gradients (nblocks = 0 partials).
+  k2_param_reduce<<<dim3(kNPar), kWave, 0, s>>>(partial, T > 0 ? nblocks : 0, grad_alpha_pre,
+                                                grad_alpha_post, grad_alpha_res, grad_bias);
+  return launch_status();
+}

@@ -29,6 +29,9 @@ SIGNATURES: dict[str, list] = {
     "fmhc_k1_bwd_dx": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
     "fmhc_k1_bwd": [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
     "fmhc_k1_bwd_workspace_bytes": [_I64, _I64],
+    "fmhc_k2_fwd": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _P],
+    "fmhc_k2_bwd": [_P] * 15 + [_I64, _I64, _I64, _P],
+    "fmhc_k2_bwd_workspace_bytes": [_I64],
     "fmhc_k3_fwd": [_P, _P, _P, _I64, _I64, _I64, _P],
     "fmhc_k3_bwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
     "fmhc_k4_fwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
@@ -37,9 +40,13 @@ SIGNATURES: dict[str, list] = {
     "fmhc_stream_probe": [ctypes.c_int, _P, _P, _I64, _P],
     "fmhc_abi_version": [],
 }
-RESTYPES = {"fmhc_error_string": ctypes.c_char_p, "fmhc_k1_bwd_workspace_bytes": ctypes.c_int64}
+RESTYPES = {
+    "fmhc_error_string": ctypes.c_char_p,
+    "fmhc_k1_bwd_workspace_bytes": ctypes.c_int64,
+    "fmhc_k2_bwd_workspace_bytes": ctypes.c_int64,
+}
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

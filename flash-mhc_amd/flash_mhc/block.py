@@ -12,7 +12,8 @@ Per layer, with x of shape (T, n, C):
   K1  proj, inv_rms = rmsnorm-project(x.reshape(T, nC), W_all.weight)   HIP kernel
   K2  h_pre = sigmoid(a_pre * proj[:, :n] + b), h_post = 2 sigmoid(...),
       H_res = softmax(a_res * proj[:, 2n:] + b) @ perm, H_merged = H_res - h_post h_pre^T
-                                                                         PyTorch ops
+                                                 HIP kernel (the reference's bf16 ops
+                                                 with FLASH_MHC_FUSED_K2=0)
   K3  layer_input = sum_j h_pre[:, j] x[:, j]                             HIP kernel
       layer_output = layer(layer_input)                                  user module
   K4  out = H_merged @ x + h_post (x) layer_output                       HIP kernel
@@ -159,7 +160,8 @@ class MHCLiteBlock(nn.Module):
 
     # -- fused HIP path (block.py:150-219) ------------------------------------
 
-    def _mhc_coeffs_triton(self, x_streams: torch.Tensor):
+    def _project_triton(self, x_streams: torch.Tensor) -> torch.Tensor:
+        """K1: the (T, 2n + n!) projection of the RMS-normalised streams."""
         dt = x_streams.dtype
         T = x_streams.shape[0]
         if self.rms_weight is None:
@@ -169,9 +171,21 @@ class MHCLiteBlock(nn.Module):
         proj, _inv_rms = torch.ops.flash_mhc.fused_rmsnorm_project(
             x_streams.reshape(T, self.nC), W
         )
-        return self._coefficients(proj, dt)
+        return proj
+
+    def _mhc_coeffs_triton(self, x_streams: torch.Tensor):
+        """K1 + K2 as the reference's PyTorch ops: bf16 (h_pre, h_post, H_merged)."""
+        return self._coefficients(self._project_triton(x_streams), x_streams.dtype)
 
     def _mhc_pre_map_triton(self, x_streams: torch.Tensor):
+        if _ops.fused_k2_enabled():
+            # One kernel for K2, same values as the ops below (fp32 outputs).
+            h_pre, h_post, H_merged = torch.ops.flash_mhc.mhc_coefficients(
+                self._project_triton(x_streams), self.alpha_pre, self.alpha_post,
+                self.alpha_res, self.W_all.bias, self.perm_mat,
+            )
+            layer_input = torch.ops.flash_mhc.fused_pre_map(x_streams, h_pre)
+            return layer_input, H_merged, h_post
         h_pre, h_post, H_merged = self._mhc_coeffs_triton(x_streams)
         layer_input = torch.ops.flash_mhc.fused_pre_map(x_streams, h_pre.float())
         return layer_input, H_merged.float(), h_post.float()
@@ -180,7 +194,7 @@ class MHCLiteBlock(nn.Module):
         return torch.ops.flash_mhc.fused_post_res(x_streams, layer_output, H_merged, h_post)
 
     def _forward_triton(self, x_streams: torch.Tensor, **kwargs) -> torch.Tensor:
-        """Fused path: K1/K3/K4 on the HIP kernels (K2 in PyTorch)."""
+        """Fused path: K1/K2/K3/K4 on the HIP kernels."""
         ctx = nullcontext() if self.training else _ops.disable_autotune_temporarily()
         return self._run(x_streams, self._mhc_pre_map_triton, self._mhc_post_res_triton, ctx, kwargs)
 

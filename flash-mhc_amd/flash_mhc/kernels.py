@@ -10,6 +10,8 @@ Reference counterparts (alint77/flash-mHC):
   k1_fwd     <- src/flash_mhc/kernels.py:250-303  _fused_rmsnorm_project_fwd_kernel
   k1_bwd_dx  <- src/flash_mhc/kernels.py:306-376  _fused_rmsnorm_project_bwd_dx_kernel
   k1_bwd     <- the above plus the grad_W matmul of src/flash_mhc/ops.py:683-684, fused
+  k2_fwd     <- src/flash_mhc/block.py:161-170 (PyTorch ops) and the .float() casts of :176-177
+  k2_bwd     <- autograd through the same ops
   k3_fwd     <- src/flash_mhc/kernels.py:673-717  _fused_pre_map_fwd_kernel
   k3_bwd     <- src/flash_mhc/kernels.py:720-853  _fused_pre_map_bwd_fused_kernel_n4
   k4_fwd     <- src/flash_mhc/kernels.py:384-481  _fused_post_res_fwd_kernel_n4
@@ -150,6 +152,77 @@ def k1_bwd(grad_out: torch.Tensor, x_flat: torch.Tensor, W: torch.Tensor,
                              ws.numel(), T, nC, D_OUT, _abi.stream_of(x_flat))
     _abi.check(st, "k1_bwd")
     return grad_x, grad_W
+
+
+N_PERM = 24  # n! at n = 4
+
+
+def _k2_params(alpha_pre, alpha_post, alpha_res, bias, perm, dev):
+    for t, name, shape in ((alpha_pre, "alpha_pre", (1,)), (alpha_post, "alpha_post", (1,)),
+                           (alpha_res, "alpha_res", (1,)), (bias, "bias", (D_OUT,)),
+                           (perm, "perm", (N_PERM, N_STREAMS * N_STREAMS))):
+        _require(t, name, _F32, shape, dev)
+
+
+def k2_fwd(proj: torch.Tensor, alpha_pre: torch.Tensor, alpha_post: torch.Tensor,
+           alpha_res: torch.Tensor, bias: torch.Tensor, perm: torch.Tensor
+           ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(h_pre (T,4), h_post (T,4), H_merged (T,4,4)) fp32 from proj (T,32) bf16,
+    with the bf16 rounding points of the reference's coefficient ops.
+    Parameters are fp32 tensors: alphas (1,), bias (32,), perm (24,16)."""
+    dev = _device_of(proj)
+    if proj.dim() != 2:
+        raise ValueError(f"proj must be 2-D (T, 32), got shape {tuple(proj.shape)}")
+    T = proj.shape[0]
+    _require(proj, "proj", _BF16, (T, D_OUT), dev)
+    _k2_params(alpha_pre, alpha_post, alpha_res, bias, perm, dev)
+    h_pre = torch.empty((T, N_STREAMS), device=dev, dtype=_F32)
+    h_post = torch.empty((T, N_STREAMS), device=dev, dtype=_F32)
+    H = torch.empty((T, N_STREAMS, N_STREAMS), device=dev, dtype=_F32)
+    lib = _abi.load()
+    with _OnDevice(dev):
+        st = lib.fmhc_k2_fwd(proj.data_ptr(), alpha_pre.data_ptr(), alpha_post.data_ptr(),
+                             alpha_res.data_ptr(), bias.data_ptr(), perm.data_ptr(), h_pre.data_ptr(),
+                             h_post.data_ptr(), H.data_ptr(), T, N_STREAMS, _abi.stream_of(proj))
+    _abi.check(st, "k2_fwd")
+    return h_pre, h_post, H
+
+
+def k2_bwd(proj: torch.Tensor, alpha_pre: torch.Tensor, alpha_post: torch.Tensor,
+           alpha_res: torch.Tensor, bias: torch.Tensor, perm: torch.Tensor,
+           grad_h_pre: torch.Tensor | None, grad_h_post: torch.Tensor | None,
+           grad_H: torch.Tensor | None):
+    """Gradients of k2_fwd: (grad_proj (T,32) bf16, grad_alpha_pre (1,),
+    grad_alpha_post (1,), grad_alpha_res (1,), grad_bias (32,)), fp32 parameter
+    gradients.  A None output gradient counts as zero."""
+    dev = _device_of(proj)
+    if proj.dim() != 2:
+        raise ValueError(f"proj must be 2-D (T, 32), got shape {tuple(proj.shape)}")
+    T = proj.shape[0]
+    _require(proj, "proj", _BF16, (T, D_OUT), dev)
+    _k2_params(alpha_pre, alpha_post, alpha_res, bias, perm, dev)
+    for t, name, shape in ((grad_h_pre, "grad_h_pre", (T, N_STREAMS)),
+                           (grad_h_post, "grad_h_post", (T, N_STREAMS)),
+                           (grad_H, "grad_H_merged", (T, N_STREAMS, N_STREAMS))):
+        if t is not None:
+            _require(t, name, _F32, shape, dev)
+    grad_proj = torch.empty((T, D_OUT), device=dev, dtype=_BF16)
+    g_ap = torch.empty((1,), device=dev, dtype=_F32)
+    g_apo = torch.empty((1,), device=dev, dtype=_F32)
+    g_ar = torch.empty((1,), device=dev, dtype=_F32)
+    g_b = torch.empty((D_OUT,), device=dev, dtype=_F32)
+    lib = _abi.load()
+    nbytes = int(lib.fmhc_k2_bwd_workspace_bytes(T))
+    ws = torch.empty((max(nbytes, 16),), device=dev, dtype=torch.uint8)
+    ptr = lambda t: None if t is None else t.data_ptr()
+    with _OnDevice(dev):
+        st = lib.fmhc_k2_bwd(proj.data_ptr(), alpha_pre.data_ptr(), alpha_post.data_ptr(),
+                             alpha_res.data_ptr(), bias.data_ptr(), perm.data_ptr(), ptr(grad_h_pre),
+                             ptr(grad_h_post), ptr(grad_H), grad_proj.data_ptr(), g_ap.data_ptr(),
+                             g_apo.data_ptr(), g_ar.data_ptr(), g_b.data_ptr(), ws.data_ptr(), ws.numel(),
+                             T, N_STREAMS, _abi.stream_of(proj))
+    _abi.check(st, "k2_bwd")
+    return grad_proj, g_ap, g_apo, g_ar, g_b
 
 
 def _streams_shape(x: torch.Tensor) -> tuple[int, int, int]:

@@ -15,9 +15,16 @@ Reference map:
   autograd (setup_context + backward)  ops.py:670-714
   disable_autotune_temporarily         ops.py:44-58
 
-Addition: fused_rmsnorm_project_bwd (grad_x and grad_W of K1 in one pass over
-x); the K1 autograd rule uses it unless FLASH_MHC_FUSED_DW=0, in which case it
-runs the reference's two-step rule (bwd_dx, then a matmul for grad_W).
+Additions (not in the reference):
+  fused_rmsnorm_project_bwd   grad_x and grad_W of K1 in one pass over x; the K1
+                              autograd rule uses it unless FLASH_MHC_FUSED_DW=0,
+                              which runs the reference's two-step rule (bwd_dx,
+                              then a matmul for grad_W).
+  mhc_coefficients (+ _backward)
+                              K2, the coefficient math of block.py:161-170 and
+                              the .float() casts of :176-177, as one kernel each
+                              way, with the reference's bf16 rounding points.
+                              MHCLiteBlock uses it unless FLASH_MHC_FUSED_K2=0.
 """
 
 from __future__ import annotations
@@ -44,6 +51,15 @@ _lib.define(
 # reference's autograd rule computes grad_W with a second matmul over x).
 _lib.define(
     "fused_rmsnorm_project_bwd(Tensor grad_out, Tensor x_flat, Tensor W, Tensor proj_out, Tensor inv_rms) -> (Tensor grad_x, Tensor grad_W)"
+)
+
+# Not in the reference: K2 as one op (block.py:161-170 of the reference is a
+# chain of ~15 PyTorch ops).  Outputs are the fp32 casts K3/K4 consume.
+_lib.define(
+    "mhc_coefficients(Tensor proj, Tensor alpha_pre, Tensor alpha_post, Tensor alpha_res, Tensor bias, Tensor perm_mat) -> (Tensor h_pre, Tensor h_post, Tensor H_merged)"
+)
+_lib.define(
+    "mhc_coefficients_backward(Tensor? grad_h_pre, Tensor? grad_h_post, Tensor? grad_H_merged, Tensor proj, Tensor alpha_pre, Tensor alpha_post, Tensor alpha_res, Tensor bias, Tensor perm_mat) -> (Tensor grad_proj, Tensor grad_alpha_pre, Tensor grad_alpha_post, Tensor grad_alpha_res, Tensor grad_bias)"
 )
 
 _lib.define("fused_pre_map(Tensor x_streams, Tensor h_pre) -> Tensor out")
@@ -102,6 +118,23 @@ def _fused_rmsnorm_project_bwd_dx_fake(grad_out, x_flat, W, proj_out, inv_rms):
 @torch.library.register_fake("flash_mhc::fused_rmsnorm_project_bwd")
 def _fused_rmsnorm_project_bwd_fake(grad_out, x_flat, W, proj_out, inv_rms):
     return torch.empty_like(x_flat), torch.empty_like(W, dtype=x_flat.dtype)
+
+
+@torch.library.register_fake("flash_mhc::mhc_coefficients")
+def _mhc_coefficients_fake(proj, alpha_pre, alpha_post, alpha_res, bias, perm_mat):
+    T = proj.shape[0]
+    n = int(round(perm_mat.shape[1] ** 0.5))
+    h_pre = proj.new_empty((T, n), dtype=torch.float32)
+    h_post = proj.new_empty((T, n), dtype=torch.float32)
+    H_merged = proj.new_empty((T, n, n), dtype=torch.float32)
+    return h_pre, h_post, H_merged
+
+
+@torch.library.register_fake("flash_mhc::mhc_coefficients_backward")
+def _mhc_coefficients_backward_fake(grad_h_pre, grad_h_post, grad_H_merged, proj, alpha_pre,
+                                    alpha_post, alpha_res, bias, perm_mat):
+    return (torch.empty_like(proj), torch.empty_like(alpha_pre), torch.empty_like(alpha_post),
+            torch.empty_like(alpha_res), torch.empty_like(bias))
 
 
 @torch.library.register_fake("flash_mhc::fused_pre_map")
@@ -165,6 +198,33 @@ def _fused_rmsnorm_project_bwd_cuda(grad_out, x_flat, W, proj_out, inv_rms):
                      proj_out.contiguous(), inv_rms.contiguous())
 
 
+def _check_k2(proj: torch.Tensor, perm_mat: torch.Tensor) -> None:
+    if proj.dim() != 2 or proj.shape[1] != 32 or tuple(perm_mat.shape) != (24, 16):
+        raise ValueError(
+            "flash_mhc::mhc_coefficients supports n=4 only: proj must be (T, 32) and "
+            f"perm_mat (24, 16), got {tuple(proj.shape)} and {tuple(perm_mat.shape)}"
+        )
+
+
+@torch.library.impl(_lib, "mhc_coefficients", "CUDA")
+def _mhc_coefficients_cuda(proj, alpha_pre, alpha_post, alpha_res, bias, perm_mat):
+    _check_k2(proj, perm_mat)
+    return _k.k2_fwd(proj.contiguous(), _coeff(alpha_pre), _coeff(alpha_post), _coeff(alpha_res),
+                     _coeff(bias), _coeff(perm_mat))
+
+
+@torch.library.impl(_lib, "mhc_coefficients_backward", "CUDA")
+def _mhc_coefficients_backward_cuda(grad_h_pre, grad_h_post, grad_H_merged, proj, alpha_pre,
+                                    alpha_post, alpha_res, bias, perm_mat):
+    _check_k2(proj, perm_mat)
+    g = [None if t is None else _coeff(t) for t in (grad_h_pre, grad_h_post, grad_H_merged)]
+    gp, ga1, ga2, ga3, gb = _k.k2_bwd(proj.contiguous(), _coeff(alpha_pre), _coeff(alpha_post),
+                                      _coeff(alpha_res), _coeff(bias), _coeff(perm_mat), *g)
+    # Parameter gradients in the parameters' dtype (exact: the values are bf16).
+    return (gp, ga1.to(alpha_pre.dtype), ga2.to(alpha_post.dtype), ga3.to(alpha_res.dtype),
+            gb.to(bias.dtype))
+
+
 @torch.library.impl(_lib, "fused_pre_map", "CUDA")
 def _fused_pre_map_cuda(x_streams: torch.Tensor, h_pre: torch.Tensor):
     _check_n4(x_streams, "flash_mhc::fused_pre_map currently supports n=4 only")
@@ -203,9 +263,17 @@ def _setup_k1(ctx, inputs, output):
     ctx.save_for_backward(x_flat, W, out, inv_rms)
 
 
+def _env_flag(name: str) -> bool:
+    return os.getenv(name, "1").strip().lower() not in {"0", "false", "off", "no"}
+
+
 def _fused_dw_enabled() -> bool:
-    v = os.getenv("FLASH_MHC_FUSED_DW", "1").strip().lower()
-    return v not in {"0", "false", "off", "no"}
+    return _env_flag("FLASH_MHC_FUSED_DW")
+
+
+def fused_k2_enabled() -> bool:
+    """MHCLiteBlock runs K2 as flash_mhc::mhc_coefficients unless FLASH_MHC_FUSED_K2=0."""
+    return _env_flag("FLASH_MHC_FUSED_K2")
 
 
 def _fused_rmsnorm_project_backward(ctx, grad_out, grad_inv_rms):
@@ -229,6 +297,15 @@ def _setup_inputs(ctx, inputs, output):
     ctx.save_for_backward(*inputs)
 
 
+def _mhc_coefficients_backward(ctx, grad_h_pre, grad_h_post, grad_H_merged):
+    # The backward recomputes the chain from proj (64 bytes per token).
+    proj, alpha_pre, alpha_post, alpha_res, bias, perm_mat = ctx.saved_tensors
+    grads = torch.ops.flash_mhc.mhc_coefficients_backward(
+        grad_h_pre, grad_h_post, grad_H_merged, proj, alpha_pre, alpha_post, alpha_res, bias, perm_mat
+    )
+    return (*grads, None)
+
+
 def _fused_pre_map_backward(ctx, grad_out):
     x_streams, h_pre = ctx.saved_tensors
     return torch.ops.flash_mhc.fused_pre_map_backward(grad_out, x_streams, h_pre)
@@ -245,6 +322,11 @@ torch.library.register_autograd(
     "flash_mhc::fused_rmsnorm_project",
     _fused_rmsnorm_project_backward,
     setup_context=_setup_k1,
+)
+torch.library.register_autograd(
+    "flash_mhc::mhc_coefficients",
+    _mhc_coefficients_backward,
+    setup_context=_setup_inputs,
 )
 torch.library.register_autograd(
     "flash_mhc::fused_pre_map",

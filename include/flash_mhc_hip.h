@@ -35,7 +35,7 @@ extern "C" {
 #define FMHC_ERR_INVALID_ARGUMENT 1 /* negative size, n != 4, D_out != 32, null pointer */
 #define FMHC_ERR_HIP_BASE 1000      /* + hipError_t from the launch */
 
-#define FMHC_ABI_VERSION 1
+#define FMHC_ABI_VERSION 2
 
 /* K1 forward: fused RMSNorm + projection.
  *   inv_rms[t] = rsqrt(sum_k x[t,k]^2 / nC + 1e-6)
@@ -73,6 +73,41 @@ int fmhc_k1_bwd(const uint16_t* x_flat, const uint16_t* W, const uint16_t* grad_
  * No counterpart in the reference. */
 int64_t fmhc_k1_bwd_workspace_bytes(int64_t T, int64_t nC);
 
+/* K2 forward, the coefficient math of the fused path with the reference's bf16
+ * rounding points (every intermediate rounded to bf16, as the reference's chain
+ * of bf16 tensor ops does), per token t:
+ *   h_pre[t,j]    = bf16(sigmoid(bf16(bf16(a_pre  * p[j])     + b[j])))
+ *   h_post[t,j]   = bf16(2 * bf16(sigmoid(bf16(bf16(a_post * p[4+j]) + b[4+j]))))
+ *   a[m]          = bf16(softmax_m(bf16(bf16(a_res * p[8+m]) + b[8+m])))
+ *   H_merged[t,i,j] = bf16(bf16(sum_m a[m] perm[m, 4i+j]) - bf16(h_post[t,i] h_pre[t,j]))
+ * with p = proj[t,:] (T, 32) bf16, a_* = bf16(alpha_*[0]), b = bf16(bias) (32,),
+ * perm (24, 16) fp32 (the block's perm_mat).  Outputs are fp32 (the values are
+ * bf16), 16-byte aligned: h_pre (T, 4), h_post (T, 4), H_merged (T, 4, 4).
+ * n must be 4.
+ * Replaces: src/flash_mhc/block.py:161-170 (_mhc_coeffs_triton's PyTorch ops)
+ *           and the .float() casts of block.py:176-177. */
+int fmhc_k2_fwd(const uint16_t* proj, const float* alpha_pre, const float* alpha_post,
+                const float* alpha_res, const float* bias, const float* perm,
+                float* h_pre, float* h_post, float* H_merged, int64_t T, int64_t n, void* stream);
+/* K2 backward: autograd of the chain above with the rounding points of
+ * PyTorch's GPU kernels (the incoming fp32 gradients are rounded to bf16 first,
+ * as the .float() casts' backward does; the sigmoid and softmax backward steps
+ * round their intermediate products to bf16 as the bf16 GPU kernels do:
+ * rb(rb(g rb(1 - y)) y) and rb(gy - y sum(gy)), gy = rb(g y)).  grad_h_pre / grad_h_post / grad_H_merged may be NULL
+ * (zero).  Writes grad_proj (T, 32) bf16 and the parameter gradients
+ * grad_alpha_pre, grad_alpha_post, grad_alpha_res (one fp32 each) and
+ * grad_bias (32 fp32): sums over tokens, accumulated in fp32 in a fixed
+ * order and rounded once to bf16.  `workspace`: at least
+ * fmhc_k2_bwd_workspace_bytes(T) bytes of device memory for per-block partials.
+ * Replaces: autograd through src/flash_mhc/block.py:161-170 and :176-177. */
+int fmhc_k2_bwd(const uint16_t* proj, const float* alpha_pre, const float* alpha_post,
+                const float* alpha_res, const float* bias, const float* perm,
+                const float* grad_h_pre, const float* grad_h_post, const float* grad_H_merged,
+                uint16_t* grad_proj, float* grad_alpha_pre, float* grad_alpha_post,
+                float* grad_alpha_res, float* grad_bias, void* workspace, int64_t workspace_bytes,
+                int64_t T, int64_t n, void* stream);
+/* Workspace bytes fmhc_k2_bwd needs for T tokens.  No counterpart in the reference. */
+int64_t fmhc_k2_bwd_workspace_bytes(int64_t T);
 /* K3 forward: out[t,c] = bf16(sum_j h_pre[t,j] * x[t,j,c]), j = 0..3 in order.
  * x (T, n, C) bf16; h_pre (T, n) fp32; out (T, C) bf16.
  * Replaces: src/flash_mhc/ops.py:347-414 (_fused_pre_map_cuda) launching

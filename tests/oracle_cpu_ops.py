@@ -12,8 +12,10 @@ from __future__ import annotations
 
 from contextlib import contextmanager
 
+import numpy as np
 import torch
 
+from oracle import k2_oracle as K2O
 from oracle import mhc_oracle as O
 
 BF16 = torch.bfloat16
@@ -33,6 +35,24 @@ def _k1_bwd(grad_out, x_flat, W, proj_out, inv_rms):
     gx, _ = O.k1_bwd_dx(grad_out, x_flat, W, proj_out, inv_rms)
     gW, _ = O.k1_grad_W(grad_out, x_flat, inv_rms)
     return gx.to(x_flat.dtype), gW.to(x_flat.dtype)
+
+
+def _k2(proj, ap, apo, ar, b, perm):
+    f = K2O.k2_fwd(proj, ap, apo, ar, b, perm)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32))
+    return t(f["h_pre"]), t(f["h_post"]), t(f["H_merged"])
+
+
+def _k2_bwd(g_hpre, g_hpost, g_H, proj, ap, apo, ar, b, perm):
+    r = K2O.k2_bwd(proj, ap, apo, ar, b, perm, g_hpre, g_hpost, g_H)
+    gp = torch.from_numpy(np.ascontiguousarray(r["grad_proj"])).to(proj.dtype)
+
+    def par(key, like):
+        R = torch.as_tensor(r[key][0], dtype=torch.float64).reshape(like.shape)
+        return R.float().to(torch.bfloat16).to(like.dtype)
+
+    return (gp, par("grad_alpha_pre", ap), par("grad_alpha_post", apo), par("grad_alpha_res", ar),
+            par("grad_bias", b))
 
 
 def _k3(x, h):
@@ -62,6 +82,8 @@ IMPLS = {
     "fused_rmsnorm_project": _k1,
     "fused_rmsnorm_project_bwd_dx": _k1_bwd_dx,
     "fused_rmsnorm_project_bwd": _k1_bwd,
+    "mhc_coefficients": _k2,
+    "mhc_coefficients_backward": _k2_bwd,
     "fused_pre_map": _k3,
     "fused_pre_map_backward": _k3_bwd,
     "fused_post_res": _k4,

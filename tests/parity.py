@@ -92,3 +92,25 @@ def block_close(name: str, out: torch.Tensor, ref: torch.Tensor, rtol: float = 2
     assert not bool(bad.any()), f"{name}: {int(bad.sum())} of {err.numel()} out of tolerance; {_stats(err, tol)}"
     rel = float(err.norm() / max(float(r.norm()), 1e-30))
     return {"rel_l2": rel, "max_err_over_tol": float((err / tol).max()) if err.numel() else 0.0}
+
+
+def check_chain(name: str, out, ref, max_rate: float = 1e-3) -> dict:
+    """bf16 op chains (K2): ``out`` and ``ref`` are both bf16-exact, ``ref``
+    from the oracle's step-by-step rounding of the same chain.  The two can
+    only differ through last-bit flips of exp or of an fp32 summation order
+    that a later rounding carries on, so at most ``max_rate`` of the elements
+    may differ, and each by at most ulp_bf16(ref) + 4 ulp_bf16(max |ref| of
+    its token).  Dim 0 indexes tokens."""
+    o = torch.as_tensor(out).detach().to("cpu", torch.float64)
+    r = torch.as_tensor(ref).detach().to("cpu", torch.float64)
+    assert o.numel() == r.numel(), f"{name}: {o.numel()} != {r.numel()} elements"
+    T = r.shape[0] if r.dim() else 1
+    o, r = o.reshape(T, -1), r.reshape(T, -1)
+    err = (o - r).abs()
+    rowmax = r.abs().amax(dim=1, keepdim=True).expand_as(r)
+    tol = bf16_ulp(r) + 4.0 * bf16_ulp(rowmax)
+    bad = ~(err <= tol)
+    assert not bool(bad.any()), f"{name}: {int(bad.sum())} of {err.numel()} elements out of tolerance; {_stats(err, tol)}"
+    rate = float((err != 0).double().mean()) if err.numel() else 0.0
+    assert rate <= max_rate, f"{name}: {rate:.2e} of the elements differ (allowed {max_rate:.0e})"
+    return {"frac_differ": rate}

@@ -56,6 +56,36 @@ def test_fused_backward_op_contract():
         assert gx.shape == xf.shape and gx.dtype == BF16 and gW.shape == W.shape and gW.dtype == BF16
 
 
+ADDED_SCHEMAS = {
+    "fused_rmsnorm_project_bwd": "fused_rmsnorm_project_bwd(Tensor grad_out, Tensor x_flat, Tensor W, Tensor proj_out, Tensor inv_rms) -> (Tensor grad_x, Tensor grad_W)",
+    "mhc_coefficients": "mhc_coefficients(Tensor proj, Tensor alpha_pre, Tensor alpha_post, Tensor alpha_res, Tensor bias, Tensor perm_mat) -> (Tensor h_pre, Tensor h_post, Tensor H_merged)",
+    "mhc_coefficients_backward": "mhc_coefficients_backward(Tensor? grad_h_pre, Tensor? grad_h_post, Tensor? grad_H_merged, Tensor proj, Tensor alpha_pre, Tensor alpha_post, Tensor alpha_res, Tensor bias, Tensor perm_mat) -> (Tensor grad_proj, Tensor grad_alpha_pre, Tensor grad_alpha_post, Tensor grad_alpha_res, Tensor grad_bias)",
+}
+
+
+@pytest.mark.parametrize("name", sorted(ADDED_SCHEMAS))
+def test_added_ops_device_only(name):
+    op = getattr(torch.ops.flash_mhc, name).default
+    assert str(op._schema) == "flash_mhc::" + ADDED_SCHEMAS[name]
+    assert torch._C._dispatch_has_kernel_for_dispatch_key(f"flash_mhc::{name}", "CUDA")
+    assert not torch._C._dispatch_has_kernel_for_dispatch_key(f"flash_mhc::{name}", "CPU")
+
+
+def test_mhc_coefficients_fakes_and_n4_error():
+    with FakeTensorMode():
+        proj = torch.empty(7, 32, dtype=BF16)
+        a = torch.empty(1)
+        hp, hq, H = torch.ops.flash_mhc.mhc_coefficients(proj, a, a, a, torch.empty(32), torch.empty(24, 16))
+        assert hp.shape == (7, 4) and hq.shape == (7, 4) and H.shape == (7, 4, 4)
+        assert hp.dtype == hq.dtype == H.dtype == torch.float32
+        g = torch.ops.flash_mhc.mhc_coefficients_backward(hp, None, H, proj, a, a, a, torch.empty(32),
+                                                          torch.empty(24, 16))
+        assert g[0].shape == proj.shape and g[0].dtype == BF16 and g[4].shape == (32,)
+    with pytest.raises(ValueError, match="n=4 only"):
+        ops._mhc_coefficients_cuda(torch.empty(3, 12, dtype=BF16), *[torch.empty(1)] * 3, torch.empty(12),
+                                   torch.empty(6, 9))
+
+
 def test_only_device_kernels_registered():
     """No CPU implementation ships: the device path cannot silently fall back."""
     for name in REFERENCE_SCHEMAS:
@@ -164,6 +194,14 @@ def test_opcheck_all_ops(cpu_kernels):
          (x.clone().requires_grad_(True), lo.clone().requires_grad_(True), H.clone().requires_grad_(True), hp.clone().requires_grad_(True))),
         (torch.ops.flash_mhc.fused_post_res_backward.default, (rnd((T, 4, C), 18), x, lo, H, hp)),
     ]
+    k2p = [torch.tensor([0.7]), torch.tensor([1.1]), torch.tensor([1.9]), rnd((32,), 19, 0.5, torch.float32)]
+    perm = O.permutation_matrices(4)[0]
+    cases += [
+        (torch.ops.flash_mhc.mhc_coefficients.default,
+         (proj.clone().requires_grad_(True), *[t.clone().requires_grad_(True) for t in k2p], perm)),
+        (torch.ops.flash_mhc.mhc_coefficients_backward.default,
+         (hp, None, H, proj, *k2p, perm)),
+    ]
     for op, args in cases:
         torch.library.opcheck(op, args)
 
@@ -244,3 +282,34 @@ def test_fused_block_matches_plain_block_on_cpu(cpu_kernels):
         a = blk._forward_triton(x)
         b = blk.float()._forward_pytorch(x.float())
     block_close("fused vs plain", a, b)
+
+
+def test_fused_k2_matches_reference_chain_on_cpu(cpu_kernels, monkeypatch):
+    """The block with K2 as one op (FLASH_MHC_FUSED_K2=1) and with the
+    reference's PyTorch ops (=0) give the same outputs and gradients: the op's
+    autograd wiring routes every gradient to the right parameter."""
+
+    def run(flag):
+        monkeypatch.setenv("FLASH_MHC_FUSED_K2", flag)
+        blk = _block(C=32)
+        with torch.no_grad():
+            blk.alpha_pre.fill_(0.8)
+            blk.alpha_post.fill_(1.2)
+            blk.alpha_res.fill_(1.7)
+        x = rnd((64, 4, 32), 41).requires_grad_(True)
+        out = blk._forward_triton(x)
+        out.float().pow(2).sum().backward()
+        return out.detach(), x.grad, {n: p.grad for n, p in blk.named_parameters()}
+
+    from parity import block_close
+
+    o1, gx1, gp1 = run("1")
+    o0, gx0, gp0 = run("0")
+    assert torch.equal(o1, o0)
+    # The op rounds the sigmoid / softmax backward steps as torch's GPU kernels
+    # do, the CPU chain as torch's CPU kernels do: gradients agree to bf16
+    # accuracy (the reference's end-to-end gradient tolerance, per token).
+    block_close("grad_x fused K2 vs ops", gx1.float(), gx0.float(), rtol=5e-2, atol=1e-1)
+    for n in gp0:
+        torch.testing.assert_close(gp1[n].float(), gp0[n].float(), rtol=5e-2,
+                                   atol=2e-2 * float(gp0[n].float().abs().max()) + 1e-6, msg=n)

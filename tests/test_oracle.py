@@ -17,8 +17,9 @@ import pytest
 import torch
 import torch.nn.functional as F
 
+from oracle import k2_oracle as K2O
 from oracle import mhc_oracle as O
-from parity import bf16_ulp, check_bf16, check_fp32
+from parity import bf16_ulp, check_bf16, check_chain, check_fp32
 
 F64 = torch.float64
 
@@ -302,3 +303,99 @@ def test_parity_rule_catches_planted_mistakes():
     R3b, _ = O.k3_fwd(x.roll(1, dims=1), h)
     with pytest.raises(AssertionError):
         check_bf16("stream index", R3b.to(torch.bfloat16), R3, S3, 4)
+
+
+# ---------------------------------------------------------------------------
+# K2 coefficient chain with bf16 rounding points (oracle/k2_oracle.py), pinned
+# against torch's own bf16 CPU forward + autograd through the reference's op
+# sequence (mhc_oracle.coefficients, i.e. block.py:161-170 + the .float()
+# casts of block.py:176-177).  The GPU rounding of the sigmoid / softmax
+# backward steps is pinned against torch's GPU ops in tests/test_gpu_k2.py.
+
+
+def test_k2_rounding_variants_differ_only_in_two_steps():
+    """The GPU and CPU variants of the two backward steps: identical on values
+    that need no intermediate rounding, different (and each within 2 ulps of
+    the other) in general."""
+    g = torch.Generator().manual_seed(9)
+    y = torch.rand(4096, 24, generator=g).to(torch.bfloat16).float().numpy()
+    gr = torch.randn(4096, 24, generator=g).to(torch.bfloat16).float().numpy()
+    for fn in (K2O.sigmoid_bwd, K2O.softmax_bwd):
+        a, b = fn(gr, y, "gpu"), fn(gr, y, "cpu")
+        assert (a != b).mean() > 0.05
+        check_chain(fn.__name__ + " gpu vs cpu", a, b, max_rate=1.0)
+    half = 0.5 * torch.ones(8, 4).numpy()
+    ones = torch.ones(8, 4).numpy()
+    assert (K2O.sigmoid_bwd(ones, half, "gpu") == 0.25).all() and (K2O.sigmoid_bwd(ones, half, "cpu") == 0.25).all()
+
+
+def _k2_case(T, seed, proj_scale=3.0):
+    g = torch.Generator().manual_seed(seed)
+    proj = (torch.randn(T, 32, generator=g) * proj_scale).to(torch.bfloat16)
+    bias = torch.randn(32, generator=g) * 0.5
+    alphas = [torch.tensor([v]) for v in (0.9, 1.3, 2.1)]
+    gh = [torch.randn(T, 4, generator=g), torch.randn(T, 4, generator=g), torch.randn(T, 4, 4, generator=g)]
+    return proj, alphas, bias, gh
+
+
+def _k2_torch_cpu(proj, alphas, bias, perm, gh):
+    """The reference's chain on CPU in bf16, with torch autograd."""
+    p = proj.clone().requires_grad_(True)
+    a = [x.clone().requires_grad_(True) for x in alphas]
+    b = bias.clone().requires_grad_(True)
+    h_pre, h_post, H, _ = O.coefficients(p, b, a[0], a[1], a[2], perm, 4)
+    outs = (h_pre.float(), h_post.float(), H.float())
+    loss = sum((o * g).sum() for o, g in zip(outs, gh))
+    loss.backward()
+    return outs, p.grad, [x.grad for x in a], b.grad
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_k2_chain_matches_torch_bf16_autograd(seed):
+    T = 4096
+    proj, alphas, bias, gh = _k2_case(T, seed)
+    perm, _ = O.permutation_matrices(4)
+    outs, gproj, galpha, gbias = _k2_torch_cpu(proj, alphas, bias, perm, gh)
+    f = K2O.k2_fwd(proj, *alphas, bias, perm)
+    check_chain("k2 h_pre", f["h_pre"], outs[0])
+    check_chain("k2 h_post", f["h_post"], outs[1])
+    check_chain("k2 H_merged", f["H_merged"], outs[2])
+    b = K2O.k2_bwd(proj, *alphas, bias, perm, *gh, rounding="cpu")  # torch's CPU kernels
+    check_chain("k2 grad_proj", b["grad_proj"], gproj)
+    for name, got in zip(("grad_alpha_pre", "grad_alpha_post", "grad_alpha_res"), galpha):
+        R, S = b[name]
+        check_bf16(name, got.to(torch.bfloat16), torch.tensor([R], dtype=F64), torch.tensor([S], dtype=F64), 24 * T)
+    R, S = b["grad_bias"]
+    check_bf16("grad_bias", gbias.to(torch.bfloat16), torch.as_tensor(R), torch.as_tensor(S), T)
+
+
+def test_k2_chain_closed_forms():
+    """Saturated logits: h_pre, h_post reach their limits and the softmax puts
+    all weight on one permutation, so H_res is that permutation matrix."""
+    T = 24
+    perm, _ = O.permutation_matrices(4)
+    proj = torch.zeros(T, 32)
+    proj[:, :4] = 200.0  # exp(-200) and exp(-200 - 0) underflow in fp32
+    proj[:, 4:8] = -200.0
+    for t in range(T):
+        proj[t, 8 + t] = 200.0
+    f = K2O.k2_fwd(proj.to(torch.bfloat16), torch.tensor([1.0]), torch.tensor([1.0]), torch.tensor([1.0]),
+                   torch.zeros(32), perm)
+    assert (f["h_pre"] == 1.0).all() and (f["h_post"] == 0.0).all()
+    assert torch.equal(torch.from_numpy(f["H_res"]), perm)
+    assert torch.equal(torch.from_numpy(f["H_merged"]).reshape(T, 16), perm)
+
+
+@pytest.mark.parametrize("plant", ["no_round_scale", "transpose_perm", "sigmoid_derivative"])
+def test_k2_chain_catches_planted_mistakes(plant):
+    T = 4096
+    proj, alphas, bias, gh = _k2_case(T, 3)
+    perm, _ = O.permutation_matrices(4)
+    outs, gproj, _, _ = _k2_torch_cpu(proj, alphas, bias, perm, gh)
+    with pytest.raises(AssertionError):
+        if plant == "sigmoid_derivative":
+            check_chain("planted", K2O.k2_bwd(proj, *alphas, bias, perm, *gh, rounding="cpu", _plant=plant)["grad_proj"], gproj)
+        else:
+            f = K2O.k2_fwd(proj, *alphas, bias, perm, _plant=plant)
+            check_chain("planted h_pre", f["h_pre"], outs[0])
+            check_chain("planted H", f["H_merged"], outs[2])
