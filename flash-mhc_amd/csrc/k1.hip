@@ -211,10 +211,13 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
 // instruction covers 4 token rows x 256 contiguous bytes (whole cache lines).
 // The B tiles depend only on the slice, so each wave builds them once: eight
 // 16-byte loads of W rows and an 8 x 8 bf16 transpose in registers.
+template <bool EPI>
 struct BwdFrag {
   u32x4 gv, pv;   // go / proj_out row of token tbase + col, d = 8 * grp .. + 8
   float inv[4];   // inv_rms of tokens tbase + 4 * grp + q
   u32x4 xv[4];    // x of those tokens, k = kl .. kl + 8
+  u32x4 g3[EPI ? 4 : 1];  // EPI: the K3 output gradient of those tokens at the lane's c
+  float hp[EPI ? 4 : 1];  // EPI: their h_pre of the lane's stream j
 };
 
 // With DW = true the same pass also accumulates the weight gradient
@@ -227,7 +230,12 @@ struct BwdFrag {
 // with G = bf16(go * inv_rms).  G reaches the B layout through a 1 KiB
 // wave-private LDS tile.  Each wave writes its fp32 partial dW for its slice;
 // k1_dw_reduce sums the partials of all runs in a fixed order.
-template <int NTB, bool DW, bool FULLK>
+//
+// With EPI = true (the pre-map backward) the store also adds the K3 term of
+// x's gradient, grad_x = bf16(bf16(h_pre[t, j] go3[t, c]) + bf16(dx)), k = j C + c:
+// the bf16 sum autograd forms when K3 and K1 are separate ops.  The B tiles
+// then live in LDS so that the extra operands keep two waves per SIMD.
+template <int NTB, bool DW, bool FULLK, bool EPI>
 __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ x,
                                                    const uint16_t* __restrict__ W,
                                                    const uint16_t* __restrict__ go,
@@ -235,7 +243,9 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
                                                    const float* __restrict__ inv_rms,
                                                    uint16_t* __restrict__ gx,
                                                    float* __restrict__ dw_partial,
-                                                   int64_t T, int nC, int nslices) {
+                                                   const uint16_t* __restrict__ go3,
+                                                   const float* __restrict__ h_pre,
+                                                   int64_t T, int nC, int nslices, int C) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
   const int col = lane & 15;  // A row (token) for the loads of go, B/D column
@@ -261,6 +271,10 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
   const uint32_t kbytes = 2u * static_cast<uint32_t>(kl);
 
   __shared__ uint32_t gtile[DW ? 4 : 1][16 * 16];  // wave-private 16 tokens x 32 d bf16
+  __shared__ u32x4 btile[EPI ? 4 : 1][EPI ? 8 : 1][EPI ? kWave : 1];  // EPI: wave-private B tiles
+  // EPI: the lane's stream j and position c (C % 8 == 0: k .. k + 7 stay in one stream).
+  const int sj = EPI ? kl / C : 0;
+  const uint32_t c3bytes = EPI ? 2u * static_cast<uint32_t>(kl - sj * C) : 0u;
   f32x4 dacc[DW ? 8 : 1][2];
 #pragma unroll
   for (int m = 0; m < (DW ? 8 : 1); ++m) dacc[m][0] = dacc[m][1] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -284,8 +298,16 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
       }
       const u32x4 v = {h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
       bfr[m] = as_bf16x8(v);
+      if constexpr (EPI) btile[wave][m][lane] = v;
     }
   }
+  // Same-wave LDS writes and reads are ordered: the tiles need no barrier.
+  auto btile_at = [&](int m) -> bf16x8 {
+    if constexpr (EPI)
+      return as_bf16x8(btile[wave][m][lane]);
+    else
+      return bfr[m];
+  };
 
   // Token blocks of this wave, two per trip with double-buffered fragments:
   // the next block's go / proj_out / inv_rms / x are in flight while the
@@ -296,7 +318,7 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
   auto block_base = [&](int tb) { return (run + static_cast<int64_t>(tb) * nruns) * 16; };
   // Valid rows of the block starting at tbase (16 except in the last block).
   auto block_rows = [&](int64_t tbase) { return static_cast<int>(T - tbase < 16 ? T - tbase : 16); };
-  auto load = [&](BwdFrag& f, int tb) {
+  auto load = [&](BwdFrag<EPI>& f, int tb) {
     const int64_t tbase = block_base(tb);
     const int last = block_rows(tbase) - 1;  // rows past the end re-read the last one
     const int rg = col < last ? col : last;
@@ -312,9 +334,19 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
       f.inv[q] = *reinterpret_cast<const float*>(ib + 4u * r);
       f.xv[q] = u32x4{0u, 0u, 0u, 0u};
       if (kok) f.xv[q] = ld_stream(reinterpret_cast<const u32x4*>(xb + (r * row_bytes + kbytes)));
+      if constexpr (EPI) {
+        f.hp[q] = 0.f;
+        f.g3[q] = u32x4{0u, 0u, 0u, 0u};
+        if (kok) {  // lanes past nC have no stream
+          const char* g3b = reinterpret_cast<const char*>(go3 + tbase * C);
+          f.hp[q] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(h_pre + tbase * 4) +
+                                                    16u * r + 4u * static_cast<uint32_t>(sj));
+          f.g3[q] = ld_stream(reinterpret_cast<const u32x4*>(g3b + (r * 2u * static_cast<uint32_t>(C) + c3bytes)));
+        }
+      }
     }
   };
-  auto compute = [&](const BwdFrag& f, int tb) {
+  auto compute = [&](const BwdFrag<EPI>& f, int tb) {
     const int64_t tbase = block_base(tb);
     const int rows = block_rows(tbase);
     // dot(go, proj_out) of token tbase + col, over the four 8-wide d groups.
@@ -335,7 +367,7 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
     f32x4 acc[8];
     const bf16x8 a = as_bf16x8(f.gv);
 #pragma unroll
-    for (int m = 0; m < 8; ++m) acc[m] = mfma16(a, bfr[m], f32x4{0.f, 0.f, 0.f, 0.f});
+    for (int m = 0; m < 8; ++m) acc[m] = mfma16(a, btile_at(m), f32x4{0.f, 0.f, 0.f, 0.f});
     if (kok) {
       char* gxb = reinterpret_cast<char*>(gx + tbase * nC);
 #pragma unroll
@@ -346,6 +378,13 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
           unpack8(f.xv[q], xf);
 #pragma unroll
           for (int m = 0; m < 8; ++m) o[m] = f.inv[q] * acc[m][q] - scale[q] * xf[m];
+          if constexpr (EPI) {
+            float g3f[8];
+            unpack8(f.g3[q], g3f);
+#pragma unroll
+            for (int m = 0; m < 8; ++m)
+              o[m] = bf16_to_f32(f32_to_bf16(f.hp[q] * g3f[m])) + bf16_to_f32(f32_to_bf16(o[m]));
+          }
           st_stream(reinterpret_cast<u32x4*>(gxb + (static_cast<uint32_t>(r) * row_bytes + kbytes)), pack8(o));
         }
       }
@@ -395,7 +434,7 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
       }
     }
   };
-  BwdFrag f0, f1;
+  BwdFrag<EPI> f0, f1;
   load(f0, 0);
   int i = 0;
   for (; i + 1 < nb; i += 2) {
@@ -519,6 +558,8 @@ __global__ __launch_bounds__(256) void k1_fwd_scalar(const uint16_t* __restrict_
   }
 }
 
+// ACC: grad_x already holds the pre-map's K3 term; store bf16(that + bf16(dx)).
+template <bool ACC>
 __global__ __launch_bounds__(256) void k1_bwd_scalar(const uint16_t* __restrict__ x,
                                                      const uint16_t* __restrict__ W,
                                                      const uint16_t* __restrict__ go,
@@ -546,7 +587,11 @@ __global__ __launch_bounds__(256) void k1_bwd_scalar(const uint16_t* __restrict_
 #pragma unroll
     for (int d = 0; d < kDout; ++d)
       s = __builtin_fmaf(g[d], bf16_to_f32(W[static_cast<int64_t>(d) * nC + k]), s);
-    gr[k] = f32_to_bf16(inv * s - scale * bf16_to_f32(xr[k]));
+    const float v = inv * s - scale * bf16_to_f32(xr[k]);
+    if constexpr (ACC)
+      gr[k] = f32_to_bf16(bf16_to_f32(gr[k]) + bf16_to_f32(f32_to_bf16(v)));
+    else
+      gr[k] = f32_to_bf16(v);
   }
 }
 
@@ -566,14 +611,17 @@ bool k1_bwd_mfma_path(const void* x, const void* W, const void* go, const void* 
          aligned16(proj) && aligned16(gx);
 }
 
-template <int NTB, bool DW>
+template <int NTB, bool DW, bool EPI = false>
 void launch_k1_bwd_mfma(dim3 grid, hipStream_t s, const uint16_t* x, const uint16_t* W,
                         const uint16_t* go, const uint16_t* proj, const float* inv_rms, uint16_t* gx,
-                        float* partial, int64_t T, int nC, int nslices) {
+                        float* partial, int64_t T, int nC, int nslices,
+                        const uint16_t* go3 = nullptr, const float* h_pre = nullptr, int C = 1) {
   if (nC % 128 == 0)
-    k1_bwd_mfma<NTB, DW, true><<<grid, 256, 0, s>>>(x, W, go, proj, inv_rms, gx, partial, T, nC, nslices);
+    k1_bwd_mfma<NTB, DW, true, EPI><<<grid, 256, 0, s>>>(x, W, go, proj, inv_rms, gx, partial, go3, h_pre,
+                                                         T, nC, nslices, C);
   else
-    k1_bwd_mfma<NTB, DW, false><<<grid, 256, 0, s>>>(x, W, go, proj, inv_rms, gx, partial, T, nC, nslices);
+    k1_bwd_mfma<NTB, DW, false, EPI><<<grid, 256, 0, s>>>(x, W, go, proj, inv_rms, gx, partial, go3, h_pre,
+                                                          T, nC, nslices, C);
 }
 
 }  // namespace
@@ -614,7 +662,7 @@ extern "C" int fmhc_k1_bwd_dx(const uint16_t* x_flat, const uint16_t* W, const u
                                        proj_out, inv_rms, grad_x, nullptr, T, nc, nslices);
   } else {
     const dim3 grid(blocks_for(T, 4));
-    k1_bwd_scalar<<<grid, 256, 0, s>>>(x_flat, W, grad_out, proj_out, inv_rms, grad_x, T, nc);
+    k1_bwd_scalar<false><<<grid, 256, 0, s>>>(x_flat, W, grad_out, proj_out, inv_rms, grad_x, T, nc);
   }
   return launch_status();
 }
@@ -666,3 +714,49 @@ extern "C" int fmhc_k1_bwd(const uint16_t* x_flat, const uint16_t* W, const uint
       x_flat, grad_out, inv_rms, grad_W, T, nc);
   return launch_status();
 }
+
+namespace fmhc {
+
+// K1 backward of the pre-map region (premap.hip): grad_W as fmhc_k1_bwd and
+// grad_x = bf16(bf16(h_pre[t, j] go3[t, c]) + bf16(dx)).  On the MFMA path the
+// K3 term is computed in the store; otherwise grad_x must already hold it
+// (fmhc_k3_bwd's grad_x) and the element-wise kernel adds dx to it.
+bool k1_bwd_premap_fused(const void* x, const void* W, const void* go, const void* proj, const void* gx,
+                         const void* go3, int64_t C) {
+  return C % 8 == 0 && k1_bwd_mfma_path(x, W, go, proj, gx, 4 * C) && aligned16(go3);
+}
+
+int k1_bwd_premap(const uint16_t* x_flat, const uint16_t* W, const uint16_t* grad_proj,
+                  const uint16_t* proj, const float* inv_rms, const uint16_t* go3, const float* h_pre,
+                  uint16_t* grad_x, uint16_t* grad_W, void* workspace, int64_t workspace_bytes, int64_t T,
+                  int64_t C, hipStream_t s) {
+  const int64_t nC = 4 * C;
+  const int nc = static_cast<int>(nC);
+  if (T == 0) {
+    k1_dw_zero<<<dim3(blocks_for(static_cast<int64_t>(kDout) * nC, 256)), 256, 0, s>>>(grad_W, nc);
+    return launch_status();
+  }
+  if (k1_bwd_premap_fused(x_flat, W, grad_proj, proj, grad_x, go3, C)) {
+    if (!workspace || workspace_bytes < fmhc_k1_bwd_workspace_bytes(T, nC) || !aligned16(workspace))
+      return FMHC_ERR_INVALID_ARGUMENT;
+    const int nslices = static_cast<int>((nC + 127) / 128);
+    const int64_t nruns = k1_bwd_runs(T);
+    float* partial = static_cast<float*>(workspace);
+    launch_k1_bwd_mfma<kBwdDwNTB, true, true>(dim3(blocks_for(nruns * nslices, 4)), s, x_flat, W, grad_proj,
+                                              proj, inv_rms, grad_x, partial, T, nc, nslices, go3, h_pre,
+                                              static_cast<int>(C));
+    const int st = launch_status();
+    if (st != FMHC_OK) return st;
+    const int64_t per_part = static_cast<int64_t>(nslices) * (8 * 2 * 4 * kWave);
+    k1_dw_reduce<<<dim3(blocks_for(per_part / 4, 256)), 256, 0, s>>>(partial, grad_W, nruns, nslices, nc);
+    return launch_status();
+  }
+  k1_bwd_scalar<true><<<dim3(blocks_for(T, 4)), 256, 0, s>>>(x_flat, W, grad_proj, proj, inv_rms, grad_x, T, nc);
+  const int st = launch_status();
+  if (st != FMHC_OK) return st;
+  k1_dw_scalar<<<dim3(blocks_for(static_cast<int64_t>(kDout) * nC, 256)), 256, 0, s>>>(
+      x_flat, grad_proj, inv_rms, grad_W, T, nc);
+  return launch_status();
+}
+
+}  // namespace fmhc

@@ -1,0 +1,101 @@
+// Per-token pieces of K2, the mHC-lite coefficient chain (block.py:161-170 of
+// alint77/flash-mHC), shared by the K2 kernels and the one-pass pre-map kernel.
+// Every value the reference holds in a bf16 tensor is rounded with rb(); the
+// fp32 operations run in the reference's order, with contraction off.
+#pragma once
+
+#include "fmhc_common.h"
+
+namespace fmhc {
+
+constexpr int kN = 4;
+constexpr int kNF = 24;             // n! for n = 4
+constexpr int kDk = 2 * kN + kNF;   // 32 projection columns
+constexpr int kNPar = 3 + kDk;      // alpha_pre, alpha_post, alpha_res, bias[32]
+__device__ __forceinline__ float rb(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+
+// perm (24 x 16) rounded to bf16 (the reference multiplies by perm_mat.to(bf16)),
+// staged in LDS once per block; every lane then reads the same rows (broadcast).
+template <int THREADS>
+__device__ __forceinline__ void stage_perm(const float* __restrict__ perm, f32x4 sperm[kNF * 4]) {
+  float* s = reinterpret_cast<float*>(sperm);
+  for (int i = threadIdx.x; i < kNF * kN * kN; i += THREADS) s[i] = rb(perm[i]);
+  __syncthreads();
+}
+
+__device__ __forceinline__ float sigmoid_f32(float z) {
+#pragma clang fp contract(off)
+  const float d = 1.f + expf(-z);
+  return 1.f / d;
+}
+
+template <bool VEC>
+__device__ __forceinline__ void load_proj(const uint16_t* __restrict__ row, float p[kDk]) {
+  if constexpr (VEC) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) unpack8(reinterpret_cast<const u32x4*>(row)[i], p + 8 * i);
+  } else {
+#pragma unroll
+    for (int i = 0; i < kDk; ++i) p[i] = bf16_to_f32(row[i]);
+  }
+}
+
+// Forward chain of one token.  Fills the values the backward reuses.
+struct K2Fwd {
+  float hp[kN], hq[kN], sq[kN];  // h_pre, h_post, sigmoid of the post logits
+  float a[kNF];                  // softmax weights
+};
+
+__device__ __forceinline__ void k2_chain(const float p[kDk], float ap, float apo, float ar,
+                                         const float* __restrict__ bias, K2Fwd& f) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int j = 0; j < kN; ++j) {
+    const float z = rb(rb(ap * p[j]) + rb(bias[j]));
+    f.hp[j] = rb(sigmoid_f32(z));
+  }
+#pragma unroll
+  for (int j = 0; j < kN; ++j) {
+    const float z = rb(rb(apo * p[kN + j]) + rb(bias[kN + j]));
+    f.sq[j] = rb(sigmoid_f32(z));
+    f.hq[j] = rb(2.f * f.sq[j]);
+  }
+  float z[kNF];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int m = 0; m < kNF; ++m) {
+    z[m] = rb(rb(ar * p[2 * kN + m]) + rb(bias[2 * kN + m]));
+    mx = fmaxf(mx, z[m]);
+  }
+  float sum = 0.f;
+#pragma unroll
+  for (int m = 0; m < kNF; ++m) {
+    z[m] = expf(z[m] - mx);
+    sum = sum + z[m];
+  }
+#pragma unroll
+  for (int m = 0; m < kNF; ++m) f.a[m] = rb(z[m] / sum);
+}
+
+// H_merged row i of one token: rb(rb(sum_m a[m] perm[m, 4i + j]) - rb(h_post[i] h_pre[j])),
+// the sum over m in order.
+__device__ __forceinline__ void k2_h_merged(const K2Fwd& f, const f32x4 sperm[kNF * 4], f32x4 H[kN]) {
+#pragma clang fp contract(off)
+  float acc[kN * kN];
+#pragma unroll
+  for (int ij = 0; ij < kN * kN; ++ij) acc[ij] = 0.f;
+#pragma unroll
+  for (int m = 0; m < kNF; ++m)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const f32x4 pm = sperm[m * 4 + q];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[4 * q + e] = acc[4 * q + e] + f.a[m] * pm[e];
+    }
+#pragma unroll
+  for (int i = 0; i < kN; ++i)
+#pragma unroll
+    for (int j = 0; j < kN; ++j) H[i][j] = rb(rb(acc[i * kN + j]) - rb(f.hq[i] * f.hp[j]));
+}
+
+}  // namespace fmhc

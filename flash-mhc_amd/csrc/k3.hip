@@ -67,7 +67,9 @@ __global__ __launch_bounds__(kBlock) void k3_fwd_kernel(const uint16_t* __restri
   }
 }
 
-template <int VEC, int LPT>
+// GX = false: grad_h_pre only (the pre-map backward adds h_pre * go into K1's
+// grad_x store instead of writing it here).
+template <int VEC, int LPT, bool GX>
 __global__ __launch_bounds__(kBlock) void k3_bwd_kernel(const uint16_t* __restrict__ x,
                                                         const float* __restrict__ h_pre,
                                                         const uint16_t* __restrict__ go,
@@ -101,18 +103,20 @@ __global__ __launch_bounds__(kBlock) void k3_bwd_kernel(const uint16_t* __restri
     Lanes<VEC>::load(x1, g, b);
     Lanes<VEC>::load(x2, g, c);
     Lanes<VEC>::load(x3, g, d);
+    if constexpr (GX) {
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) o[e] = h0 * q[e];
-    Lanes<VEC>::store(gx0, g, o);
+      for (int e = 0; e < VEC; ++e) o[e] = h0 * q[e];
+      Lanes<VEC>::store(gx0, g, o);
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) o[e] = h1 * q[e];
-    Lanes<VEC>::store(gx1, g, o);
+      for (int e = 0; e < VEC; ++e) o[e] = h1 * q[e];
+      Lanes<VEC>::store(gx1, g, o);
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) o[e] = h2 * q[e];
-    Lanes<VEC>::store(gx2, g, o);
+      for (int e = 0; e < VEC; ++e) o[e] = h2 * q[e];
+      Lanes<VEC>::store(gx2, g, o);
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) o[e] = h3 * q[e];
-    Lanes<VEC>::store(gx3, g, o);
+      for (int e = 0; e < VEC; ++e) o[e] = h3 * q[e];
+      Lanes<VEC>::store(gx3, g, o);
+    }
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
       s0 = __builtin_fmaf(a[e], q[e], s0);
@@ -160,17 +164,17 @@ int launch_k3_fwd(const uint16_t* x, const float* h_pre, uint16_t* out, int64_t 
   return launch_status();
 }
 
-template <int VEC>
+template <int VEC, bool GX>
 int launch_k3_bwd(const uint16_t* x, const float* h_pre, const uint16_t* go, uint16_t* grad_x,
                   float* grad_h_pre, int64_t T, int C, hipStream_t s) {
   const int lpt = pick_lpt<VEC>(C);
   const int64_t tokens_per_block = (kBlock / kWave) * (kWave / lpt);
   const dim3 grid(blocks_for(T, tokens_per_block));
   switch (lpt) {
-    case 64: k3_bwd_kernel<VEC, 64><<<grid, kBlock, 0, s>>>(x, h_pre, go, grad_x, grad_h_pre, T, C); break;
-    case 32: k3_bwd_kernel<VEC, 32><<<grid, kBlock, 0, s>>>(x, h_pre, go, grad_x, grad_h_pre, T, C); break;
-    case 16: k3_bwd_kernel<VEC, 16><<<grid, kBlock, 0, s>>>(x, h_pre, go, grad_x, grad_h_pre, T, C); break;
-    default: k3_bwd_kernel<VEC, 8><<<grid, kBlock, 0, s>>>(x, h_pre, go, grad_x, grad_h_pre, T, C); break;
+    case 64: k3_bwd_kernel<VEC, 64, GX><<<grid, kBlock, 0, s>>>(x, h_pre, go, grad_x, grad_h_pre, T, C); break;
+    case 32: k3_bwd_kernel<VEC, 32, GX><<<grid, kBlock, 0, s>>>(x, h_pre, go, grad_x, grad_h_pre, T, C); break;
+    case 16: k3_bwd_kernel<VEC, 16, GX><<<grid, kBlock, 0, s>>>(x, h_pre, go, grad_x, grad_h_pre, T, C); break;
+    default: k3_bwd_kernel<VEC, 8, GX><<<grid, kBlock, 0, s>>>(x, h_pre, go, grad_x, grad_h_pre, T, C); break;
   }
   return launch_status();
 }
@@ -201,10 +205,13 @@ extern "C" int fmhc_k3_bwd(const uint16_t* x, const float* h_pre, const uint16_t
   using namespace fmhc;
   if (bad_sizes(T, C, n)) return FMHC_ERR_INVALID_ARGUMENT;
   if (T == 0) return FMHC_OK;
-  if (!x || !h_pre || !grad_out || !grad_x || !grad_h_pre) return FMHC_ERR_INVALID_ARGUMENT;
+  if (!x || !h_pre || !grad_out || !grad_h_pre) return FMHC_ERR_INVALID_ARGUMENT;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int c = static_cast<int>(C);
-  if (C % 8 == 0 && aligned16(x) && aligned16(grad_out) && aligned16(grad_x))
-    return launch_k3_bwd<8>(x, h_pre, grad_out, grad_x, grad_h_pre, T, c, s);
-  return launch_k3_bwd<1>(x, h_pre, grad_out, grad_x, grad_h_pre, T, c, s);
+  const bool vec = C % 8 == 0 && aligned16(x) && aligned16(grad_out) && (!grad_x || aligned16(grad_x));
+  if (!grad_x)  // grad_h_pre only
+    return vec ? launch_k3_bwd<8, false>(x, h_pre, grad_out, nullptr, grad_h_pre, T, c, s)
+               : launch_k3_bwd<1, false>(x, h_pre, grad_out, nullptr, grad_h_pre, T, c, s);
+  return vec ? launch_k3_bwd<8, true>(x, h_pre, grad_out, grad_x, grad_h_pre, T, c, s)
+             : launch_k3_bwd<1, true>(x, h_pre, grad_out, grad_x, grad_h_pre, T, c, s);
 }

@@ -160,16 +160,17 @@ class MHCLiteBlock(nn.Module):
 
     # -- fused HIP path (block.py:150-219) ------------------------------------
 
+    def _projection_weight(self, dt: torch.dtype) -> torch.Tensor:
+        """K1's W in dtype dt, with the optional RMSNorm weight folded in."""
+        if self.rms_weight is None:
+            return self.W_all.weight.to(dt)
+        return (self.W_all.weight.float() * self.rms_weight.float()).to(dt)
+
     def _project_triton(self, x_streams: torch.Tensor) -> torch.Tensor:
         """K1: the (T, 2n + n!) projection of the RMS-normalised streams."""
-        dt = x_streams.dtype
         T = x_streams.shape[0]
-        if self.rms_weight is None:
-            W = self.W_all.weight.to(dt)
-        else:
-            W = (self.W_all.weight.float() * self.rms_weight.float()).to(dt)
         proj, _inv_rms = torch.ops.flash_mhc.fused_rmsnorm_project(
-            x_streams.reshape(T, self.nC), W
+            x_streams.reshape(T, self.nC), self._projection_weight(x_streams.dtype)
         )
         return proj
 
@@ -178,6 +179,13 @@ class MHCLiteBlock(nn.Module):
         return self._coefficients(self._project_triton(x_streams), x_streams.dtype)
 
     def _mhc_pre_map_triton(self, x_streams: torch.Tensor):
+        if _ops.fused_premap_enabled():
+            # K1 + K2 + K3 in one op: one forward read of x.
+            layer_input, H_merged, h_post, _h_pre, _proj, _inv_rms = torch.ops.flash_mhc.mhc_pre_map(
+                x_streams, self._projection_weight(x_streams.dtype), self.alpha_pre,
+                self.alpha_post, self.alpha_res, self.W_all.bias, self.perm_mat,
+            )
+            return layer_input, H_merged, h_post
         if _ops.fused_k2_enabled():
             # One kernel for K2, same values as the ops below (fp32 outputs).
             h_pre, h_post, H_merged = torch.ops.flash_mhc.mhc_coefficients(
@@ -194,13 +202,17 @@ class MHCLiteBlock(nn.Module):
         return torch.ops.flash_mhc.fused_post_res(x_streams, layer_output, H_merged, h_post)
 
     def _forward_triton(self, x_streams: torch.Tensor, **kwargs) -> torch.Tensor:
-        """Fused path: K1/K2/K3/K4 on the HIP kernels."""
+        """Fused path: K1/K2/K3/K4 on the HIP kernels (K1 + K2 + K3 as one pass)."""
         ctx = nullcontext() if self.training else _ops.disable_autotune_temporarily()
-        return self._run(x_streams, self._mhc_pre_map_triton, self._mhc_post_res_triton, ctx, kwargs)
+        # Only the pre-map region is checkpointed: post-res's backward needs
+        # exactly the inputs a checkpoint would keep (x, layer_output,
+        # H_merged, h_post), so recomputing its forward would only cost time.
+        return self._run(x_streams, self._mhc_pre_map_triton, self._mhc_post_res_triton, ctx, kwargs,
+                         checkpoint_post_res=False)
 
     # -- common driver ------------------------------------------------------
 
-    def _run(self, x_streams, pre_map, post_res, ctx, kwargs) -> torch.Tensor:
+    def _run(self, x_streams, pre_map, post_res, ctx, kwargs, checkpoint_post_res=True) -> torch.Tensor:
         use_ckpt = self._use_activation_checkpointing(x_streams)
         with ctx:
             if use_ckpt:
@@ -212,7 +224,7 @@ class MHCLiteBlock(nn.Module):
 
             layer_output = self.layer(layer_input, **kwargs)
 
-            if use_ckpt:
+            if use_ckpt and checkpoint_post_res:
                 return _checkpoint(
                     post_res, x_streams, layer_output, H_merged, h_post, use_reentrant=False
                 )

@@ -27,7 +27,7 @@ LIB_DIR = PKG_DIR / "_lib"
 LIB_NAME = "libflash_mhc_hip.so"
 LIB_PATH = LIB_DIR / LIB_NAME
 
-SOURCES = ("k1.hip", "k2.hip", "k3.hip", "k4.hip", "abi.hip", "stream_probe.hip")
+SOURCES = ("k1.hip", "k2.hip", "k3.hip", "k4.hip", "premap.hip", "abi.hip", "stream_probe.hip")
 
 ARCH = "gfx950"
 

@@ -12,6 +12,8 @@ Reference counterparts (alint77/flash-mHC):
   k1_bwd     <- the above plus the grad_W matmul of src/flash_mhc/ops.py:683-684, fused
   k2_fwd     <- src/flash_mhc/block.py:161-170 (PyTorch ops) and the .float() casts of :176-177
   k2_bwd     <- autograd through the same ops
+  premap_fwd <- K1 + K2 + K3 of src/flash_mhc/block.py:157-177 (one entry point)
+  premap_bwd <- autograd through the same, x's two gradients summed in K1's store
   k3_fwd     <- src/flash_mhc/kernels.py:673-717  _fused_pre_map_fwd_kernel
   k3_bwd     <- src/flash_mhc/kernels.py:720-853  _fused_pre_map_bwd_fused_kernel_n4
   k4_fwd     <- src/flash_mhc/kernels.py:384-481  _fused_post_res_fwd_kernel_n4
@@ -223,6 +225,72 @@ def k2_bwd(proj: torch.Tensor, alpha_pre: torch.Tensor, alpha_post: torch.Tensor
                              T, N_STREAMS, _abi.stream_of(proj))
     _abi.check(st, "k2_bwd")
     return grad_proj, g_ap, g_apo, g_ar, g_b
+
+
+def premap_fwd(x_streams: torch.Tensor, W: torch.Tensor, alpha_pre: torch.Tensor,
+               alpha_post: torch.Tensor, alpha_res: torch.Tensor, bias: torch.Tensor,
+               perm: torch.Tensor):
+    """K1 + K2 + K3: (layer_input (T,C) bf16, H_merged (T,4,4), h_post (T,4),
+    h_pre (T,4) fp32, proj (T,32) bf16, inv_rms (T,) fp32)."""
+    T, n, C = _streams_shape(x_streams)
+    dev = _device_of(x_streams)
+    _require(x_streams, "x_streams", _BF16, (T, n, C), dev)
+    _require(W, "W", _BF16, (D_OUT, n * C), dev)
+    _k2_params(alpha_pre, alpha_post, alpha_res, bias, perm, dev)
+    li = torch.empty((T, C), device=dev, dtype=_BF16)
+    proj = torch.empty((T, D_OUT), device=dev, dtype=_BF16)
+    inv = torch.empty((T,), device=dev, dtype=_F32)
+    h_pre = torch.empty((T, n), device=dev, dtype=_F32)
+    h_post = torch.empty((T, n), device=dev, dtype=_F32)
+    H = torch.empty((T, n, n), device=dev, dtype=_F32)
+    lib = _abi.load()
+    with _OnDevice(dev):
+        st = lib.fmhc_premap_fwd(x_streams.data_ptr(), W.data_ptr(), alpha_pre.data_ptr(),
+                                 alpha_post.data_ptr(), alpha_res.data_ptr(), bias.data_ptr(),
+                                 perm.data_ptr(), li.data_ptr(), proj.data_ptr(), inv.data_ptr(),
+                                 h_pre.data_ptr(), h_post.data_ptr(), H.data_ptr(), T, C, n,
+                                 _abi.stream_of(x_streams))
+    _abi.check(st, "premap_fwd")
+    return li, H, h_post, h_pre, proj, inv
+
+
+def premap_bwd(x_streams: torch.Tensor, W: torch.Tensor, alpha_pre: torch.Tensor,
+               alpha_post: torch.Tensor, alpha_res: torch.Tensor, bias: torch.Tensor,
+               perm: torch.Tensor, h_pre: torch.Tensor, proj: torch.Tensor, inv_rms: torch.Tensor,
+               grad_layer_input: torch.Tensor, grad_h_post: torch.Tensor | None,
+               grad_H: torch.Tensor | None):
+    """Gradients of premap_fwd's inputs: (grad_x (T,4,C) bf16, grad_W (32,4C) bf16,
+    grad_alpha_pre, grad_alpha_post, grad_alpha_res (1,), grad_bias (32,) fp32)."""
+    T, n, C = _streams_shape(x_streams)
+    dev = _device_of(x_streams)
+    _require(x_streams, "x_streams", _BF16, (T, n, C), dev)
+    _require(W, "W", _BF16, (D_OUT, n * C), dev)
+    _k2_params(alpha_pre, alpha_post, alpha_res, bias, perm, dev)
+    _require(h_pre, "h_pre", _F32, (T, n), dev)
+    _require(proj, "proj", _BF16, (T, D_OUT), dev)
+    _require(inv_rms, "inv_rms", _F32, (T,), dev)
+    _require(grad_layer_input, "grad_layer_input", _BF16, (T, C), dev)
+    if grad_h_post is not None:
+        _require(grad_h_post, "grad_h_post", _F32, (T, n), dev)
+    if grad_H is not None:
+        _require(grad_H, "grad_H_merged", _F32, (T, n, n), dev)
+    gx = torch.empty_like(x_streams)
+    gW = torch.empty((D_OUT, n * C), device=dev, dtype=_BF16)
+    ga = [torch.empty((1,), device=dev, dtype=_F32) for _ in range(3)]
+    gb = torch.empty((D_OUT,), device=dev, dtype=_F32)
+    lib = _abi.load()
+    nbytes = int(lib.fmhc_premap_bwd_workspace_bytes(T, C))
+    ws = torch.empty((max(nbytes, 16),), device=dev, dtype=torch.uint8)
+    ptr = lambda t: None if t is None else t.data_ptr()
+    with _OnDevice(dev):
+        st = lib.fmhc_premap_bwd(x_streams.data_ptr(), W.data_ptr(), alpha_pre.data_ptr(),
+                                 alpha_post.data_ptr(), alpha_res.data_ptr(), bias.data_ptr(),
+                                 perm.data_ptr(), h_pre.data_ptr(), proj.data_ptr(), inv_rms.data_ptr(),
+                                 grad_layer_input.data_ptr(), ptr(grad_h_post), ptr(grad_H), gx.data_ptr(),
+                                 gW.data_ptr(), ga[0].data_ptr(), ga[1].data_ptr(), ga[2].data_ptr(),
+                                 gb.data_ptr(), ws.data_ptr(), ws.numel(), T, C, n, _abi.stream_of(x_streams))
+    _abi.check(st, "premap_bwd")
+    return gx, gW, ga[0], ga[1], ga[2], gb
 
 
 def _streams_shape(x: torch.Tensor) -> tuple[int, int, int]:

@@ -25,6 +25,11 @@ Additions (not in the reference):
                               the .float() casts of :176-177, as one kernel each
                               way, with the reference's bf16 rounding points.
                               MHCLiteBlock uses it unless FLASH_MHC_FUSED_K2=0.
+  mhc_pre_map (+ _backward)   the pre-map region (K1, K2, K3 of block.py:157-177)
+                              as one op: x is read once forward; the backward
+                              runs K3's reduction, K2 and K1 (with grad_W) and
+                              returns one grad_x.  MHCLiteBlock uses it unless
+                              FLASH_MHC_FUSED_PREMAP=0 (or FLASH_MHC_FUSED_K2=0).
 """
 
 from __future__ import annotations
@@ -60,6 +65,14 @@ _lib.define(
 )
 _lib.define(
     "mhc_coefficients_backward(Tensor? grad_h_pre, Tensor? grad_h_post, Tensor? grad_H_merged, Tensor proj, Tensor alpha_pre, Tensor alpha_post, Tensor alpha_res, Tensor bias, Tensor perm_mat) -> (Tensor grad_proj, Tensor grad_alpha_pre, Tensor grad_alpha_post, Tensor grad_alpha_res, Tensor grad_bias)"
+)
+
+# Not in the reference: the pre-map region (K1 + K2 + K3) as one op.
+_lib.define(
+    "mhc_pre_map(Tensor x_streams, Tensor W, Tensor alpha_pre, Tensor alpha_post, Tensor alpha_res, Tensor bias, Tensor perm_mat) -> (Tensor layer_input, Tensor H_merged, Tensor h_post, Tensor h_pre, Tensor proj, Tensor inv_rms)"
+)
+_lib.define(
+    "mhc_pre_map_backward(Tensor? grad_layer_input, Tensor? grad_H_merged, Tensor? grad_h_post, Tensor? grad_h_pre, Tensor? grad_proj, Tensor x_streams, Tensor W, Tensor alpha_pre, Tensor alpha_post, Tensor alpha_res, Tensor bias, Tensor perm_mat, Tensor h_pre, Tensor proj, Tensor inv_rms) -> (Tensor grad_x, Tensor grad_W, Tensor grad_alpha_pre, Tensor grad_alpha_post, Tensor grad_alpha_res, Tensor grad_bias)"
 )
 
 _lib.define("fused_pre_map(Tensor x_streams, Tensor h_pre) -> Tensor out")
@@ -135,6 +148,23 @@ def _mhc_coefficients_backward_fake(grad_h_pre, grad_h_post, grad_H_merged, proj
                                     alpha_post, alpha_res, bias, perm_mat):
     return (torch.empty_like(proj), torch.empty_like(alpha_pre), torch.empty_like(alpha_post),
             torch.empty_like(alpha_res), torch.empty_like(bias))
+
+
+@torch.library.register_fake("flash_mhc::mhc_pre_map")
+def _mhc_pre_map_fake(x_streams, W, alpha_pre, alpha_post, alpha_res, bias, perm_mat):
+    T, n, C = x_streams.shape
+    f32 = torch.float32
+    return (x_streams.new_empty((T, C)), x_streams.new_empty((T, n, n), dtype=f32),
+            x_streams.new_empty((T, n), dtype=f32), x_streams.new_empty((T, n), dtype=f32),
+            x_streams.new_empty((T, W.shape[0])), x_streams.new_empty((T,), dtype=f32))
+
+
+@torch.library.register_fake("flash_mhc::mhc_pre_map_backward")
+def _mhc_pre_map_backward_fake(grad_layer_input, grad_H_merged, grad_h_post, grad_h_pre, grad_proj,
+                               x_streams, W, alpha_pre, alpha_post, alpha_res, bias, perm_mat, h_pre,
+                               proj, inv_rms):
+    return (torch.empty_like(x_streams), torch.empty_like(W), torch.empty_like(alpha_pre),
+            torch.empty_like(alpha_post), torch.empty_like(alpha_res), torch.empty_like(bias))
 
 
 @torch.library.register_fake("flash_mhc::fused_pre_map")
@@ -225,6 +255,45 @@ def _mhc_coefficients_backward_cuda(grad_h_pre, grad_h_post, grad_H_merged, proj
             gb.to(bias.dtype))
 
 
+@torch.library.impl(_lib, "mhc_pre_map", "CUDA")
+def _mhc_pre_map_cuda(x_streams, W, alpha_pre, alpha_post, alpha_res, bias, perm_mat):
+    _check_n4(x_streams, "flash_mhc::mhc_pre_map supports n=4 only")
+    _check_k2(x_streams.new_empty((0, W.shape[0])), perm_mat)
+    return _k.premap_fwd(x_streams.contiguous(), W.to(x_streams.dtype).contiguous(), _coeff(alpha_pre),
+                         _coeff(alpha_post), _coeff(alpha_res), _coeff(bias), _coeff(perm_mat))
+
+
+@torch.library.impl(_lib, "mhc_pre_map_backward", "CUDA")
+def _mhc_pre_map_backward_cuda(grad_layer_input, grad_H_merged, grad_h_post, grad_h_pre, grad_proj,
+                               x_streams, W, alpha_pre, alpha_post, alpha_res, bias, perm_mat, h_pre,
+                               proj, inv_rms):
+    _check_n4(x_streams, "flash_mhc::mhc_pre_map_backward supports n=4 only")
+    x = x_streams.contiguous()
+    T, n, C = x.shape
+    Wc = W.to(x.dtype).contiguous()
+    coeffs = [_coeff(t) for t in (alpha_pre, alpha_post, alpha_res, bias, perm_mat)]
+    g_li = (torch.zeros((T, C), device=x.device, dtype=x.dtype) if grad_layer_input is None
+            else grad_layer_input.to(x.dtype).contiguous())
+    g_hp = None if grad_h_post is None else _coeff(grad_h_post)
+    g_H = None if grad_H_merged is None else _coeff(grad_H_merged)
+    if grad_h_pre is None and grad_proj is None:
+        # One launch sequence: K3's reduction, K2, K1 with K3's term in its store.
+        gx, gW, ga1, ga2, ga3, gb = _k.premap_bwd(x, Wc, *coeffs, h_pre.contiguous(), proj.contiguous(),
+                                                  inv_rms.contiguous(), g_li, g_hp, g_H)
+    else:
+        # Gradients also flow into the h_pre / proj outputs: compose the ops.
+        gx3, gh = _k.k3_bwd(g_li, x, h_pre.contiguous())
+        if grad_h_pre is not None:
+            gh = gh + grad_h_pre.float()
+        gp, ga1, ga2, ga3, gb = _k.k2_bwd(proj.contiguous(), *coeffs, gh, g_hp, g_H)
+        if grad_proj is not None:
+            gp = (gp.float() + grad_proj.float()).to(gp.dtype)
+        gx1, gW = _k.k1_bwd(gp, x.view(T, n * C), Wc, proj.contiguous(), inv_rms.contiguous())
+        gx = gx3 + gx1.view(T, n, C)
+    return (gx, gW.to(W.dtype), ga1.to(alpha_pre.dtype), ga2.to(alpha_post.dtype),
+            ga3.to(alpha_res.dtype), gb.to(bias.dtype))
+
+
 @torch.library.impl(_lib, "fused_pre_map", "CUDA")
 def _fused_pre_map_cuda(x_streams: torch.Tensor, h_pre: torch.Tensor):
     _check_n4(x_streams, "flash_mhc::fused_pre_map currently supports n=4 only")
@@ -274,6 +343,12 @@ def _fused_dw_enabled() -> bool:
 def fused_k2_enabled() -> bool:
     """MHCLiteBlock runs K2 as flash_mhc::mhc_coefficients unless FLASH_MHC_FUSED_K2=0."""
     return _env_flag("FLASH_MHC_FUSED_K2")
+
+
+def fused_premap_enabled() -> bool:
+    """MHCLiteBlock runs K1 + K2 + K3 as flash_mhc::mhc_pre_map unless
+    FLASH_MHC_FUSED_PREMAP=0 or FLASH_MHC_FUSED_K2=0."""
+    return _env_flag("FLASH_MHC_FUSED_PREMAP") and fused_k2_enabled()
 
 
 def _fused_rmsnorm_project_backward(ctx, grad_out, grad_inv_rms):
@@ -327,6 +402,28 @@ torch.library.register_autograd(
     "flash_mhc::mhc_coefficients",
     _mhc_coefficients_backward,
     setup_context=_setup_inputs,
+)
+def _setup_pre_map(ctx, inputs, output):
+    _li, _H, _hp, h_pre, proj, inv_rms = output
+    ctx.save_for_backward(*inputs, h_pre, proj, inv_rms)
+    # Outputs nobody differentiates (h_pre, proj, inv_rms in the block) arrive
+    # as None rather than as zero tensors.
+    ctx.set_materialize_grads(False)
+
+
+def _mhc_pre_map_backward(ctx, g_li, g_H, g_hp, g_hpre, g_proj, _g_inv_rms):
+    # inv_rms is not differentiable, as K1's in the reference.
+    x, W, ap, apo, ar, b, perm, h_pre, proj, inv_rms = ctx.saved_tensors
+    grads = torch.ops.flash_mhc.mhc_pre_map_backward(
+        g_li, g_H, g_hp, g_hpre, g_proj, x, W, ap, apo, ar, b, perm, h_pre, proj, inv_rms
+    )
+    return (*grads, None)
+
+
+torch.library.register_autograd(
+    "flash_mhc::mhc_pre_map",
+    _mhc_pre_map_backward,
+    setup_context=_setup_pre_map,
 )
 torch.library.register_autograd(
     "flash_mhc::fused_pre_map",

@@ -108,6 +108,39 @@ int fmhc_k2_bwd(const uint16_t* proj, const float* alpha_pre, const float* alpha
                 int64_t T, int64_t n, void* stream);
 /* Workspace bytes fmhc_k2_bwd needs for T tokens.  No counterpart in the reference. */
 int64_t fmhc_k2_bwd_workspace_bytes(int64_t T);
+/* Pre-map forward: K1, K2 and K3 of the same tokens (fmhc_k1_fwd, fmhc_k2_fwd,
+ * fmhc_k3_fwd in order, on `stream`).  Outputs: layer_input (T, C) bf16,
+ * proj (T, 32) bf16, inv_rms (T,) fp32, h_pre, h_post (T, 4) and
+ * H_merged (T, 4, 4) fp32 (16-byte aligned).  x (T, n, C) bf16, W (32, n C)
+ * bf16, alphas / bias / perm as fmhc_k2_fwd; n must be 4.
+ * Replaces: src/flash_mhc/block.py:157-177 (_mhc_pre_map_triton: the K1 launch,
+ *           the K2 PyTorch ops and the K3 launch). */
+int fmhc_premap_fwd(const uint16_t* x, const uint16_t* W, const float* alpha_pre,
+                    const float* alpha_post, const float* alpha_res, const float* bias,
+                    const float* perm, uint16_t* layer_input, uint16_t* proj, float* inv_rms,
+                    float* h_pre, float* h_post, float* H_merged, int64_t T, int64_t C, int64_t n,
+                    void* stream);
+/* Pre-map backward: the gradients of fmhc_premap_fwd's inputs from those of
+ * layer_input (T, C) bf16, h_post (T, 4) and H_merged (T, 4, 4) fp32 (the
+ * latter two may be NULL: zero):
+ *   grad_x = bf16(K3's h_pre[t,j] * grad_layer_input[t,c] + K1's dx)
+ *            (each term rounded to bf16 first, as autograd sums them),
+ *   grad_W (32, n C) bf16 as fmhc_k1_bwd, the alpha / bias gradients as
+ *   fmhc_k2_bwd.
+ * h_pre, proj, inv_rms are fmhc_premap_fwd's outputs.  `workspace`: at least
+ * fmhc_premap_bwd_workspace_bytes(T, C) bytes, 16-byte aligned.
+ * Replaces: autograd through src/flash_mhc/block.py:157-177 (the K3, K2 and K1
+ *           backward launches, and the addition of x's two gradients). */
+int fmhc_premap_bwd(const uint16_t* x, const uint16_t* W, const float* alpha_pre,
+                    const float* alpha_post, const float* alpha_res, const float* bias,
+                    const float* perm, const float* h_pre, const uint16_t* proj, const float* inv_rms,
+                    const uint16_t* grad_layer_input, const float* grad_h_post,
+                    const float* grad_H_merged, uint16_t* grad_x, uint16_t* grad_W,
+                    float* grad_alpha_pre, float* grad_alpha_post, float* grad_alpha_res,
+                    float* grad_bias, void* workspace, int64_t workspace_bytes, int64_t T, int64_t C,
+                    int64_t n, void* stream);
+/* Workspace bytes fmhc_premap_bwd needs.  No counterpart in the reference. */
+int64_t fmhc_premap_bwd_workspace_bytes(int64_t T, int64_t C);
 /* K3 forward: out[t,c] = bf16(sum_j h_pre[t,j] * x[t,j,c]), j = 0..3 in order.
  * x (T, n, C) bf16; h_pre (T, n) fp32; out (T, C) bf16.
  * Replaces: src/flash_mhc/ops.py:347-414 (_fused_pre_map_cuda) launching
@@ -119,6 +152,8 @@ int fmhc_k3_fwd(const uint16_t* x, const float* h_pre, uint16_t* out,
  *   grad_x[t,j,c]   = bf16(h_pre[t,j] * go[t,c])
  *   grad_h_pre[t,j] = sum_c x[t,j,c] * go[t,c]              (fp32)
  * grad_out (T, C) bf16; grad_x (T, n, C) bf16; grad_h_pre (T, n) fp32.
+ * grad_x may be NULL: then only grad_h_pre is computed (no counterpart in the
+ * reference; the pre-map backward folds h_pre * go into K1's grad_x store).
  * Replaces: src/flash_mhc/ops.py:417-493 (_fused_pre_map_backward_cuda) launching
  *           src/flash_mhc/kernels.py:720-853 (_fused_pre_map_bwd_fused_kernel_n4). */
 int fmhc_k3_bwd(const uint16_t* x, const float* h_pre, const uint16_t* grad_out,

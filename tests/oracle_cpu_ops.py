@@ -55,6 +55,27 @@ def _k2_bwd(g_hpre, g_hpost, g_H, proj, ap, apo, ar, b, perm):
             par("grad_bias", b))
 
 
+def _pre_map(x, W, ap, apo, ar, b, perm):
+    T, n, C = x.shape
+    proj, inv = _k1(x.reshape(T, n * C), W.to(x.dtype))
+    h_pre, h_post, H = _k2(proj, ap, apo, ar, b, perm)
+    return _k3(x, h_pre), H, h_post, h_pre, proj, inv
+
+
+def _pre_map_bwd(g_li, g_H, g_hp, g_hpre, g_proj, x, W, ap, apo, ar, b, perm, h_pre, proj, inv):
+    T, n, C = x.shape
+    if g_li is None:
+        g_li = torch.zeros(T, C, dtype=x.dtype)
+    gx3, gh = _k3_bwd(g_li, x, h_pre)
+    if g_hpre is not None:
+        gh = gh + g_hpre.float()
+    gp, ga1, ga2, ga3, gb = _k2_bwd(gh, g_hp, g_H, proj, ap, apo, ar, b, perm)
+    if g_proj is not None:
+        gp = (gp.float() + g_proj.float()).to(gp.dtype)
+    gx1, gW = _k1_bwd(gp, x.reshape(T, n * C), W.to(x.dtype), proj, inv)
+    return gx3 + gx1.view(T, n, C), gW.to(W.dtype), ga1, ga2, ga3, gb
+
+
 def _k3(x, h):
     if x.shape[1] != 4:
         raise ValueError("flash_mhc::fused_pre_map currently supports n=4 only")
@@ -84,6 +105,8 @@ IMPLS = {
     "fused_rmsnorm_project_bwd": _k1_bwd,
     "mhc_coefficients": _k2,
     "mhc_coefficients_backward": _k2_bwd,
+    "mhc_pre_map": _pre_map,
+    "mhc_pre_map_backward": _pre_map_bwd,
     "fused_pre_map": _k3,
     "fused_pre_map_backward": _k3_bwd,
     "fused_post_res": _k4,

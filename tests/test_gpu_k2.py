@@ -116,8 +116,10 @@ def test_k2_deterministic():
 
 
 def _block_run(flag, T, C, seed=50):
-    old = os.environ.get("FLASH_MHC_FUSED_K2")
+    # K2 alone: the one-pass pre-map (which also fuses K1 and K3) stays off.
+    old = {k: os.environ.get(k) for k in ("FLASH_MHC_FUSED_K2", "FLASH_MHC_FUSED_PREMAP")}
     os.environ["FLASH_MHC_FUSED_K2"] = flag
+    os.environ["FLASH_MHC_FUSED_PREMAP"] = "0"
     try:
         torch.manual_seed(seed)
         layer = torch.nn.Linear(C, C, bias=False).to(BF16)
@@ -134,10 +136,11 @@ def _block_run(flag, T, C, seed=50):
         torch.cuda.synchronize()
         return out.detach(), x.grad, {n: p.grad for n, p in blk.named_parameters()}
     finally:
-        if old is None:
-            os.environ.pop("FLASH_MHC_FUSED_K2", None)
-        else:
-            os.environ["FLASH_MHC_FUSED_K2"] = old
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
 
 
 def test_block_fused_k2_equals_reference_ops():

@@ -60,6 +60,8 @@ ADDED_SCHEMAS = {
     "fused_rmsnorm_project_bwd": "fused_rmsnorm_project_bwd(Tensor grad_out, Tensor x_flat, Tensor W, Tensor proj_out, Tensor inv_rms) -> (Tensor grad_x, Tensor grad_W)",
     "mhc_coefficients": "mhc_coefficients(Tensor proj, Tensor alpha_pre, Tensor alpha_post, Tensor alpha_res, Tensor bias, Tensor perm_mat) -> (Tensor h_pre, Tensor h_post, Tensor H_merged)",
     "mhc_coefficients_backward": "mhc_coefficients_backward(Tensor? grad_h_pre, Tensor? grad_h_post, Tensor? grad_H_merged, Tensor proj, Tensor alpha_pre, Tensor alpha_post, Tensor alpha_res, Tensor bias, Tensor perm_mat) -> (Tensor grad_proj, Tensor grad_alpha_pre, Tensor grad_alpha_post, Tensor grad_alpha_res, Tensor grad_bias)",
+    "mhc_pre_map": "mhc_pre_map(Tensor x_streams, Tensor W, Tensor alpha_pre, Tensor alpha_post, Tensor alpha_res, Tensor bias, Tensor perm_mat) -> (Tensor layer_input, Tensor H_merged, Tensor h_post, Tensor h_pre, Tensor proj, Tensor inv_rms)",
+    "mhc_pre_map_backward": "mhc_pre_map_backward(Tensor? grad_layer_input, Tensor? grad_H_merged, Tensor? grad_h_post, Tensor? grad_h_pre, Tensor? grad_proj, Tensor x_streams, Tensor W, Tensor alpha_pre, Tensor alpha_post, Tensor alpha_res, Tensor bias, Tensor perm_mat, Tensor h_pre, Tensor proj, Tensor inv_rms) -> (Tensor grad_x, Tensor grad_W, Tensor grad_alpha_pre, Tensor grad_alpha_post, Tensor grad_alpha_res, Tensor grad_bias)",
 }
 
 
@@ -201,7 +203,13 @@ def test_opcheck_all_ops(cpu_kernels):
          (proj.clone().requires_grad_(True), *[t.clone().requires_grad_(True) for t in k2p], perm)),
         (torch.ops.flash_mhc.mhc_coefficients_backward.default,
          (hp, None, H, proj, *k2p, perm)),
+        (torch.ops.flash_mhc.mhc_pre_map.default,
+         (x.clone().requires_grad_(True), W.clone().requires_grad_(True),
+          *[t.clone().requires_grad_(True) for t in k2p], perm)),
     ]
+    li, H2, hq2, hp2, proj2, inv2 = torch.ops.flash_mhc.mhc_pre_map(x, W, *k2p, perm)
+    cases.append((torch.ops.flash_mhc.mhc_pre_map_backward.default,
+                  (rnd((T, C), 22), H, hp, None, None, x, W, *k2p, perm, hp2, proj2, inv2)))
     for op, args in cases:
         torch.library.opcheck(op, args)
 
@@ -291,6 +299,7 @@ def test_fused_k2_matches_reference_chain_on_cpu(cpu_kernels, monkeypatch):
 
     def run(flag):
         monkeypatch.setenv("FLASH_MHC_FUSED_K2", flag)
+        monkeypatch.setenv("FLASH_MHC_FUSED_PREMAP", "0")
         blk = _block(C=32)
         with torch.no_grad():
             blk.alpha_pre.fill_(0.8)
@@ -313,3 +322,38 @@ def test_fused_k2_matches_reference_chain_on_cpu(cpu_kernels, monkeypatch):
     for n in gp0:
         torch.testing.assert_close(gp1[n].float(), gp0[n].float(), rtol=5e-2,
                                    atol=2e-2 * float(gp0[n].float().abs().max()) + 1e-6, msg=n)
+
+
+@pytest.mark.parametrize("premap", ["1", "0"])
+def test_fused_premap_matches_separate_ops_on_cpu(cpu_kernels, monkeypatch, premap):
+    """The block with K1 + K2 + K3 as one op (FLASH_MHC_FUSED_PREMAP=1) and as
+    three ops (=0) gives identical outputs and parameter gradients, with and
+    without activation checkpointing.  grad_x is the bf16 sum of x's three
+    gradients (from K4, K3, K1): the separate ops let autograd add them as
+    (g4 + g3) + g1, the fused op returns g3 + g1 to which autograd adds g4, so
+    the two may differ by a last bit of the sum."""
+    from parity import check_chain
+
+    def run(flag, ckpt):
+        monkeypatch.setenv("FLASH_MHC_FUSED_PREMAP", flag)
+        blk = _block(C=32)
+        blk.activation_checkpointing = ckpt
+        with torch.no_grad():
+            blk.alpha_pre.fill_(0.8)
+            blk.alpha_post.fill_(1.2)
+            blk.alpha_res.fill_(1.7)
+        x = rnd((64, 4, 32), 43).requires_grad_(True)
+        out = blk._forward_triton(x)
+        out.float().pow(2).sum().backward()
+        return out.detach(), x.grad, {n: p.grad for n, p in blk.named_parameters()}
+
+    ref = run("0", False)
+    for ckpt in (False, True):
+        o, gx, gp = run(premap, ckpt)
+        assert torch.equal(o, ref[0])
+        if premap == "0":
+            assert torch.equal(gx, ref[1])
+        else:
+            check_chain("grad_x", gx.float(), ref[1].float(), max_rate=1.0)
+        for n in gp:
+            assert torch.equal(gp[n], ref[2][n]), n
