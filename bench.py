@@ -7,8 +7,12 @@ input resident in HBM (the kernel microbenchmark of the reference's
 scripts/benchmark_kernels.py, with its mandatory-bytes model, :64-105).
 
 Prints ONE JSON line.  ``value`` = sum of the six kernels' algorithmic bytes /
-measured step time.  ``roofline`` describes the dominant kernel (largest
-average duration), timed with HIP events on the stream it runs on.
+measured step time (K steps of bare launches between two events).  Per-kernel
+durations come from a second pass of K steps with an event pair around each
+launch; ``roofline`` describes the dominant kernel (largest average duration),
+timed with those HIP events on the stream it runs on.  Extra fields report
+K1's full backward (fused grad_W vs the reference's matmul) and a whole
+MHCLiteBlock forward + backward with the fused path vs the reference's rules.
 ``cpu_baseline`` times the reference's PyTorch formulation of the same six ops
 (fp32 autograd, restated in oracle/) on the host's cores, on a bounded token
 sample, reported with the same bytes model.
@@ -152,6 +156,48 @@ def k1_backward_paths(inp: dict, T: int, C: int, iters: int = 20) -> dict:
     return out
 
 
+def block_step(T: int, C: int, iters: int = 10) -> dict:
+    """MHCLiteBlock(4, C, Linear(C, C)) forward + backward (bf16, random
+    weights) with the fused path as shipped, and with the reference's rules
+    (K2 as PyTorch ops, K1's grad_W as a matmul, separate pre-map ops)."""
+    import flash_mhc
+
+    torch.manual_seed(0)
+    blk = flash_mhc.MHCLiteBlock(4, C, torch.nn.Linear(C, C, bias=False)).cuda().bfloat16()
+    x = torch.randn(T, 4, C, device="cuda", dtype=torch.bfloat16).requires_grad_(True)
+    up = torch.randn(T, 4, C, device="cuda", dtype=torch.bfloat16)
+    flags = ("FLASH_MHC_FUSED_K2", "FLASH_MHC_FUSED_DW", "FLASH_MHC_FUSED_PREMAP")
+    saved = {f: os.environ.get(f) for f in flags}
+    out = {}
+    try:
+        for name, val in (("fused", "1"), ("reference_rules", "0")):
+            for f in flags:
+                os.environ[f] = val
+
+            def one():
+                blk.zero_grad(set_to_none=True)
+                x.grad = None
+                blk(x).backward(up)
+
+            for _ in range(3):
+                one()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(iters):
+                one()
+            e1.record()
+            torch.cuda.synchronize()
+            out[name + "_ms"] = round(e0.elapsed_time(e1) / iters, 3)
+    finally:
+        for f, v in saved.items():
+            if v is None:
+                os.environ.pop(f, None)
+            else:
+                os.environ[f] = v
+    out["workload"] = f"MHCLiteBlock(4, {C}, Linear({C}, {C})) forward + backward, T={T}, bf16"
+    return out
+
+
 def read_write_split(T: int, n: int, C: int, D: int) -> dict[str, tuple[int, int]]:
     """(bytes read, bytes written) per launch; sums to bytes_model."""
     bf, f4 = 2, 4
@@ -262,6 +308,8 @@ def main() -> None:
     ap.add_argument("--C", type=int, default=1024)
     ap.add_argument("--cpu-tokens", type=int, default=8192)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the K1-backward and block-step fields (profiler runs: only the six kernels)")
     ap.add_argument("--traffic", type=str, default=str(ROOT / "profiles" / "traffic_k4_bwd_T65536_C1024.json"),
                     help="measured HBM traffic summary (rocprofv3 --pmc) for the dominant kernel")
     args = ap.parse_args()
@@ -296,21 +344,29 @@ def main() -> None:
         step()
     torch.cuda.synchronize()
 
+    # Timed region: exactly K steps, nothing but the six launches per step.
     K_steps = args.steps
-    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in KERNELS]
-           for _ in range(K_steps)]
     torch.cuda.synchronize()
     t_start = time.perf_counter()
     s0 = torch.cuda.Event(enable_timing=True)
     s1 = torch.cuda.Event(enable_timing=True)
     s0.record()
     for k in range(K_steps):
-        step(evs[k])
+        step()
     s1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_start
     ms_total = s0.elapsed_time(s1)
     ms_per_step = ms_total / K_steps
+
+    # Per-kernel durations: a second pass of K steps with an event pair around
+    # each launch on the launch stream (events between launches would add
+    # their own gaps to the step above).
+    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in KERNELS]
+           for _ in range(K_steps)]
+    for k in range(K_steps):
+        step(evs[k])
+    torch.cuda.synchronize()
 
     per = {}
     for i, name in enumerate(KERNELS):
@@ -338,7 +394,8 @@ def main() -> None:
         except (OSError, ValueError):
             traffic = None
 
-    k1_full_bwd = k1_backward_paths(inp, T, C)
+    k1_full_bwd = None if args.no_extras else k1_backward_paths(inp, T, C)
+    blk = None if args.no_extras else block_step(T, C)
     ceil = stream_ceilings()
     split = read_write_split(T, n, C, D)
     for name in KERNELS:
@@ -369,6 +426,7 @@ def main() -> None:
         "sum_kernel_ms": round(sum_kernel_ms, 4),
         "ceilings_GBps": ceil,
         "k1_backward_with_grad_W": k1_full_bwd,
+        "block_step": blk,
         "kernels": per,
         "roofline": {
             "kernel": dom,
