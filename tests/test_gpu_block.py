@@ -295,3 +295,32 @@ def test_activation_checkpointing_same_grads():
     assert torch.equal(g0, g1)
     for n in p0:
         assert torch.equal(p0[n], p1[n]), n
+
+
+@pytest.mark.parametrize("T", [1, 64, 4096])
+def test_graph_capture_eval_forward(T):
+    """The fused block's eval forward (K1, K2, K3 on the pre-map op, the layer,
+    K4) can be captured in a HIP graph: every replay, with eager work and
+    synchronisations between replays, equals the eager forward."""
+    C = 1024
+    torch.manual_seed(3)
+    blk = flash_mhc.MHCLiteBlock(4, C, torch.nn.Linear(C, C, bias=False)).to(DEV, BF16).eval()
+    x = randn((T, 4, C), 70 + T, dtype=BF16).to(DEV)
+    with torch.no_grad():
+        ref = blk(x).clone()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(2):
+                blk(x)
+        torch.cuda.current_stream().wait_stream(s)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            out = blk(x)
+        for i in range(4):
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, ref), f"replay {i}"
+            eager = blk(x)  # eager work between replays
+            torch.cuda.synchronize()
+            assert torch.equal(eager, ref)
