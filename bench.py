@@ -17,7 +17,7 @@ MHCLiteBlock forward + backward with the fused path vs the reference's rules.
 (fp32 autograd, restated in oracle/) on the host's cores, on a bounded token
 sample, reported with the same bytes model.
 
-Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--T 65536] [--C 1024]
+Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--T 65536] [--C 1024]
 """
 
 from __future__ import annotations
@@ -302,8 +302,8 @@ def cpu_baseline(C: int, tokens: int, iters: int = 3) -> dict:
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--T", type=int, default=65536)
     ap.add_argument("--C", type=int, default=1024)
     ap.add_argument("--cpu-tokens", type=int, default=8192)
