@@ -45,6 +45,12 @@ __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
 // squares also runs on the matrix cores: the same x registers are both A and
 // B of a third MFMA, G (16 x 16) += x x^T, whose diagonal is sum_k x[t,k]^2
 // in fp32 (the bf16 products are exact).
+//
+// The MFMA operand layout puts 16 tokens x 64 bytes in one register, i.e.
+// half of each 128-byte line per load instruction.  Loading that layout
+// directly from HBM is 3% slower than loading whole lines (8 tokens x 128
+// bytes per instruction) and moving them into the MFMA layout through a
+// wave-private LDS tile (16R tokens x 128 bytes).
 template <int R>
 struct FwdFrag {
   u32x4 wa[2], wb[2];  // W rows 0-15 / 16-31, two 32-wide k steps
@@ -59,6 +65,7 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
                                                              int64_t T, int nC) {
   __shared__ float red_acc[SPLIT][R][8][kWave];
   __shared__ float red_ss[SPLIT][R][16];
+  __shared__ u32x4 xs[SPLIT][16 * R * 8];  // per wave: 16R tokens x 8 swizzled 16-byte slots
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
@@ -66,13 +73,25 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
   const int grp = lane >> 4;
   const int64_t t0 = static_cast<int64_t>(blockIdx.x) * (16 * R);
 
-  const uint16_t* xrow[R];
+  // Full-line loads: instruction j (0 .. 2R-1) covers tokens 8j .. 8j+7 of the
+  // workgroup, lane l the 16-byte slot l & 7 of token 8j + (l >> 3).  Tail
+  // rows re-read the last token; their results are not stored.
+  const uint16_t* xw = x + t0 * nC;
+  const int64_t rem = T - 1 - t0;
+  const int tmax = rem < 16 * R ? static_cast<int>(rem) : 16 * R - 1;
+  uint32_t xoff[2 * R];
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    int64_t t = t0 + 16 * r + row;
-    t = t < T ? t : T - 1;  // tail rows re-read the last token; their results are not stored
-    xrow[r] = x + t * nC + 8 * grp;
+  for (int j = 0; j < 2 * R; ++j) {
+    const int tl = 8 * j + (lane >> 3);
+    xoff[j] = static_cast<uint32_t>(tl < tmax ? tl : tmax) * static_cast<uint32_t>(nC) + 8u * (lane & 7);
   }
+  // LDS slots are swizzled (slot ^ ((token >> 1) & 7)) so that the row writes
+  // and the MFMA-layout reads are free of bank conflicts.
+  u32x4* xl = xs[wave];
+  const int wr0 = (lane >> 3) * 8 + ((lane & 7) ^ (lane >> 4));
+  const int wr1 = (lane >> 3) * 8 + ((lane & 7) ^ (4 + (lane >> 4)));
+  const int rd0 = row * 8 + (grp ^ ((row >> 1) & 7));
+  const int rd1 = row * 8 + ((4 + grp) ^ ((row >> 1) & 7));
   const uint16_t* w0 = W + static_cast<int64_t>(row) * nC + 8 * grp;
   const uint16_t* w1 = W + static_cast<int64_t>(16 + row) * nC + 8 * grp;
 
@@ -90,9 +109,10 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
   // concurrent reads of all workgroups over the DRAM channels instead of every
   // workgroup hitting the same column of its 8 KiB-strided rows), and
   // double-buffers: the next chunk's fragments are loaded while the MFMAs of
-  // the current one run.  x uses ordinary loads here: each load instruction
-  // covers half of a 128-byte line and the other half follows one
-  // instruction later, which the nontemporal hint would evict in between.
+  // the current one run.  x uses ordinary loads: with the nontemporal hint
+  // this kernel alone is 10% faster, but K3's forward, which reads x next,
+  // loses as much, because it no longer finds the tail of x in the
+  // memory-side cache.
   const int nfull = nC >> 6;
   const int rot = nfull > 0 ? static_cast<int>(blockIdx.x % static_cast<unsigned>(nfull)) : 0;
   FwdFrag<R> f0, f1;
@@ -104,8 +124,19 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
       f.wa[s] = *reinterpret_cast<const u32x4*>(w0 + k + 32 * s);
       f.wb[s] = *reinterpret_cast<const u32x4*>(w1 + k + 32 * s);
 #pragma unroll
-      for (int r = 0; r < R; ++r) f.xv[s][r] = *reinterpret_cast<const u32x4*>(xrow[r] + k + 32 * s);
+      for (int r = 0; r < R; ++r) f.xv[s][r] = *reinterpret_cast<const u32x4*>(xw + xoff[s * R + r] + k);
     }
+  };
+  // Token rows -> MFMA layout (lane: token row, 8 consecutive k) through the
+  // wave's LDS tile.  Same-wave LDS operations complete in order, so the
+  // next chunk's writes cannot overtake these reads.
+  auto transpose = [&](FwdFrag<R>& f) {
+#pragma unroll
+    for (int j = 0; j < 2 * R; ++j) xl[64 * j + ((j & 1) ? wr1 : wr0)] = f.xv[j / R][j % R];
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int r = 0; r < R; ++r) f.xv[s][r] = xl[128 * r + (s ? rd1 : rd0)];
   };
   auto compute = [&](const FwdFrag<R>& f) {
 #pragma unroll
@@ -130,12 +161,17 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
     for (; i + 1 < n; i += 2) {
       load(f1, pos(i + 1));
       __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the MFMAs
+      transpose(f0);
       compute(f0);
       load(f0, pos(i + 2));
       __builtin_amdgcn_sched_barrier(0);
+      transpose(f1);
       compute(f1);
     }
-    if (i < n) compute(f0);
+    if (i < n) {
+      transpose(f0);
+      compute(f0);
+    }
   }
   // Ragged last chunk (nC % 64 != 0): 16-byte pieces past nC contribute zero.
   if ((nC & 63) != 0 && wave == nfull % SPLIT) {
@@ -150,7 +186,11 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
         f0.wa[s] = *reinterpret_cast<const u32x4*>(w0 + k + 32 * s);
         f0.wb[s] = *reinterpret_cast<const u32x4*>(w1 + k + 32 * s);
 #pragma unroll
-        for (int r = 0; r < R; ++r) f0.xv[s][r] = *reinterpret_cast<const u32x4*>(xrow[r] + k + 32 * s);
+        for (int r = 0; r < R; ++r) {
+          int64_t t = t0 + 16 * r + row;
+          t = t < T ? t : T - 1;
+          f0.xv[s][r] = *reinterpret_cast<const u32x4*>(x + t * nC + 8 * grp + k + 32 * s);
+        }
       }
     }
     compute(f0);
@@ -643,7 +683,9 @@ extern "C" int fmhc_k1_fwd(const uint16_t* x_flat, const uint16_t* W, uint16_t* 
   if (!x_flat || !W || !out || !inv_rms) return FMHC_ERR_INVALID_ARGUMENT;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int nc = static_cast<int>(nC);
-  if (nC % 8 == 0 && aligned16(x_flat) && aligned16(W) && aligned16(out)) {
+  // The MFMA kernel addresses a workgroup's 16 R rows of x with 32-bit
+  // element offsets.
+  if (nC % 8 == 0 && nC <= (int64_t{1} << 24) && aligned16(x_flat) && aligned16(W) && aligned16(out)) {
     const dim3 grid(blocks_for(T, 16 * kFwdR));
     k1_fwd_mfma<kFwdR, kFwdSplit><<<grid, kWave * kFwdSplit, 0, s>>>(x_flat, W, out, inv_rms, T, nc);
   } else {
