@@ -251,13 +251,14 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
 // instruction covers 4 token rows x 256 contiguous bytes (whole cache lines).
 // The B tiles depend only on the slice, so each wave builds them once: eight
 // 16-byte loads of W rows and an 8 x 8 bf16 transpose in registers.
-template <bool EPI>
+template <bool EPI, bool GI>
 struct BwdFrag {
   u32x4 gv, pv;   // go / proj_out row of token tbase + col, d = 8 * grp .. + 8
   float inv[4];   // inv_rms of tokens tbase + 4 * grp + q
   u32x4 xv[4];    // x of those tokens, k = kl .. kl + 8
   u32x4 g3[EPI ? 4 : 1];  // EPI: the K3 output gradient of those tokens at the lane's c
   float hp[EPI ? 4 : 1];  // EPI: their h_pre of the lane's stream j
+  u32x4 gi[GI ? 4 : 1];   // GI: x's incoming gradient at the lane's 8 k
 };
 
 // With DW = true the same pass also accumulates the weight gradient
@@ -275,7 +276,14 @@ struct BwdFrag {
 // x's gradient, grad_x = bf16(bf16(h_pre[t, j] go3[t, c]) + bf16(dx)), k = j C + c:
 // the bf16 sum autograd forms when K3 and K1 are separate ops.  The B tiles
 // then live in LDS so that the extra operands keep two waves per SIMD.
-template <int NTB, bool DW, bool FULLK, bool EPI>
+//
+// With GI = true (EPI only) the store also adds an incoming gradient of x (the
+// post-res op's H_merged^T grad_out): grad_x = bf16(gi + bf16(pre-map term)),
+// the value autograd's accumulation of x's gradients gives.  The extra
+// operand takes the kernel to one wave per SIMD; it is still bound by HBM
+// (measured: +80 us at T=65536, C=1024 for the 512 MiB it reads, against
+// 260 us for the separate accumulation pass it replaces).
+template <int NTB, bool DW, bool FULLK, bool EPI, bool GI>
 __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ x,
                                                    const uint16_t* __restrict__ W,
                                                    const uint16_t* __restrict__ go,
@@ -285,6 +293,7 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
                                                    float* __restrict__ dw_partial,
                                                    const uint16_t* __restrict__ go3,
                                                    const float* __restrict__ h_pre,
+                                                   const uint16_t* __restrict__ gi,
                                                    int64_t T, int nC, int nslices, int C) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
@@ -366,7 +375,7 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
   auto block_base = [&](int tb) { return (run + static_cast<int64_t>(tb) * nruns) * 16; };
   // Valid rows of the block starting at tbase (16 except in the last block).
   auto block_rows = [&](int64_t tbase) { return static_cast<int>(T - tbase < 16 ? T - tbase : 16); };
-  auto load = [&](BwdFrag<EPI>& f, int tb) {
+  auto load = [&](BwdFrag<EPI, GI>& f, int tb) {
     const int64_t tbase = block_base(tb);
     const int last = block_rows(tbase) - 1;  // rows past the end re-read the last one
     const int rg = col < last ? col : last;
@@ -392,9 +401,15 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
           f.g3[q] = ld_stream(reinterpret_cast<const u32x4*>(g3b + (r * 2u * static_cast<uint32_t>(C) + c3bytes)));
         }
       }
+      if constexpr (GI) {
+        f.gi[q] = u32x4{0u, 0u, 0u, 0u};
+        if (kok)
+          f.gi[q] = ld_stream(reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(gi + tbase * nC) +
+                                                             (r * row_bytes + kbytes)));
+      }
     }
   };
-  auto compute = [&](const BwdFrag<EPI>& f, int tb) {
+  auto compute = [&](const BwdFrag<EPI, GI>& f, int tb) {
     const int64_t tbase = block_base(tb);
     const int rows = block_rows(tbase);
     // dot(go, proj_out) of token tbase + col, over the four 8-wide d groups.
@@ -432,6 +447,12 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
 #pragma unroll
             for (int m = 0; m < 8; ++m)
               o[m] = bf16_to_f32(f32_to_bf16(f.hp[q] * g3f[m])) + bf16_to_f32(f32_to_bf16(o[m]));
+            if constexpr (GI) {
+              float gif[8];
+              unpack8(f.gi[q], gif);
+#pragma unroll
+              for (int m = 0; m < 8; ++m) o[m] = gif[m] + bf16_to_f32(f32_to_bf16(o[m]));
+            }
           }
           st_stream(reinterpret_cast<u32x4*>(gxb + (static_cast<uint32_t>(r) * row_bytes + kbytes)), pack8(o));
         }
@@ -482,7 +503,7 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
       }
     }
   };
-  BwdFrag<EPI> f0, f1;
+  BwdFrag<EPI, GI> f0, f1;
   load(f0, 0);
   int i = 0;
   for (; i + 1 < nb; i += 2) {
@@ -606,7 +627,8 @@ __global__ __launch_bounds__(256) void k1_fwd_scalar(const uint16_t* __restrict_
   }
 }
 
-// ACC: grad_x already holds the pre-map's K3 term; store bf16(that + bf16(dx)).
+// ACC: grad_x already holds the pre-map's K3 term; store bf16(that + bf16(dx)),
+// and with an incoming gradient gi (may be null) bf16(gi + bf16(that + bf16(dx))).
 template <bool ACC>
 __global__ __launch_bounds__(256) void k1_bwd_scalar(const uint16_t* __restrict__ x,
                                                      const uint16_t* __restrict__ W,
@@ -614,6 +636,7 @@ __global__ __launch_bounds__(256) void k1_bwd_scalar(const uint16_t* __restrict_
                                                      const uint16_t* __restrict__ proj,
                                                      const float* __restrict__ inv_rms,
                                                      uint16_t* __restrict__ gx,
+                                                     const uint16_t* __restrict__ gi,
                                                      int64_t T, int nC) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
@@ -636,9 +659,11 @@ __global__ __launch_bounds__(256) void k1_bwd_scalar(const uint16_t* __restrict_
     for (int d = 0; d < kDout; ++d)
       s = __builtin_fmaf(g[d], bf16_to_f32(W[static_cast<int64_t>(d) * nC + k]), s);
     const float v = inv * s - scale * bf16_to_f32(xr[k]);
-    if constexpr (ACC)
-      gr[k] = f32_to_bf16(bf16_to_f32(gr[k]) + bf16_to_f32(f32_to_bf16(v)));
-    else
+    if constexpr (ACC) {
+      float u = bf16_to_f32(f32_to_bf16(bf16_to_f32(gr[k]) + bf16_to_f32(f32_to_bf16(v))));
+      if (gi) u += bf16_to_f32(gi[t * nC + k]);
+      gr[k] = f32_to_bf16(u);
+    } else
       gr[k] = f32_to_bf16(v);
   }
 }
@@ -659,17 +684,18 @@ bool k1_bwd_mfma_path(const void* x, const void* W, const void* go, const void* 
          aligned16(proj) && aligned16(gx);
 }
 
-template <int NTB, bool DW, bool EPI = false>
+template <int NTB, bool DW, bool EPI = false, bool GI = false>
 void launch_k1_bwd_mfma(dim3 grid, hipStream_t s, const uint16_t* x, const uint16_t* W,
                         const uint16_t* go, const uint16_t* proj, const float* inv_rms, uint16_t* gx,
                         float* partial, int64_t T, int nC, int nslices,
-                        const uint16_t* go3 = nullptr, const float* h_pre = nullptr, int C = 1) {
+                        const uint16_t* go3 = nullptr, const float* h_pre = nullptr, int C = 1,
+                        const uint16_t* gi = nullptr) {
   if (nC % 128 == 0)
-    k1_bwd_mfma<NTB, DW, true, EPI><<<grid, 256, 0, s>>>(x, W, go, proj, inv_rms, gx, partial, go3, h_pre,
-                                                         T, nC, nslices, C);
+    k1_bwd_mfma<NTB, DW, true, EPI, GI><<<grid, 256, 0, s>>>(x, W, go, proj, inv_rms, gx, partial, go3, h_pre,
+                                                             gi, T, nC, nslices, C);
   else
-    k1_bwd_mfma<NTB, DW, false, EPI><<<grid, 256, 0, s>>>(x, W, go, proj, inv_rms, gx, partial, go3, h_pre,
-                                                          T, nC, nslices, C);
+    k1_bwd_mfma<NTB, DW, false, EPI, GI><<<grid, 256, 0, s>>>(x, W, go, proj, inv_rms, gx, partial, go3, h_pre,
+                                                              gi, T, nC, nslices, C);
 }
 
 }  // namespace
@@ -712,7 +738,7 @@ extern "C" int fmhc_k1_bwd_dx(const uint16_t* x_flat, const uint16_t* W, const u
                                        proj_out, inv_rms, grad_x, nullptr, T, nc, nslices);
   } else {
     const dim3 grid(blocks_for(T, 4));
-    k1_bwd_scalar<false><<<grid, 256, 0, s>>>(x_flat, W, grad_out, proj_out, inv_rms, grad_x, T, nc);
+    k1_bwd_scalar<false><<<grid, 256, 0, s>>>(x_flat, W, grad_out, proj_out, inv_rms, grad_x, nullptr, T, nc);
   }
   return launch_status();
 }
@@ -772,36 +798,42 @@ namespace fmhc {
 // K3 term is computed in the store; otherwise grad_x must already hold it
 // (fmhc_k3_bwd's grad_x) and the element-wise kernel adds dx to it.
 bool k1_bwd_premap_fused(const void* x, const void* W, const void* go, const void* proj, const void* gx,
-                         const void* go3, int64_t C) {
-  return C % 8 == 0 && k1_bwd_mfma_path(x, W, go, proj, gx, 4 * C) && aligned16(go3);
+                         const void* go3, const void* gi, int64_t C) {
+  return C % 8 == 0 && k1_bwd_mfma_path(x, W, go, proj, gx, 4 * C) && aligned16(go3) && aligned16(gi);
 }
 
 int k1_bwd_premap(const uint16_t* x_flat, const uint16_t* W, const uint16_t* grad_proj,
                   const uint16_t* proj, const float* inv_rms, const uint16_t* go3, const float* h_pre,
-                  uint16_t* grad_x, uint16_t* grad_W, void* workspace, int64_t workspace_bytes, int64_t T,
-                  int64_t C, hipStream_t s) {
+                  const uint16_t* grad_x_in, uint16_t* grad_x, uint16_t* grad_W, void* workspace,
+                  int64_t workspace_bytes, int64_t T, int64_t C, hipStream_t s) {
   const int64_t nC = 4 * C;
   const int nc = static_cast<int>(nC);
   if (T == 0) {
     k1_dw_zero<<<dim3(blocks_for(static_cast<int64_t>(kDout) * nC, 256)), 256, 0, s>>>(grad_W, nc);
     return launch_status();
   }
-  if (k1_bwd_premap_fused(x_flat, W, grad_proj, proj, grad_x, go3, C)) {
+  if (k1_bwd_premap_fused(x_flat, W, grad_proj, proj, grad_x, go3, grad_x_in, C)) {
     if (!workspace || workspace_bytes < fmhc_k1_bwd_workspace_bytes(T, nC) || !aligned16(workspace))
       return FMHC_ERR_INVALID_ARGUMENT;
     const int nslices = static_cast<int>((nC + 127) / 128);
     const int64_t nruns = k1_bwd_runs(T);
     float* partial = static_cast<float*>(workspace);
-    launch_k1_bwd_mfma<kBwdDwNTB, true, true>(dim3(blocks_for(nruns * nslices, 4)), s, x_flat, W, grad_proj,
-                                              proj, inv_rms, grad_x, partial, T, nc, nslices, go3, h_pre,
-                                              static_cast<int>(C));
+    const dim3 grid(blocks_for(nruns * nslices, 4));
+    if (grad_x_in)
+      launch_k1_bwd_mfma<kBwdDwNTB, true, true, true>(grid, s, x_flat, W, grad_proj, proj, inv_rms, grad_x,
+                                                      partial, T, nc, nslices, go3, h_pre, static_cast<int>(C),
+                                                      grad_x_in);
+    else
+      launch_k1_bwd_mfma<kBwdDwNTB, true, true>(grid, s, x_flat, W, grad_proj, proj, inv_rms, grad_x, partial,
+                                                T, nc, nslices, go3, h_pre, static_cast<int>(C));
     const int st = launch_status();
     if (st != FMHC_OK) return st;
     const int64_t per_part = static_cast<int64_t>(nslices) * (8 * 2 * 4 * kWave);
     k1_dw_reduce<<<dim3(blocks_for(per_part / 4, 256)), 256, 0, s>>>(partial, grad_W, nruns, nslices, nc);
     return launch_status();
   }
-  k1_bwd_scalar<true><<<dim3(blocks_for(T, 4)), 256, 0, s>>>(x_flat, W, grad_proj, proj, inv_rms, grad_x, T, nc);
+  k1_bwd_scalar<true><<<dim3(blocks_for(T, 4)), 256, 0, s>>>(x_flat, W, grad_proj, proj, inv_rms, grad_x,
+                                                             grad_x_in, T, nc);
   const int st = launch_status();
   if (st != FMHC_OK) return st;
   k1_dw_scalar<<<dim3(blocks_for(static_cast<int64_t>(kDout) * nC, 256)), 256, 0, s>>>(

@@ -8,15 +8,17 @@
 namespace fmhc {
 
 // True when k1_bwd_premap computes the K3 term of grad_x itself (MFMA path);
-// otherwise grad_x must hold it on entry.
+// otherwise grad_x must hold it on entry.  gi: the incoming gradient or null.
 bool k1_bwd_premap_fused(const void* x, const void* W, const void* go, const void* proj, const void* gx,
-                         const void* go3, int64_t C);
+                         const void* go3, const void* gi, int64_t C);
 
 // grad_W (32, 4C) and grad_x = bf16(bf16(h_pre[t, j] go3[t, c]) + bf16(dx)) of
-// K1 for x (T, 4, C); `workspace` as fmhc_k1_bwd (fmhc_k1_bwd_workspace_bytes(T, 4C)).
+// K1 for x (T, 4, C); with grad_x_in (may be null, must not overlap grad_x)
+// grad_x = bf16(grad_x_in + that).  `workspace` as fmhc_k1_bwd
+// (fmhc_k1_bwd_workspace_bytes(T, 4C)).
 int k1_bwd_premap(const uint16_t* x_flat, const uint16_t* W, const uint16_t* grad_proj,
                   const uint16_t* proj, const float* inv_rms, const uint16_t* go3, const float* h_pre,
-                  uint16_t* grad_x, uint16_t* grad_W, void* workspace, int64_t workspace_bytes, int64_t T,
-                  int64_t C, hipStream_t s);
+                  const uint16_t* grad_x_in, uint16_t* grad_x, uint16_t* grad_W, void* workspace,
+                  int64_t workspace_bytes, int64_t T, int64_t C, hipStream_t s);
 
 }  // namespace fmhc

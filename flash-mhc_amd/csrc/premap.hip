@@ -6,7 +6,10 @@
 // third pass.  Here K3's backward only reduces grad_h_pre (x and go3 read, no
 // grad_x written), K2's backward gives K1's grad_out, and K1's backward
 // (with grad_W) adds bf16(h_pre go3) to bf16(dx) in its store: one grad_x
-// write, the same bf16 sum.
+// write, the same bf16 sum.  x's third gradient in a block, post-res's
+// H_merged^T grad_out, can come in as grad_x_in: K1's store then adds it too
+// (bf16(grad_x_in + pre-map gradient), autograd's sum), which replaces
+// autograd's separate accumulation pass (1.5 x T x nC x 2 bytes).
 //
 // Forward: K1 -> K2 -> K3, the three kernels of k1.hip, k2.hip, k3.hip.  A
 // one-pass variant that kept each token tile of x in LDS between K1 and K3
@@ -69,7 +72,8 @@ extern "C" int fmhc_premap_bwd(const uint16_t* x, const uint16_t* W, const float
                                const float* alpha_post, const float* alpha_res, const float* bias,
                                const float* perm, const float* h_pre, const uint16_t* proj,
                                const float* inv_rms, const uint16_t* grad_layer_input,
-                               const float* grad_h_post, const float* grad_H_merged, uint16_t* grad_x,
+                               const float* grad_h_post, const float* grad_H_merged,
+                               const uint16_t* grad_x_in, uint16_t* grad_x,
                                uint16_t* grad_W, float* grad_alpha_pre, float* grad_alpha_post,
                                float* grad_alpha_res, float* grad_bias, void* workspace,
                                int64_t workspace_bytes, int64_t T, int64_t C, int64_t n, void* stream) {
@@ -79,6 +83,11 @@ extern "C" int fmhc_premap_bwd(const uint16_t* x, const uint16_t* W, const float
       !grad_alpha_post || !grad_alpha_res || !grad_bias)
     return FMHC_ERR_INVALID_ARGUMENT;
   if (T > 0 && (!x || !h_pre || !proj || !inv_rms || !grad_layer_input || !grad_x)) return FMHC_ERR_INVALID_ARGUMENT;
+  if (T > 0 && grad_x_in) {  // grad_x_in is read while grad_x is written: no overlap
+    const auto a = reinterpret_cast<uintptr_t>(grad_x_in), b = reinterpret_cast<uintptr_t>(grad_x);
+    const auto bytes = static_cast<uintptr_t>(T * n * C * 2);
+    if (a < b + bytes && b < a + bytes) return FMHC_ERR_INVALID_ARGUMENT;
+  }
   const PremapWs w = premap_ws(T, C);
   if (T > 0 && (!workspace || workspace_bytes < w.total || !aligned16(workspace))) return FMHC_ERR_INVALID_ARGUMENT;
   char* ws = static_cast<char*>(workspace);
@@ -86,14 +95,14 @@ extern "C" int fmhc_premap_bwd(const uint16_t* x, const uint16_t* W, const float
   float* gh = T > 0 ? reinterpret_cast<float*>(ws + w.gh) : nullptr;
   uint16_t* gp = T > 0 ? reinterpret_cast<uint16_t*>(ws + w.gp) : nullptr;
   int st = FMHC_OK;
-  const bool fused = T > 0 && k1_bwd_premap_fused(x, W, gp, proj, grad_x, grad_layer_input, C);
+  const bool fused = T > 0 && k1_bwd_premap_fused(x, W, gp, proj, grad_x, grad_layer_input, grad_x_in, C);
   if (T > 0) st = fmhc_k3_bwd(x, h_pre, grad_layer_input, fused ? nullptr : grad_x, gh, T, C, n, stream);
   if (st == FMHC_OK)
     st = fmhc_k2_bwd(proj, alpha_pre, alpha_post, alpha_res, bias, perm, gh, grad_h_post, grad_H_merged, gp,
                      grad_alpha_pre, grad_alpha_post, grad_alpha_res, grad_bias, T > 0 ? ws + w.k2 : nullptr,
                      T > 0 ? w.k1 - w.k2 : 0, T, n, stream);
   if (st == FMHC_OK)
-    st = k1_bwd_premap(x, W, gp, proj, inv_rms, grad_layer_input, h_pre, grad_x, grad_W,
+    st = k1_bwd_premap(x, W, gp, proj, inv_rms, grad_layer_input, h_pre, grad_x_in, grad_x, grad_W,
                        T > 0 ? ws + w.k1 : nullptr, T > 0 ? w.total - w.k1 : 0, T, C, s);
   return st;
 }

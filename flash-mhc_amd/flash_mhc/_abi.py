@@ -33,7 +33,7 @@ SIGNATURES: dict[str, list] = {
     "fmhc_k2_bwd": [_P] * 15 + [_I64, _I64, _I64, _P],
     "fmhc_k2_bwd_workspace_bytes": [_I64],
     "fmhc_premap_fwd": [_P] * 13 + [_I64, _I64, _I64, _P],
-    "fmhc_premap_bwd": [_P] * 20 + [_I64, _I64, _I64, _I64, _P],
+    "fmhc_premap_bwd": [_P] * 21 + [_I64, _I64, _I64, _I64, _P],
     "fmhc_premap_bwd_workspace_bytes": [_I64, _I64],
     "fmhc_k3_fwd": [_P, _P, _P, _I64, _I64, _I64, _P],
     "fmhc_k3_bwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
@@ -50,7 +50,7 @@ RESTYPES = {
     "fmhc_premap_bwd_workspace_bytes": ctypes.c_int64,
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

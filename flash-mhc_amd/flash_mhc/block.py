@@ -180,11 +180,14 @@ class MHCLiteBlock(nn.Module):
 
     def _mhc_pre_map_triton(self, x_streams: torch.Tensor):
         if _ops.fused_premap_enabled():
-            # K1 + K2 + K3 in one op: one forward read of x.
-            layer_input, H_merged, h_post, _h_pre, _proj, _inv_rms = torch.ops.flash_mhc.mhc_pre_map(
+            # K1 + K2 + K3 in one op.  With x_sink, post-res's x-gradient is
+            # added in K1's backward store rather than by autograd.
+            layer_input, H_merged, h_post, _h_pre, _proj, _inv_rms, x_sink = torch.ops.flash_mhc.mhc_pre_map(
                 x_streams, self._projection_weight(x_streams.dtype), self.alpha_pre,
                 self.alpha_post, self.alpha_res, self.W_all.bias, self.perm_mat,
             )
+            if _ops.fused_xgrad_enabled():
+                return layer_input, H_merged, h_post, x_sink
             return layer_input, H_merged, h_post
         if _ops.fused_k2_enabled():
             # One kernel for K2, same values as the ops below (fp32 outputs).
@@ -198,7 +201,9 @@ class MHCLiteBlock(nn.Module):
         layer_input = torch.ops.flash_mhc.fused_pre_map(x_streams, h_pre.float())
         return layer_input, H_merged.float(), h_post.float()
 
-    def _mhc_post_res_triton(self, x_streams, layer_output, H_merged, h_post):
+    def _mhc_post_res_triton(self, x_streams, layer_output, H_merged, h_post, x_sink=None):
+        if x_sink is not None:
+            return torch.ops.flash_mhc.mhc_post_res(x_streams, x_sink, layer_output, H_merged, h_post)
         return torch.ops.flash_mhc.fused_post_res(x_streams, layer_output, H_merged, h_post)
 
     def _forward_triton(self, x_streams: torch.Tensor, **kwargs) -> torch.Tensor:
@@ -215,20 +220,18 @@ class MHCLiteBlock(nn.Module):
     def _run(self, x_streams, pre_map, post_res, ctx, kwargs, checkpoint_post_res=True) -> torch.Tensor:
         use_ckpt = self._use_activation_checkpointing(x_streams)
         with ctx:
+            # pre_map returns (layer_input, H_merged, h_post, *extra); post_res
+            # takes (x_streams, layer_output, H_merged, h_post, *extra).
             if use_ckpt:
-                layer_input, H_merged, h_post = _checkpoint(
-                    pre_map, x_streams, use_reentrant=False
-                )
+                layer_input, *coeffs = _checkpoint(pre_map, x_streams, use_reentrant=False)
             else:
-                layer_input, H_merged, h_post = pre_map(x_streams)
+                layer_input, *coeffs = pre_map(x_streams)
 
             layer_output = self.layer(layer_input, **kwargs)
 
             if use_ckpt and checkpoint_post_res:
-                return _checkpoint(
-                    post_res, x_streams, layer_output, H_merged, h_post, use_reentrant=False
-                )
-            return post_res(x_streams, layer_output, H_merged, h_post)
+                return _checkpoint(post_res, x_streams, layer_output, *coeffs, use_reentrant=False)
+            return post_res(x_streams, layer_output, *coeffs)
 
     def forward(self, x_streams: torch.Tensor, **kwargs) -> torch.Tensor:
         use_fused = (

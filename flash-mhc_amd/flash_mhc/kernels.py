@@ -258,9 +258,10 @@ def premap_bwd(x_streams: torch.Tensor, W: torch.Tensor, alpha_pre: torch.Tensor
                alpha_post: torch.Tensor, alpha_res: torch.Tensor, bias: torch.Tensor,
                perm: torch.Tensor, h_pre: torch.Tensor, proj: torch.Tensor, inv_rms: torch.Tensor,
                grad_layer_input: torch.Tensor, grad_h_post: torch.Tensor | None,
-               grad_H: torch.Tensor | None):
+               grad_H: torch.Tensor | None, grad_x_in: torch.Tensor | None = None):
     """Gradients of premap_fwd's inputs: (grad_x (T,4,C) bf16, grad_W (32,4C) bf16,
-    grad_alpha_pre, grad_alpha_post, grad_alpha_res (1,), grad_bias (32,) fp32)."""
+    grad_alpha_pre, grad_alpha_post, grad_alpha_res (1,), grad_bias (32,) fp32).
+    grad_x_in (T,4,C) bf16, optional: a further gradient of x, added (bf16) into grad_x."""
     T, n, C = _streams_shape(x_streams)
     dev = _device_of(x_streams)
     _require(x_streams, "x_streams", _BF16, (T, n, C), dev)
@@ -274,6 +275,8 @@ def premap_bwd(x_streams: torch.Tensor, W: torch.Tensor, alpha_pre: torch.Tensor
         _require(grad_h_post, "grad_h_post", _F32, (T, n), dev)
     if grad_H is not None:
         _require(grad_H, "grad_H_merged", _F32, (T, n, n), dev)
+    if grad_x_in is not None:
+        _require(grad_x_in, "grad_x_in", _BF16, (T, n, C), dev)
     gx = torch.empty_like(x_streams)
     gW = torch.empty((D_OUT, n * C), device=dev, dtype=_BF16)
     ga = [torch.empty((1,), device=dev, dtype=_F32) for _ in range(3)]
@@ -286,7 +289,8 @@ def premap_bwd(x_streams: torch.Tensor, W: torch.Tensor, alpha_pre: torch.Tensor
         st = lib.fmhc_premap_bwd(x_streams.data_ptr(), W.data_ptr(), alpha_pre.data_ptr(),
                                  alpha_post.data_ptr(), alpha_res.data_ptr(), bias.data_ptr(),
                                  perm.data_ptr(), h_pre.data_ptr(), proj.data_ptr(), inv_rms.data_ptr(),
-                                 grad_layer_input.data_ptr(), ptr(grad_h_post), ptr(grad_H), gx.data_ptr(),
+                                 grad_layer_input.data_ptr(), ptr(grad_h_post), ptr(grad_H), ptr(grad_x_in),
+                                 gx.data_ptr(),
                                  gW.data_ptr(), ga[0].data_ptr(), ga[1].data_ptr(), ga[2].data_ptr(),
                                  gb.data_ptr(), ws.data_ptr(), ws.numel(), T, C, n, _abi.stream_of(x_streams))
     _abi.check(st, "premap_bwd")

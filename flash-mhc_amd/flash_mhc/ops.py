@@ -68,11 +68,20 @@ _lib.define(
 )
 
 # Not in the reference: the pre-map region (K1 + K2 + K3) as one op.
+# x_sink is a (T, n, C) placeholder with zero strides (one element of storage)
+# that stands for x: passed to mhc_post_res in place of a second use of x, it
+# brings post-res's x-gradient back into this op's backward, which adds it in
+# K1's store instead of leaving autograd a separate accumulation pass.
 _lib.define(
-    "mhc_pre_map(Tensor x_streams, Tensor W, Tensor alpha_pre, Tensor alpha_post, Tensor alpha_res, Tensor bias, Tensor perm_mat) -> (Tensor layer_input, Tensor H_merged, Tensor h_post, Tensor h_pre, Tensor proj, Tensor inv_rms)"
+    "mhc_pre_map(Tensor x_streams, Tensor W, Tensor alpha_pre, Tensor alpha_post, Tensor alpha_res, Tensor bias, Tensor perm_mat) -> (Tensor layer_input, Tensor H_merged, Tensor h_post, Tensor h_pre, Tensor proj, Tensor inv_rms, Tensor x_sink)"
 )
 _lib.define(
-    "mhc_pre_map_backward(Tensor? grad_layer_input, Tensor? grad_H_merged, Tensor? grad_h_post, Tensor? grad_h_pre, Tensor? grad_proj, Tensor x_streams, Tensor W, Tensor alpha_pre, Tensor alpha_post, Tensor alpha_res, Tensor bias, Tensor perm_mat, Tensor h_pre, Tensor proj, Tensor inv_rms) -> (Tensor grad_x, Tensor grad_W, Tensor grad_alpha_pre, Tensor grad_alpha_post, Tensor grad_alpha_res, Tensor grad_bias)"
+    "mhc_pre_map_backward(Tensor? grad_layer_input, Tensor? grad_H_merged, Tensor? grad_h_post, Tensor? grad_h_pre, Tensor? grad_proj, Tensor? grad_x_sink, Tensor x_streams, Tensor W, Tensor alpha_pre, Tensor alpha_post, Tensor alpha_res, Tensor bias, Tensor perm_mat, Tensor h_pre, Tensor proj, Tensor inv_rms) -> (Tensor grad_x, Tensor grad_W, Tensor grad_alpha_pre, Tensor grad_alpha_post, Tensor grad_alpha_res, Tensor grad_bias)"
+)
+# Not in the reference: fused_post_res whose x-gradient goes to x_sink (an
+# output of mhc_pre_map for the same x) instead of x.  Same forward.
+_lib.define(
+    "mhc_post_res(Tensor x_streams, Tensor x_sink, Tensor layer_output, Tensor H_merged, Tensor h_post) -> Tensor out"
 )
 
 _lib.define("fused_pre_map(Tensor x_streams, Tensor h_pre) -> Tensor out")
@@ -150,19 +159,32 @@ def _mhc_coefficients_backward_fake(grad_h_pre, grad_h_post, grad_H_merged, proj
             torch.empty_like(alpha_res), torch.empty_like(bias))
 
 
+def x_sink_like(x_streams: torch.Tensor) -> torch.Tensor:
+    """mhc_pre_map's x_sink: x's shape and dtype, zero strides, one element of storage."""
+    return x_streams.new_empty_strided(tuple(x_streams.shape), (0,) * x_streams.dim())
+
+
+def _x_sink(x_streams: torch.Tensor) -> torch.Tensor:
+    """x_sink_like with its one element set to zero (a one-element fill, not T n C)."""
+    sink = x_sink_like(x_streams)
+    sink.as_strided((1,), (1,)).zero_()
+    return sink
+
+
 @torch.library.register_fake("flash_mhc::mhc_pre_map")
 def _mhc_pre_map_fake(x_streams, W, alpha_pre, alpha_post, alpha_res, bias, perm_mat):
     T, n, C = x_streams.shape
     f32 = torch.float32
     return (x_streams.new_empty((T, C)), x_streams.new_empty((T, n, n), dtype=f32),
             x_streams.new_empty((T, n), dtype=f32), x_streams.new_empty((T, n), dtype=f32),
-            x_streams.new_empty((T, W.shape[0])), x_streams.new_empty((T,), dtype=f32))
+            x_streams.new_empty((T, W.shape[0])), x_streams.new_empty((T,), dtype=f32),
+            x_sink_like(x_streams))
 
 
 @torch.library.register_fake("flash_mhc::mhc_pre_map_backward")
 def _mhc_pre_map_backward_fake(grad_layer_input, grad_H_merged, grad_h_post, grad_h_pre, grad_proj,
-                               x_streams, W, alpha_pre, alpha_post, alpha_res, bias, perm_mat, h_pre,
-                               proj, inv_rms):
+                               grad_x_sink, x_streams, W, alpha_pre, alpha_post, alpha_res, bias,
+                               perm_mat, h_pre, proj, inv_rms):
     return (torch.empty_like(x_streams), torch.empty_like(W), torch.empty_like(alpha_pre),
             torch.empty_like(alpha_post), torch.empty_like(alpha_res), torch.empty_like(bias))
 
@@ -178,6 +200,11 @@ def _fused_pre_map_backward_fake(grad_out, x_streams, h_pre):
     grad_x = torch.empty_like(x_streams)
     grad_h_pre = torch.empty_like(h_pre, dtype=torch.float32)
     return grad_x, grad_h_pre
+
+
+@torch.library.register_fake("flash_mhc::mhc_post_res")
+def _mhc_post_res_fake(x_streams, x_sink, layer_output, H_merged, h_post):
+    return torch.empty_like(x_streams)
 
 
 @torch.library.register_fake("flash_mhc::fused_post_res")
@@ -259,14 +286,15 @@ def _mhc_coefficients_backward_cuda(grad_h_pre, grad_h_post, grad_H_merged, proj
 def _mhc_pre_map_cuda(x_streams, W, alpha_pre, alpha_post, alpha_res, bias, perm_mat):
     _check_n4(x_streams, "flash_mhc::mhc_pre_map supports n=4 only")
     _check_k2(x_streams.new_empty((0, W.shape[0])), perm_mat)
-    return _k.premap_fwd(x_streams.contiguous(), W.to(x_streams.dtype).contiguous(), _coeff(alpha_pre),
+    outs = _k.premap_fwd(x_streams.contiguous(), W.to(x_streams.dtype).contiguous(), _coeff(alpha_pre),
                          _coeff(alpha_post), _coeff(alpha_res), _coeff(bias), _coeff(perm_mat))
+    return (*outs, _x_sink(x_streams))
 
 
 @torch.library.impl(_lib, "mhc_pre_map_backward", "CUDA")
 def _mhc_pre_map_backward_cuda(grad_layer_input, grad_H_merged, grad_h_post, grad_h_pre, grad_proj,
-                               x_streams, W, alpha_pre, alpha_post, alpha_res, bias, perm_mat, h_pre,
-                               proj, inv_rms):
+                               grad_x_sink, x_streams, W, alpha_pre, alpha_post, alpha_res, bias,
+                               perm_mat, h_pre, proj, inv_rms):
     _check_n4(x_streams, "flash_mhc::mhc_pre_map_backward supports n=4 only")
     x = x_streams.contiguous()
     T, n, C = x.shape
@@ -276,10 +304,12 @@ def _mhc_pre_map_backward_cuda(grad_layer_input, grad_H_merged, grad_h_post, gra
             else grad_layer_input.to(x.dtype).contiguous())
     g_hp = None if grad_h_post is None else _coeff(grad_h_post)
     g_H = None if grad_H_merged is None else _coeff(grad_H_merged)
+    g_sink = None if grad_x_sink is None else grad_x_sink.to(x.dtype).contiguous()
     if grad_h_pre is None and grad_proj is None:
-        # One launch sequence: K3's reduction, K2, K1 with K3's term in its store.
+        # One launch sequence: K3's reduction, K2, K1 with K3's term (and the
+        # sink's gradient) in its store.
         gx, gW, ga1, ga2, ga3, gb = _k.premap_bwd(x, Wc, *coeffs, h_pre.contiguous(), proj.contiguous(),
-                                                  inv_rms.contiguous(), g_li, g_hp, g_H)
+                                                  inv_rms.contiguous(), g_li, g_hp, g_H, g_sink)
     else:
         # Gradients also flow into the h_pre / proj outputs: compose the ops.
         gx3, gh = _k.k3_bwd(g_li, x, h_pre.contiguous())
@@ -290,6 +320,8 @@ def _mhc_pre_map_backward_cuda(grad_layer_input, grad_H_merged, grad_h_post, gra
             gp = (gp.float() + grad_proj.float()).to(gp.dtype)
         gx1, gW = _k.k1_bwd(gp, x.view(T, n * C), Wc, proj.contiguous(), inv_rms.contiguous())
         gx = gx3 + gx1.view(T, n, C)
+        if g_sink is not None:
+            gx = g_sink + gx
     return (gx, gW.to(W.dtype), ga1.to(alpha_pre.dtype), ga2.to(alpha_post.dtype),
             ga3.to(alpha_res.dtype), gb.to(bias.dtype))
 
@@ -309,6 +341,13 @@ def _fused_pre_map_backward_cuda(grad_out, x_streams, h_pre):
 @torch.library.impl(_lib, "fused_post_res", "CUDA")
 def _fused_post_res_cuda(x_streams, layer_output, H_merged, h_post):
     _check_n4(x_streams, "flash_mhc::fused_post_res currently supports n=4 only")
+    return _k.k4_fwd(x_streams.contiguous(), layer_output.contiguous(), _coeff(H_merged),
+                     _coeff(h_post))
+
+
+@torch.library.impl(_lib, "mhc_post_res", "CUDA")
+def _mhc_post_res_cuda(x_streams, x_sink, layer_output, H_merged, h_post):
+    _check_n4(x_streams, "flash_mhc::mhc_post_res supports n=4 only")
     return _k.k4_fwd(x_streams.contiguous(), layer_output.contiguous(), _coeff(H_merged),
                      _coeff(h_post))
 
@@ -349,6 +388,12 @@ def fused_premap_enabled() -> bool:
     """MHCLiteBlock runs K1 + K2 + K3 as flash_mhc::mhc_pre_map unless
     FLASH_MHC_FUSED_PREMAP=0 or FLASH_MHC_FUSED_K2=0."""
     return _env_flag("FLASH_MHC_FUSED_PREMAP") and fused_k2_enabled()
+
+
+def fused_xgrad_enabled() -> bool:
+    """With the pre-map op, MHCLiteBlock sends post-res's x-gradient through
+    mhc_pre_map's x_sink (added in K1's store) unless FLASH_MHC_FUSED_XGRAD=0."""
+    return _env_flag("FLASH_MHC_FUSED_XGRAD") and fused_premap_enabled()
 
 
 def _fused_rmsnorm_project_backward(ctx, grad_out, grad_inv_rms):
@@ -404,20 +449,29 @@ torch.library.register_autograd(
     setup_context=_setup_inputs,
 )
 def _setup_pre_map(ctx, inputs, output):
-    _li, _H, _hp, h_pre, proj, inv_rms = output
+    _li, _H, _hp, h_pre, proj, inv_rms, _sink = output
     ctx.save_for_backward(*inputs, h_pre, proj, inv_rms)
     # Outputs nobody differentiates (h_pre, proj, inv_rms in the block) arrive
     # as None rather than as zero tensors.
     ctx.set_materialize_grads(False)
 
 
-def _mhc_pre_map_backward(ctx, g_li, g_H, g_hp, g_hpre, g_proj, _g_inv_rms):
+def _mhc_pre_map_backward(ctx, g_li, g_H, g_hp, g_hpre, g_proj, _g_inv_rms, g_sink):
     # inv_rms is not differentiable, as K1's in the reference.
     x, W, ap, apo, ar, b, perm, h_pre, proj, inv_rms = ctx.saved_tensors
     grads = torch.ops.flash_mhc.mhc_pre_map_backward(
-        g_li, g_H, g_hp, g_hpre, g_proj, x, W, ap, apo, ar, b, perm, h_pre, proj, inv_rms
+        g_li, g_H, g_hp, g_hpre, g_proj, g_sink, x, W, ap, apo, ar, b, perm, h_pre, proj, inv_rms
     )
     return (*grads, None)
+
+
+def _mhc_post_res_backward(ctx, grad_out):
+    x_streams, _sink, layer_output, H_merged, h_post = ctx.saved_tensors
+    g_x, g_lo, g_H, g_hp = torch.ops.flash_mhc.fused_post_res_backward(
+        grad_out, x_streams, layer_output, H_merged, h_post
+    )
+    # x's gradient goes to the sink; mhc_pre_map's backward adds it to x's.
+    return None, g_x, g_lo, g_H, g_hp
 
 
 torch.library.register_autograd(
@@ -433,5 +487,10 @@ torch.library.register_autograd(
 torch.library.register_autograd(
     "flash_mhc::fused_post_res",
     _fused_post_res_backward,
+    setup_context=_setup_inputs,
+)
+torch.library.register_autograd(
+    "flash_mhc::mhc_post_res",
+    _mhc_post_res_backward,
     setup_context=_setup_inputs,
 )

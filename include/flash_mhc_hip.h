@@ -35,7 +35,7 @@ extern "C" {
 #define FMHC_ERR_INVALID_ARGUMENT 1 /* negative size, n != 4, D_out != 32, null pointer */
 #define FMHC_ERR_HIP_BASE 1000      /* + hipError_t from the launch */
 
-#define FMHC_ABI_VERSION 2
+#define FMHC_ABI_VERSION 3
 
 /* K1 forward: fused RMSNorm + projection.
  *   inv_rms[t] = rsqrt(sum_k x[t,k]^2 / nC + 1e-6)
@@ -127,15 +127,20 @@ int fmhc_premap_fwd(const uint16_t* x, const uint16_t* W, const float* alpha_pre
  *            (each term rounded to bf16 first, as autograd sums them),
  *   grad_W (32, n C) bf16 as fmhc_k1_bwd, the alpha / bias gradients as
  *   fmhc_k2_bwd.
+ * grad_x_in (T, n, C) bf16 may be NULL; otherwise it is a further gradient of
+ * x (in a block: post-res's H_merged^T grad_out) and
+ *   grad_x = bf16(grad_x_in + the bf16 value above)
+ * (autograd's sum of x's gradients).  It must not overlap grad_x.
  * h_pre, proj, inv_rms are fmhc_premap_fwd's outputs.  `workspace`: at least
  * fmhc_premap_bwd_workspace_bytes(T, C) bytes, 16-byte aligned.
  * Replaces: autograd through src/flash_mhc/block.py:157-177 (the K3, K2 and K1
- *           backward launches, and the addition of x's two gradients). */
+ *           backward launches, and the addition of x's gradients). */
 int fmhc_premap_bwd(const uint16_t* x, const uint16_t* W, const float* alpha_pre,
                     const float* alpha_post, const float* alpha_res, const float* bias,
                     const float* perm, const float* h_pre, const uint16_t* proj, const float* inv_rms,
                     const uint16_t* grad_layer_input, const float* grad_h_post,
-                    const float* grad_H_merged, uint16_t* grad_x, uint16_t* grad_W,
+                    const float* grad_H_merged, const uint16_t* grad_x_in, uint16_t* grad_x,
+                    uint16_t* grad_W,
                     float* grad_alpha_pre, float* grad_alpha_post, float* grad_alpha_res,
                     float* grad_bias, void* workspace, int64_t workspace_bytes, int64_t T, int64_t C,
                     int64_t n, void* stream);

@@ -59,10 +59,12 @@ def _pre_map(x, W, ap, apo, ar, b, perm):
     T, n, C = x.shape
     proj, inv = _k1(x.reshape(T, n * C), W.to(x.dtype))
     h_pre, h_post, H = _k2(proj, ap, apo, ar, b, perm)
-    return _k3(x, h_pre), H, h_post, h_pre, proj, inv
+    sink = x.new_empty_strided(tuple(x.shape), (0,) * x.dim())  # mhc_pre_map's x_sink
+    sink.as_strided((1,), (1,)).zero_()
+    return _k3(x, h_pre), H, h_post, h_pre, proj, inv, sink
 
 
-def _pre_map_bwd(g_li, g_H, g_hp, g_hpre, g_proj, x, W, ap, apo, ar, b, perm, h_pre, proj, inv):
+def _pre_map_bwd(g_li, g_H, g_hp, g_hpre, g_proj, g_sink, x, W, ap, apo, ar, b, perm, h_pre, proj, inv):
     T, n, C = x.shape
     if g_li is None:
         g_li = torch.zeros(T, C, dtype=x.dtype)
@@ -73,7 +75,10 @@ def _pre_map_bwd(g_li, g_H, g_hp, g_hpre, g_proj, x, W, ap, apo, ar, b, perm, h_
     if g_proj is not None:
         gp = (gp.float() + g_proj.float()).to(gp.dtype)
     gx1, gW = _k1_bwd(gp, x.reshape(T, n * C), W.to(x.dtype), proj, inv)
-    return gx3 + gx1.view(T, n, C), gW.to(W.dtype), ga1, ga2, ga3, gb
+    gx = gx3 + gx1.view(T, n, C)
+    if g_sink is not None:
+        gx = g_sink.to(gx.dtype) + gx
+    return gx, gW.to(W.dtype), ga1, ga2, ga3, gb
 
 
 def _k3(x, h):
@@ -93,6 +98,10 @@ def _k4(x, lo, H, hp):
     return R.to(x.dtype)
 
 
+def _post_res_sink(x, sink, lo, H, hp):
+    return _k4(x, lo, H, hp)
+
+
 def _k4_bwd(go, x, lo, H, hp):
     r = O.k4_bwd(go, x, lo, H, hp)
     return (r["grad_x"][0].to(x.dtype), r["grad_lo"][0].to(lo.dtype),
@@ -110,6 +119,7 @@ IMPLS = {
     "fused_pre_map": _k3,
     "fused_pre_map_backward": _k3_bwd,
     "fused_post_res": _k4,
+    "mhc_post_res": _post_res_sink,
     "fused_post_res_backward": _k4_bwd,
 }
 

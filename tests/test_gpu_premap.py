@@ -168,3 +168,75 @@ def test_premap_bwd_null_grads_and_empty():
     g0 = K.premap_bwd(e, W, *p, f32(0, 4), torch.empty((0, 32), dtype=BF16, device=DEV), f32(0),
                       torch.empty((0, C), dtype=BF16, device=DEV), None, None)
     assert g0[0].shape == (0, 4, C) and all(float(t.float().abs().sum()) == 0.0 for t in g0[1:])
+
+
+@pytest.mark.parametrize("T,C", [(4096, 1024), (257, 1024), (1, 256), (300, 1000), (333, 100), (45, 24)])
+def test_premap_bwd_incoming_grad(T, C):
+    """grad_x_in (post-res's x-gradient in a block) is added in K1's store:
+    grad_x = bf16(grad_x_in + the pre-map gradient), bit for bit the sum
+    autograd forms, on the MFMA path and on the element-wise path (C % 8 != 0);
+    the other gradients are unchanged."""
+    nC = 4 * C
+    x = randn((T, 4, C), 5000 + T + C).to(DEV)
+    W = randn((32, nC), 5001 + C, 0.02).to(DEV)
+    p = [t.to(DEV) for t in (*_params(C), PERM)]
+    li, H, hq, hp, proj, inv = K.premap_fwd(x, W, *p)
+    g_li = randn((T, C), 5002 + T).to(DEV)
+    g_hq = randn((T, 4), 5003, dtype=torch.float32).to(DEV)
+    g_H = randn((T, 4, 4), 5004, dtype=torch.float32).to(DEV)
+    g_in = randn((T, 4, C), 5005 + T).to(DEV)
+    a = K.premap_bwd(x, W, *p, hp, proj, inv, g_li, g_hq, g_H, g_in)
+    b = K.premap_bwd(x, W, *p, hp, proj, inv, g_li, g_hq, g_H)
+    torch.cuda.synchronize()
+    assert torch.equal(a[0], g_in + b[0])
+    for u, v in zip(a[1:], b[1:]):
+        assert torch.equal(u, v)
+
+
+def test_premap_bwd_rejects_overlapping_incoming_grad():
+    """grad_x_in must not overlap grad_x: the entry point returns an error
+    before launching anything."""
+    from flash_mhc import _abi
+
+    T, C = 64, 256
+    x = randn((T, 4, C), 60).to(DEV)
+    W = randn((32, 4 * C), 61, 0.02).to(DEV)
+    p = [t.to(DEV) for t in (*_params(C), PERM)]
+    li, H, hq, hp, proj, inv = K.premap_fwd(x, W, *p)
+    g_li = randn((T, C), 62).to(DEV)
+    gW = torch.empty_like(W)
+    ga = [torch.empty(1, device=DEV) for _ in range(3)]
+    gb = torch.empty(32, device=DEV)
+    lib = _abi.load()
+    nbytes = int(lib.fmhc_premap_bwd_workspace_bytes(T, C))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+    P = lambda t: t.data_ptr()
+    shifted = torch.empty(x.numel() + 8, dtype=BF16, device=DEV)
+    gx = shifted[8:].view(T, 4, C)
+    for g_in in (gx, shifted[:-8]):  # the same buffer, and one shifted by 16 bytes
+        st = lib.fmhc_premap_bwd(P(x), P(W), *[P(t) for t in p], P(hp), P(proj), P(inv), P(g_li), None, None,
+                                 P(g_in), P(gx), P(gW), *[P(t) for t in ga], P(gb), P(ws), nbytes, T, C, 4,
+                                 _abi.stream_of(x))
+        assert st == 1  # FMHC_ERR_INVALID_ARGUMENT
+
+
+@pytest.mark.parametrize("ckpt", [False, True])
+def test_block_xgrad_sink_equals_autograd_sum(ckpt):
+    """The block with post-res's x-gradient added in the pre-map backward
+    (FLASH_MHC_FUSED_XGRAD=1) and with autograd adding it (=0): identical
+    outputs and gradients, bit for bit."""
+    old = os.environ.get("FLASH_MHC_FUSED_XGRAD")
+    try:
+        os.environ["FLASH_MHC_FUSED_XGRAD"] = "1"
+        o1, gx1, gp1 = _block_run("1", 4096, 1024, ckpt)
+        os.environ["FLASH_MHC_FUSED_XGRAD"] = "0"
+        o0, gx0, gp0 = _block_run("1", 4096, 1024, ckpt)
+    finally:
+        if old is None:
+            os.environ.pop("FLASH_MHC_FUSED_XGRAD", None)
+        else:
+            os.environ["FLASH_MHC_FUSED_XGRAD"] = old
+    assert torch.equal(o1, o0)
+    assert torch.equal(gx1, gx0)
+    for n in gp0:
+        assert torch.equal(gp1[n], gp0[n]), n

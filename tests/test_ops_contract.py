@@ -60,8 +60,9 @@ ADDED_SCHEMAS = {
     "fused_rmsnorm_project_bwd": "fused_rmsnorm_project_bwd(Tensor grad_out, Tensor x_flat, Tensor W, Tensor proj_out, Tensor inv_rms) -> (Tensor grad_x, Tensor grad_W)",
     "mhc_coefficients": "mhc_coefficients(Tensor proj, Tensor alpha_pre, Tensor alpha_post, Tensor alpha_res, Tensor bias, Tensor perm_mat) -> (Tensor h_pre, Tensor h_post, Tensor H_merged)",
     "mhc_coefficients_backward": "mhc_coefficients_backward(Tensor? grad_h_pre, Tensor? grad_h_post, Tensor? grad_H_merged, Tensor proj, Tensor alpha_pre, Tensor alpha_post, Tensor alpha_res, Tensor bias, Tensor perm_mat) -> (Tensor grad_proj, Tensor grad_alpha_pre, Tensor grad_alpha_post, Tensor grad_alpha_res, Tensor grad_bias)",
-    "mhc_pre_map": "mhc_pre_map(Tensor x_streams, Tensor W, Tensor alpha_pre, Tensor alpha_post, Tensor alpha_res, Tensor bias, Tensor perm_mat) -> (Tensor layer_input, Tensor H_merged, Tensor h_post, Tensor h_pre, Tensor proj, Tensor inv_rms)",
-    "mhc_pre_map_backward": "mhc_pre_map_backward(Tensor? grad_layer_input, Tensor? grad_H_merged, Tensor? grad_h_post, Tensor? grad_h_pre, Tensor? grad_proj, Tensor x_streams, Tensor W, Tensor alpha_pre, Tensor alpha_post, Tensor alpha_res, Tensor bias, Tensor perm_mat, Tensor h_pre, Tensor proj, Tensor inv_rms) -> (Tensor grad_x, Tensor grad_W, Tensor grad_alpha_pre, Tensor grad_alpha_post, Tensor grad_alpha_res, Tensor grad_bias)",
+    "mhc_pre_map": "mhc_pre_map(Tensor x_streams, Tensor W, Tensor alpha_pre, Tensor alpha_post, Tensor alpha_res, Tensor bias, Tensor perm_mat) -> (Tensor layer_input, Tensor H_merged, Tensor h_post, Tensor h_pre, Tensor proj, Tensor inv_rms, Tensor x_sink)",
+    "mhc_pre_map_backward": "mhc_pre_map_backward(Tensor? grad_layer_input, Tensor? grad_H_merged, Tensor? grad_h_post, Tensor? grad_h_pre, Tensor? grad_proj, Tensor? grad_x_sink, Tensor x_streams, Tensor W, Tensor alpha_pre, Tensor alpha_post, Tensor alpha_res, Tensor bias, Tensor perm_mat, Tensor h_pre, Tensor proj, Tensor inv_rms) -> (Tensor grad_x, Tensor grad_W, Tensor grad_alpha_pre, Tensor grad_alpha_post, Tensor grad_alpha_res, Tensor grad_bias)",
+    "mhc_post_res": "mhc_post_res(Tensor x_streams, Tensor x_sink, Tensor layer_output, Tensor H_merged, Tensor h_post) -> Tensor out",
 }
 
 
@@ -207,9 +208,17 @@ def test_opcheck_all_ops(cpu_kernels):
          (x.clone().requires_grad_(True), W.clone().requires_grad_(True),
           *[t.clone().requires_grad_(True) for t in k2p], perm)),
     ]
-    li, H2, hq2, hp2, proj2, inv2 = torch.ops.flash_mhc.mhc_pre_map(x, W, *k2p, perm)
-    cases.append((torch.ops.flash_mhc.mhc_pre_map_backward.default,
-                  (rnd((T, C), 22), H, hp, None, None, x, W, *k2p, perm, hp2, proj2, inv2)))
+    li, H2, hq2, hp2, proj2, inv2, sink = torch.ops.flash_mhc.mhc_pre_map(x, W, *k2p, perm)
+    assert sink.shape == x.shape and sink.stride() == (0, 0, 0) and sink.dtype == x.dtype
+    cases += [
+        (torch.ops.flash_mhc.mhc_pre_map_backward.default,
+         (rnd((T, C), 22), H, hp, None, None, None, x, W, *k2p, perm, hp2, proj2, inv2)),
+        (torch.ops.flash_mhc.mhc_pre_map_backward.default,
+         (rnd((T, C), 22), H, hp, None, None, rnd((T, 4, C), 23), x, W, *k2p, perm, hp2, proj2, inv2)),
+        (torch.ops.flash_mhc.mhc_post_res.default,
+         (x.clone().requires_grad_(True), sink.clone().requires_grad_(True), lo.clone().requires_grad_(True),
+          H.clone().requires_grad_(True), hp.clone().requires_grad_(True))),
+    ]
     for op, args in cases:
         torch.library.opcheck(op, args)
 
@@ -330,8 +339,8 @@ def test_fused_premap_matches_separate_ops_on_cpu(cpu_kernels, monkeypatch, prem
     three ops (=0) gives identical outputs and parameter gradients, with and
     without activation checkpointing.  grad_x is the bf16 sum of x's three
     gradients (from K4, K3, K1): the separate ops let autograd add them as
-    (g4 + g3) + g1, the fused op returns g3 + g1 to which autograd adds g4, so
-    the two may differ by a last bit of the sum."""
+    (g4 + g3) + g1, the pre-map op forms g4 + (g3 + g1), so the two may differ
+    by a last bit of the sum."""
     from parity import check_chain
 
     def run(flag, ckpt):
@@ -357,3 +366,30 @@ def test_fused_premap_matches_separate_ops_on_cpu(cpu_kernels, monkeypatch, prem
             check_chain("grad_x", gx.float(), ref[1].float(), max_rate=1.0)
         for n in gp:
             assert torch.equal(gp[n], ref[2][n]), n
+
+
+@pytest.mark.parametrize("ckpt", [False, True])
+def test_xgrad_sink_equals_autograd_sum_on_cpu(cpu_kernels, monkeypatch, ckpt):
+    """Post-res's x-gradient sent through mhc_pre_map's x_sink and added in the
+    pre-map backward (FLASH_MHC_FUSED_XGRAD=1) gives the same bits as leaving
+    the sum to autograd (=0): both are bf16(g4 + bf16(pre-map gradient))."""
+
+    def run(flag):
+        monkeypatch.setenv("FLASH_MHC_FUSED_XGRAD", flag)
+        blk = _block(C=32)
+        blk.activation_checkpointing = ckpt
+        with torch.no_grad():
+            blk.alpha_pre.fill_(0.8)
+            blk.alpha_post.fill_(1.2)
+            blk.alpha_res.fill_(1.7)
+        x = rnd((64, 4, 32), 47).requires_grad_(True)
+        out = blk._forward_triton(x)
+        out.float().pow(2).sum().backward()
+        return out.detach(), x.grad, {n: p.grad for n, p in blk.named_parameters()}
+
+    o1, gx1, gp1 = run("1")
+    o0, gx0, gp0 = run("0")
+    assert torch.equal(o1, o0)
+    assert torch.equal(gx1, gx0)
+    for n in gp0:
+        assert torch.equal(gp1[n], gp0[n]), n
