@@ -57,12 +57,17 @@ struct FwdFrag {
   u32x4 xv[2][R];      // x of the R token blocks, two k steps
 };
 
-template <int R, int SPLIT>
+// SPLITK (few tokens): blockIdx.y selects a range of cps chunks, and the
+// workgroup writes its fp32 partial sums (32 projections + sum of squares per
+// token) to part[t][33][S4] (S4 = gridDim.y rounded up to 4) instead of the
+// outputs; k1_fwd_finish adds the gridDim.y partials in order.
+template <int R, int SPLIT, bool SPLITK>
 __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __restrict__ x,
                                                              const uint16_t* __restrict__ W,
                                                              uint16_t* __restrict__ out,
                                                              float* __restrict__ inv_rms,
-                                                             int64_t T, int nC) {
+                                                             float* __restrict__ part,
+                                                             int64_t T, int nC, int cps) {
   __shared__ float red_acc[SPLIT][R][8][kWave];
   __shared__ float red_ss[SPLIT][R][16];
   __shared__ u32x4 xs[SPLIT][16 * R * 8];  // per wave: 16R tokens x 8 swizzled 16-byte slots
@@ -113,10 +118,16 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
   // this kernel alone is 10% faster, but K3's forward, which reads x next,
   // loses as much, because it no longer finds the tail of x in the
   // memory-side cache.
-  const int nfull = nC >> 6;
-  const int rot = nfull > 0 ? static_cast<int>(blockIdx.x % static_cast<unsigned>(nfull)) : 0;
+  // With SPLITK the workgroup's chunks are cbeg .. cbeg + nfull - 1 (no
+  // rotation: the workgroups of one token block already cover different
+  // columns), and only the last split takes the ragged chunk.
+  const int nall = nC >> 6;
+  const int cbeg = SPLITK ? static_cast<int>(blockIdx.y) * cps : 0;
+  const int nfull = SPLITK ? (cps < nall - cbeg ? cps : nall - cbeg) : nall;
+  const bool last_split = !SPLITK || blockIdx.y + 1 == gridDim.y;
+  const int rot = !SPLITK && nfull > 0 ? static_cast<int>(blockIdx.x % static_cast<unsigned>(nfull)) : 0;
   FwdFrag<R> f0, f1;
-  auto chunk_at = [&](int p) { return p + rot < nfull ? p + rot : p + rot - nfull; };
+  auto chunk_at = [&](int p) { return cbeg + (p + rot < nfull ? p + rot : p + rot - nfull); };
   auto load = [&](FwdFrag<R>& f, int p) {
     const int k = chunk_at(p) * 64;
 #pragma unroll
@@ -174,8 +185,8 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
     }
   }
   // Ragged last chunk (nC % 64 != 0): 16-byte pieces past nC contribute zero.
-  if ((nC & 63) != 0 && wave == nfull % SPLIT) {
-    const int k = nfull * 64;
+  if ((nC & 63) != 0 && last_split && wave == nfull % SPLIT) {
+    const int k = nall * 64;
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       const bool ok = k + 32 * s + 8 * grp < nC;
@@ -223,17 +234,58 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
 #pragma unroll
       for (int i = 0; i < 8; ++i) a[i] += red_acc[w][r][i][lane];
     }
-    const float inv = rsqrtf(s2 / static_cast<float>(nC) + kEps);
     const int64_t t = t0 + 16 * r + row;
-    if (t < T) {
-      uint16_t* orow = out + t * kDout + 4 * grp;
-      u32x2 lo2 = {pack_bf16x2(a[0] * inv, a[1] * inv), pack_bf16x2(a[2] * inv, a[3] * inv)};
-      u32x2 hi2 = {pack_bf16x2(a[4] * inv, a[5] * inv), pack_bf16x2(a[6] * inv, a[7] * inv)};
-      st_stream(reinterpret_cast<u32x2*>(orow), lo2);
-      st_stream(reinterpret_cast<u32x2*>(orow + 16), hi2);
-      if (grp == 0) inv_rms[t] = inv;
+    if constexpr (SPLITK) {
+      if (t < T) {
+        const int s4 = (static_cast<int>(gridDim.y) + 3) & ~3;
+        float* pr = part + t * (kDout + 1) * s4 + blockIdx.y;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          pr[(4 * grp + q) * s4] = a[q];
+          pr[(16 + 4 * grp + q) * s4] = a[4 + q];
+        }
+        if (grp == 0) pr[kDout * s4] = s2;
+      }
+    } else {
+      const float inv = rsqrtf(s2 / static_cast<float>(nC) + kEps);
+      if (t < T) {
+        uint16_t* orow = out + t * kDout + 4 * grp;
+        u32x2 lo2 = {pack_bf16x2(a[0] * inv, a[1] * inv), pack_bf16x2(a[2] * inv, a[3] * inv)};
+        u32x2 hi2 = {pack_bf16x2(a[4] * inv, a[5] * inv), pack_bf16x2(a[6] * inv, a[7] * inv)};
+        st_stream(reinterpret_cast<u32x2*>(orow), lo2);
+        st_stream(reinterpret_cast<u32x2*>(orow + 16), hi2);
+        if (grp == 0) inv_rms[t] = inv;
+      }
     }
   }
+}
+
+// Second stage of the split K1 forward: one wave per token; lane v < 33 adds
+// the S partials of value v (32 projections, then the sum of squares) in split
+// order, so the result does not depend on scheduling.
+__global__ __launch_bounds__(256) void k1_fwd_finish(const float* __restrict__ part,
+                                                     uint16_t* __restrict__ out,
+                                                     float* __restrict__ inv_rms, int64_t T, int nC,
+                                                     int S) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const int s4 = (S + 3) & ~3;
+  float v = 0.f;
+  if (lane <= kDout) {
+    const f32x4* p = reinterpret_cast<const f32x4*>(part + (t * (kDout + 1) + lane) * s4);
+#pragma unroll 4
+    for (int i = 0; i < s4 / 4; ++i) {
+      const f32x4 q = p[i];
+      v += q[0];  // 4 i < S always
+      if (4 * i + 1 < S) v += q[1];
+      if (4 * i + 2 < S) v += q[2];
+      if (4 * i + 3 < S) v += q[3];
+    }
+  }
+  const float inv = rsqrtf(__shfl(v, kDout, kWave) / static_cast<float>(nC) + kEps);
+  if (lane < kDout) out[t * kDout + lane] = f32_to_bf16(v * inv);
+  if (lane == kDout) inv_rms[t] = inv;
 }
 
 // ---------------------------------------------------------------------------
@@ -670,6 +722,12 @@ __global__ __launch_bounds__(256) void k1_bwd_scalar(const uint16_t* __restrict_
 
 constexpr int kFwdR = 8;      // token blocks of 16 per workgroup
 constexpr int kFwdSplit = 4;  // waves per workgroup (split of the nC axis)
+// Split forward for few tokens: one 16-token block per workgroup and up to
+// kSplitMax column ranges per block, aiming at kSplitTarget workgroups.
+constexpr int kSplitR = 1;
+constexpr int64_t kSplitTarget = 512;
+constexpr int64_t kSplitMax = 64;
+constexpr int64_t kSplitMaxT = 8192;
 constexpr int kBwdNTB = 16;   // token blocks of 16 per wave (dx only)
 constexpr int kBwdDwNTB = 64; // token blocks of 16 per wave when grad_W is fused
 
@@ -682,6 +740,60 @@ bool k1_bwd_mfma_path(const void* x, const void* W, const void* go, const void* 
                       int64_t nC) {
   return nC % 8 == 0 && nC <= (int64_t{1} << 26) && aligned16(x) && aligned16(W) && aligned16(go) &&
          aligned16(proj) && aligned16(gx);
+}
+
+// Column split of the forward for T tokens (S = 1: the one-pass kernel).
+struct K1FwdSplit {
+  int S = 1, cps = 0;
+  int64_t bytes = 0;  // partial sums: T x 33 x S4 fp32
+};
+
+K1FwdSplit k1_fwd_split(int64_t T, int64_t nC) {
+  K1FwdSplit p;
+  const int64_t nall = nC >> 6;
+  if (T <= 0 || T >= kSplitMaxT || nC % 8 != 0 || nC > (int64_t{1} << 24) || nall < 2) return p;
+  const int64_t nblk = (T + 16 * kSplitR - 1) / (16 * kSplitR);
+  int64_t S = (kSplitTarget + nblk - 1) / nblk;
+  S = S < kSplitMax ? S : kSplitMax;
+  S = S < nall ? S : nall;
+  if (S < 2) return p;
+  const int64_t cps = (nall + S - 1) / S;
+  S = (nall + cps - 1) / cps;  // every split non-empty
+  if (S < 2) return p;
+  p.S = static_cast<int>(S);
+  p.cps = static_cast<int>(cps);
+  p.bytes = T * (kDout + 1) * ((S + 3) & ~int64_t{3}) * static_cast<int64_t>(sizeof(float));
+  return p;
+}
+
+// K1 forward; with a workspace of k1_fwd_split(T, nC).bytes (allow_split) few
+// tokens take the column-split kernel.
+int k1_fwd_run(const uint16_t* x_flat, const uint16_t* W, uint16_t* out, float* inv_rms, void* ws,
+               int64_t ws_bytes, bool allow_split, int64_t T, int64_t nC, hipStream_t s) {
+  const int nc = static_cast<int>(nC);
+  // The MFMA kernel addresses a workgroup's 16 R rows of x with 32-bit
+  // element offsets.
+  if (nC % 8 == 0 && nC <= (int64_t{1} << 24) && aligned16(x_flat) && aligned16(W) && aligned16(out)) {
+    const K1FwdSplit p = allow_split ? k1_fwd_split(T, nC) : K1FwdSplit{};
+    if (p.S > 1) {
+      if (!ws || ws_bytes < p.bytes || !aligned16(ws)) return FMHC_ERR_INVALID_ARGUMENT;
+      float* part = static_cast<float*>(ws);
+      const dim3 grid(blocks_for(T, 16 * kSplitR), p.S);
+      k1_fwd_mfma<kSplitR, kFwdSplit, true><<<grid, kWave * kFwdSplit, 0, s>>>(x_flat, W, out, inv_rms, part,
+                                                                              T, nc, p.cps);
+      const int st = launch_status();
+      if (st != FMHC_OK) return st;
+      k1_fwd_finish<<<dim3(blocks_for(T, 4)), 256, 0, s>>>(part, out, inv_rms, T, nc, p.S);
+    } else {
+      const dim3 grid(blocks_for(T, 16 * kFwdR));
+      k1_fwd_mfma<kFwdR, kFwdSplit, false><<<grid, kWave * kFwdSplit, 0, s>>>(x_flat, W, out, inv_rms, nullptr,
+                                                                             T, nc, 0);
+    }
+  } else {
+    const dim3 grid(blocks_for(T, 4));
+    k1_fwd_scalar<<<grid, 256, 0, s>>>(x_flat, W, out, inv_rms, T, nc);
+  }
+  return launch_status();
 }
 
 template <int NTB, bool DW, bool EPI = false, bool GI = false>
@@ -707,18 +819,22 @@ extern "C" int fmhc_k1_fwd(const uint16_t* x_flat, const uint16_t* W, uint16_t* 
   if (bad_sizes(T, nC, D_out)) return FMHC_ERR_INVALID_ARGUMENT;
   if (T == 0) return FMHC_OK;
   if (!x_flat || !W || !out || !inv_rms) return FMHC_ERR_INVALID_ARGUMENT;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const int nc = static_cast<int>(nC);
-  // The MFMA kernel addresses a workgroup's 16 R rows of x with 32-bit
-  // element offsets.
-  if (nC % 8 == 0 && nC <= (int64_t{1} << 24) && aligned16(x_flat) && aligned16(W) && aligned16(out)) {
-    const dim3 grid(blocks_for(T, 16 * kFwdR));
-    k1_fwd_mfma<kFwdR, kFwdSplit><<<grid, kWave * kFwdSplit, 0, s>>>(x_flat, W, out, inv_rms, T, nc);
-  } else {
-    const dim3 grid(blocks_for(T, 4));
-    k1_fwd_scalar<<<grid, 256, 0, s>>>(x_flat, W, out, inv_rms, T, nc);
-  }
-  return launch_status();
+  return k1_fwd_run(x_flat, W, out, inv_rms, nullptr, 0, false, T, nC, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int64_t fmhc_k1_fwd_workspace_bytes(int64_t T, int64_t nC) {
+  return fmhc::k1_fwd_split(T, nC).bytes;
+}
+
+extern "C" int fmhc_k1_fwd_ws(const uint16_t* x_flat, const uint16_t* W, uint16_t* out, float* inv_rms,
+                              void* workspace, int64_t workspace_bytes, int64_t T, int64_t nC, int64_t D_out,
+                              void* stream) {
+  using namespace fmhc;
+  if (bad_sizes(T, nC, D_out)) return FMHC_ERR_INVALID_ARGUMENT;
+  if (T == 0) return FMHC_OK;
+  if (!x_flat || !W || !out || !inv_rms) return FMHC_ERR_INVALID_ARGUMENT;
+  return k1_fwd_run(x_flat, W, out, inv_rms, workspace, workspace_bytes, true, T, nC,
+                    static_cast<hipStream_t>(stream));
 }
 
 extern "C" int fmhc_k1_bwd_dx(const uint16_t* x_flat, const uint16_t* W, const uint16_t* grad_out,

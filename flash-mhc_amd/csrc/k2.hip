@@ -31,19 +31,19 @@ constexpr int kK2Threads = 256;
 
 template <bool VEC>
 __global__ __launch_bounds__(kK2Threads) void k2_fwd_kernel(
-    const uint16_t* __restrict__ proj, const float* __restrict__ alpha_pre,
-    const float* __restrict__ alpha_post, const float* __restrict__ alpha_res,
-    const float* __restrict__ bias, const float* __restrict__ perm, float* __restrict__ h_pre,
+    const uint16_t* __restrict__ proj, const K2Params P, float* __restrict__ h_pre,
     float* __restrict__ h_post, float* __restrict__ H, int64_t T) {
 #pragma clang fp contract(off)
   __shared__ f32x4 sperm[kNF * 4];
-  stage_perm<kK2Threads>(perm, sperm);
+  stage_perm<kK2Threads>(P, sperm);
   const int64_t t = static_cast<int64_t>(blockIdx.x) * kK2Threads + threadIdx.x;
   if (t >= T) return;
   float p[kDk];
   load_proj<VEC>(proj + t * kDk, p);
+  float ap, apo, ar, b[kDk];
+  load_params(P, ap, apo, ar, b);
   K2Fwd f;
-  k2_chain(p, rb(alpha_pre[0]), rb(alpha_post[0]), rb(alpha_res[0]), bias, f);
+  k2_chain(p, ap, apo, ar, b, f);
   f32x4 hp = {f.hp[0], f.hp[1], f.hp[2], f.hp[3]};
   f32x4 hq = {f.hq[0], f.hq[1], f.hq[2], f.hq[3]};
   reinterpret_cast<f32x4*>(h_pre)[t] = hp;
@@ -62,15 +62,13 @@ __global__ __launch_bounds__(kK2Threads) void k2_fwd_kernel(
 // sum_m rb(gz_res p_res), and the 32 logit gradients (the bias terms).
 template <bool VEC>
 __global__ __launch_bounds__(kK2Threads) void k2_bwd_kernel(
-    const uint16_t* __restrict__ proj, const float* __restrict__ alpha_pre,
-    const float* __restrict__ alpha_post, const float* __restrict__ alpha_res,
-    const float* __restrict__ bias, const float* __restrict__ perm,
+    const uint16_t* __restrict__ proj, const K2Params P,
     const float* __restrict__ g_hpre, const float* __restrict__ g_hpost,
     const float* __restrict__ g_H, uint16_t* __restrict__ grad_proj,
     float* __restrict__ partial, int64_t T) {
 #pragma clang fp contract(off)
   __shared__ f32x4 sperm[kNF * 4];
-  stage_perm<kK2Threads>(perm, sperm);
+  stage_perm<kK2Threads>(P, sperm);
   const int64_t t = static_cast<int64_t>(blockIdx.x) * kK2Threads + threadIdx.x;
   float par[kNPar];
 #pragma unroll
@@ -79,9 +77,10 @@ __global__ __launch_bounds__(kK2Threads) void k2_bwd_kernel(
   if (t < T) {
     float p[kDk];
     load_proj<VEC>(proj + t * kDk, p);
-    const float ap = rb(alpha_pre[0]), apo = rb(alpha_post[0]), ar = rb(alpha_res[0]);
+    float ap, apo, ar, b[kDk];
+    load_params(P, ap, apo, ar, b);
     K2Fwd f;
-    k2_chain(p, ap, apo, ar, bias, f);
+    k2_chain(p, ap, apo, ar, b, f);
 
     float gH[kN * kN], ghp[kN], ghq[kN];
 #pragma unroll
@@ -169,47 +168,55 @@ __global__ __launch_bounds__(kK2Threads) void k2_bwd_kernel(
 
 // One wave per parameter gradient: lanes take blocks lane, lane + 64, ...,
 // then a butterfly; the result is rounded to bf16 (the reference sums a bf16
-// tensor) and stored as the fp32 parameter's gradient.
+// tensor) and stored in the parameter's dtype (fp32 or bf16).
 __global__ __launch_bounds__(kWave) void k2_param_reduce(const float* __restrict__ partial,
-                                                         int64_t nblocks, float* __restrict__ g_ap,
-                                                         float* __restrict__ g_apo,
-                                                         float* __restrict__ g_ar,
-                                                         float* __restrict__ g_bias) {
+                                                         int64_t nblocks, void* g_ap, void* g_apo,
+                                                         void* g_ar, void* g_bias, bool bf16) {
   const int k = blockIdx.x;  // 0 .. kNPar - 1
   float v = 0.f;
   for (int64_t b = threadIdx.x; b < nblocks; b += kWave) v += partial[b * kNPar + k];
 #pragma unroll
   for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
   if (threadIdx.x == 0) {
-    float* dst = k == 0 ? g_ap : (k == 1 ? g_apo : (k == 2 ? g_ar : g_bias + (k - 3)));
-    *dst = rb(v);
+    void* dst = k == 0 ? g_ap : (k == 1 ? g_apo : (k == 2 ? g_ar : g_bias));
+    const int i = k < 3 ? 0 : k - 3;
+    if (bf16)
+      static_cast<uint16_t*>(dst)[i] = f32_to_bf16(v);
+    else
+      static_cast<float*>(dst)[i] = rb(v);
   }
 }
 
 bool k2_bad(int64_t T, int64_t n) { return T < 0 || n != kN; }
+
+bool k2_params(const void* ap, const void* apo, const void* ar, const void* bias, const void* perm, int dtype,
+               K2Params& P) {
+  if (!ap || !apo || !ar || !bias || !perm || (dtype != FMHC_PARAM_F32 && dtype != FMHC_PARAM_BF16)) return false;
+  P = K2Params{ap, apo, ar, bias, perm, dtype == FMHC_PARAM_BF16};
+  return true;
+}
 int64_t k2_blocks(int64_t T) { return (T + kK2Threads - 1) / kK2Threads; }
 
 }  // namespace
 }  // namespace fmhc
 
-extern "C" int fmhc_k2_fwd(const uint16_t* proj, const float* alpha_pre, const float* alpha_post,
-                           const float* alpha_res, const float* bias, const float* perm,
+extern "C" int fmhc_k2_fwd(const uint16_t* proj, const void* alpha_pre, const void* alpha_post,
+                           const void* alpha_res, const void* bias, const void* perm, int param_dtype,
                            float* h_pre, float* h_post, float* H_merged, int64_t T, int64_t n,
                            void* stream) {
   using namespace fmhc;
   if (k2_bad(T, n)) return FMHC_ERR_INVALID_ARGUMENT;
+  K2Params P;
+  if (!k2_params(alpha_pre, alpha_post, alpha_res, bias, perm, param_dtype, P)) return FMHC_ERR_INVALID_ARGUMENT;
   if (T == 0) return FMHC_OK;
-  if (!proj || !alpha_pre || !alpha_post || !alpha_res || !bias || !perm || !h_pre || !h_post || !H_merged)
-    return FMHC_ERR_INVALID_ARGUMENT;
+  if (!proj || !h_pre || !h_post || !H_merged) return FMHC_ERR_INVALID_ARGUMENT;
   if (!aligned16(h_pre) || !aligned16(h_post) || !aligned16(H_merged)) return FMHC_ERR_INVALID_ARGUMENT;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid(static_cast<unsigned>(k2_blocks(T)));
   if (aligned16(proj))
-    k2_fwd_kernel<true><<<grid, kK2Threads, 0, s>>>(proj, alpha_pre, alpha_post, alpha_res, bias, perm,
-                                                    h_pre, h_post, H_merged, T);
+    k2_fwd_kernel<true><<<grid, kK2Threads, 0, s>>>(proj, P, h_pre, h_post, H_merged, T);
   else
-    k2_fwd_kernel<false><<<grid, kK2Threads, 0, s>>>(proj, alpha_pre, alpha_post, alpha_res, bias, perm,
-                                                     h_pre, h_post, H_merged, T);
+    k2_fwd_kernel<false><<<grid, kK2Threads, 0, s>>>(proj, P, h_pre, h_post, H_merged, T);
   return launch_status();
 }
 
@@ -219,37 +226,36 @@ extern "C" int64_t fmhc_k2_bwd_workspace_bytes(int64_t T) {
   return k2_blocks(T) * kNPar * static_cast<int64_t>(sizeof(float));
 }
 
-extern "C" int fmhc_k2_bwd(const uint16_t* proj, const float* alpha_pre, const float* alpha_post,
-                           const float* alpha_res, const float* bias, const float* perm,
+extern "C" int fmhc_k2_bwd(const uint16_t* proj, const void* alpha_pre, const void* alpha_post,
+                           const void* alpha_res, const void* bias, const void* perm, int param_dtype,
                            const float* grad_h_pre, const float* grad_h_post,
-                           const float* grad_H_merged, uint16_t* grad_proj, float* grad_alpha_pre,
-                           float* grad_alpha_post, float* grad_alpha_res, float* grad_bias,
+                           const float* grad_H_merged, uint16_t* grad_proj, void* grad_alpha_pre,
+                           void* grad_alpha_post, void* grad_alpha_res, void* grad_bias,
                            void* workspace, int64_t workspace_bytes, int64_t T, int64_t n,
                            void* stream) {
   using namespace fmhc;
   if (k2_bad(T, n)) return FMHC_ERR_INVALID_ARGUMENT;
+  K2Params P;
+  if (!k2_params(alpha_pre, alpha_post, alpha_res, bias, perm, param_dtype, P)) return FMHC_ERR_INVALID_ARGUMENT;
   if (!grad_alpha_pre || !grad_alpha_post || !grad_alpha_res || !grad_bias) return FMHC_ERR_INVALID_ARGUMENT;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t nblocks = k2_blocks(T);
   float* partial = static_cast<float*>(workspace);
   if (T > 0) {
-    if (!proj || !alpha_pre || !alpha_post || !alpha_res || !bias || !perm || !grad_proj)
-      return FMHC_ERR_INVALID_ARGUMENT;
+    if (!proj || !grad_proj) return FMHC_ERR_INVALID_ARGUMENT;
     if (!workspace || workspace_bytes < fmhc_k2_bwd_workspace_bytes(T)) return FMHC_ERR_INVALID_ARGUMENT;
     const dim3 grid(static_cast<unsigned>(nblocks));
     if (aligned16(proj) && aligned16(grad_proj))
-      k2_bwd_kernel<true><<<grid, kK2Threads, 0, s>>>(proj, alpha_pre, alpha_post, alpha_res, bias, perm,
-                                                      grad_h_pre, grad_h_post, grad_H_merged, grad_proj,
-                                                      partial, T);
+      k2_bwd_kernel<true><<<grid, kK2Threads, 0, s>>>(proj, P, grad_h_pre, grad_h_post, grad_H_merged,
+                                                      grad_proj, partial, T);
     else
-      k2_bwd_kernel<false><<<grid, kK2Threads, 0, s>>>(proj, alpha_pre, alpha_post, alpha_res, bias, perm,
-                                                       grad_h_pre, grad_h_post, grad_H_merged, grad_proj,
-                                                       partial, T);
+      k2_bwd_kernel<false><<<grid, kK2Threads, 0, s>>>(proj, P, grad_h_pre, grad_h_post, grad_H_merged,
+                                                       grad_proj, partial, T);
     const int st = launch_status();
     if (st != FMHC_OK) return st;
   }
   // T == 0: the reduce writes zero gradients (nblocks = 0 partials).
   k2_param_reduce<<<dim3(kNPar), kWave, 0, s>>>(partial, T > 0 ? nblocks : 0, grad_alpha_pre,
-                                                grad_alpha_post, grad_alpha_res, grad_bias);
+                                                grad_alpha_post, grad_alpha_res, grad_bias, P.bf16);
   return launch_status();
 }

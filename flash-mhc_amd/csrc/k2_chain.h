@@ -1,5 +1,5 @@
 // Per-token pieces of K2, the mHC-lite coefficient chain (block.py:161-170 of
-// alint77/flash-mHC), shared by the K2 kernels and the one-pass pre-map kernel.
+// alint77/flash-mHC), used by the K2 kernels.
 // Every value the reference holds in a bf16 tensor is rounded with rb(); the
 // fp32 operations run in the reference's order, with contraction off.
 #pragma once
@@ -14,13 +14,39 @@ constexpr int kDk = 2 * kN + kNF;   // 32 projection columns
 constexpr int kNPar = 3 + kDk;      // alpha_pre, alpha_post, alpha_res, bias[32]
 __device__ __forceinline__ float rb(float v) { return bf16_to_f32(f32_to_bf16(v)); }
 
+// The block parameters K2 reads, in their storage dtype: all fp32 or all bf16
+// (bf16 = true).  Every value is rounded to bf16 on use, so the two give the
+// same results.
+struct K2Params {
+  const void* alpha_pre;
+  const void* alpha_post;
+  const void* alpha_res;
+  const void* bias;
+  const void* perm;
+  bool bf16;
+};
+
+__device__ __forceinline__ float ld_param(const void* p, int i, bool bf16) {
+  return bf16 ? bf16_to_f32(static_cast<const uint16_t*>(p)[i]) : static_cast<const float*>(p)[i];
+}
+
 // perm (24 x 16) rounded to bf16 (the reference multiplies by perm_mat.to(bf16)),
 // staged in LDS once per block; every lane then reads the same rows (broadcast).
 template <int THREADS>
-__device__ __forceinline__ void stage_perm(const float* __restrict__ perm, f32x4 sperm[kNF * 4]) {
+__device__ __forceinline__ void stage_perm(const K2Params& P, f32x4 sperm[kNF * 4]) {
   float* s = reinterpret_cast<float*>(sperm);
-  for (int i = threadIdx.x; i < kNF * kN * kN; i += THREADS) s[i] = rb(perm[i]);
+  for (int i = threadIdx.x; i < kNF * kN * kN; i += THREADS) s[i] = rb(ld_param(P.perm, i, P.bf16));
   __syncthreads();
+}
+
+// bf16(alpha_pre), bf16(alpha_post), bf16(alpha_res) and bf16(bias), the
+// values the reference's ops see after .to(bf16).
+__device__ __forceinline__ void load_params(const K2Params& P, float& ap, float& apo, float& ar, float b[kDk]) {
+  ap = rb(ld_param(P.alpha_pre, 0, P.bf16));
+  apo = rb(ld_param(P.alpha_post, 0, P.bf16));
+  ar = rb(ld_param(P.alpha_res, 0, P.bf16));
+#pragma unroll
+  for (int k = 0; k < kDk; ++k) b[k] = rb(ld_param(P.bias, k, P.bf16));
 }
 
 __device__ __forceinline__ float sigmoid_f32(float z) {
@@ -47,16 +73,16 @@ struct K2Fwd {
 };
 
 __device__ __forceinline__ void k2_chain(const float p[kDk], float ap, float apo, float ar,
-                                         const float* __restrict__ bias, K2Fwd& f) {
+                                         const float b[kDk], K2Fwd& f) {
 #pragma clang fp contract(off)
 #pragma unroll
   for (int j = 0; j < kN; ++j) {
-    const float z = rb(rb(ap * p[j]) + rb(bias[j]));
+    const float z = rb(rb(ap * p[j]) + b[j]);
     f.hp[j] = rb(sigmoid_f32(z));
   }
 #pragma unroll
   for (int j = 0; j < kN; ++j) {
-    const float z = rb(rb(apo * p[kN + j]) + rb(bias[kN + j]));
+    const float z = rb(rb(apo * p[kN + j]) + b[kN + j]);
     f.sq[j] = rb(sigmoid_f32(z));
     f.hq[j] = rb(2.f * f.sq[j]);
   }
@@ -64,7 +90,7 @@ __device__ __forceinline__ void k2_chain(const float p[kDk], float ap, float apo
   float mx = -INFINITY;
 #pragma unroll
   for (int m = 0; m < kNF; ++m) {
-    z[m] = rb(rb(ar * p[2 * kN + m]) + rb(bias[2 * kN + m]));
+    z[m] = rb(rb(ar * p[2 * kN + m]) + b[2 * kN + m]);
     mx = fmaxf(mx, z[m]);
   }
   float sum = 0.f;

@@ -21,12 +21,24 @@ namespace {
 
 constexpr int kBlock = 256;  // 4 waves per workgroup
 
+// LPT <= 64: 64 / LPT tokens per wave.  LPT = 128 or 256 (forward kernels,
+// few tokens): LPT / 64 waves per token.
 template <int LPT>
 __device__ __forceinline__ int64_t token_of_lane(int lane) {
-  constexpr int TPW = kWave / LPT;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
-  const int64_t first = (static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) + wave) * TPW;
-  return LPT == kWave ? first : first + lane / LPT;
+  if constexpr (LPT > kWave) {
+    return static_cast<int64_t>(blockIdx.x) * (kBlock / LPT) + wave / (LPT / kWave);
+  } else {
+    constexpr int TPW = kWave / LPT;
+    const int64_t first = (static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) + wave) * TPW;
+    return LPT == kWave ? first : first + lane / LPT;
+  }
+}
+
+// Position of this lane among its token's LPT lanes.
+template <int LPT>
+__device__ __forceinline__ int sub_of_lane() {
+  return static_cast<int>(threadIdx.x) % LPT;
 }
 
 template <int VEC, int LPT>
@@ -39,7 +51,7 @@ __global__ __launch_bounds__(kBlock) void k4_fwd_kernel(const uint16_t* __restri
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t tok = token_of_lane<LPT>(lane);
   if (tok >= T) return;
-  const int sub = lane % LPT;
+  const int sub = sub_of_lane<LPT>();
   const int ng = C / VEC;
 
   float h[4][4], p[4];
@@ -206,13 +218,26 @@ int pick_lpt(int C) {
   return 8;
 }
 
+// Forward kernels with few tokens spread a token over more lanes (up to a
+// workgroup), so that each lane has one or two 8-element groups per stream
+// instead of a loop: latency, not bandwidth, bounds that regime.
+template <int VEC>
+int pick_lpt_fwd(int C, int64_t T) {
+  const int lpt = pick_lpt<VEC>(C);
+  const int groups = C / VEC;
+  if (T * lpt < int64_t{256} * kBlock && groups >= 128) return groups >= 256 ? 256 : 128;
+  return lpt;
+}
+
 template <int VEC>
 int launch_k4_fwd(const uint16_t* x, const uint16_t* lo, const float* H, const float* hp,
                   uint16_t* out, int64_t T, int C, hipStream_t s) {
-  const int lpt = pick_lpt<VEC>(C);
-  const int64_t tokens_per_block = (kBlock / kWave) * (kWave / lpt);
+  const int lpt = pick_lpt_fwd<VEC>(C, T);
+  const int64_t tokens_per_block = lpt > kWave ? kBlock / lpt : (kBlock / kWave) * (kWave / lpt);
   const dim3 grid(blocks_for(T, tokens_per_block));
   switch (lpt) {
+    case 256: k4_fwd_kernel<VEC, 256><<<grid, kBlock, 0, s>>>(x, lo, H, hp, out, T, C); break;
+    case 128: k4_fwd_kernel<VEC, 128><<<grid, kBlock, 0, s>>>(x, lo, H, hp, out, T, C); break;
     case 64: k4_fwd_kernel<VEC, 64><<<grid, kBlock, 0, s>>>(x, lo, H, hp, out, T, C); break;
     case 32: k4_fwd_kernel<VEC, 32><<<grid, kBlock, 0, s>>>(x, lo, H, hp, out, T, C); break;
     case 16: k4_fwd_kernel<VEC, 16><<<grid, kBlock, 0, s>>>(x, lo, H, hp, out, T, C); break;

@@ -11,7 +11,8 @@
 // (bf16(grad_x_in + pre-map gradient), autograd's sum), which replaces
 // autograd's separate accumulation pass (1.5 x T x nC x 2 bytes).
 //
-// Forward: K1 -> K2 -> K3, the three kernels of k1.hip, k2.hip, k3.hip.  A
+// Forward: K1 -> K2 -> K3, the three kernels of k1.hip, k2.hip, k3.hip (K1
+// split over the columns for few tokens, with the caller's workspace).  A
 // one-pass variant that kept each token tile of x in LDS between K1 and K3
 // (saving K3's read of x) was built and measured slower on gfx950 at
 // C <= 1024: with tiles of 8-16 tokens every tile re-reads the whole of W
@@ -30,6 +31,9 @@ namespace {
 constexpr int64_t kAlign = 256;
 int64_t round_up(int64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
+// Checked before the first launch, so that a bad dtype leaves no partial outputs.
+bool param_dtype_ok(int d) { return d == FMHC_PARAM_F32 || d == FMHC_PARAM_BF16; }
+
 struct PremapWs {
   int64_t gh, gp, k2, k1, total;  // byte offsets / sizes
 };
@@ -46,19 +50,26 @@ PremapWs premap_ws(int64_t T, int64_t C) {
 
 }  // namespace
 
-extern "C" int fmhc_premap_fwd(const uint16_t* x, const uint16_t* W, const float* alpha_pre,
-                               const float* alpha_post, const float* alpha_res, const float* bias,
-                               const float* perm, uint16_t* layer_input, uint16_t* proj,
+extern "C" int64_t fmhc_premap_fwd_workspace_bytes(int64_t T, int64_t C) {
+  if (T <= 0 || C <= 0) return 0;
+  return fmhc_k1_fwd_workspace_bytes(T, 4 * C);
+}
+
+extern "C" int fmhc_premap_fwd(const uint16_t* x, const uint16_t* W, const void* alpha_pre,
+                               const void* alpha_post, const void* alpha_res, const void* bias,
+                               const void* perm, int param_dtype, uint16_t* layer_input, uint16_t* proj,
                                float* inv_rms, float* h_pre, float* h_post, float* H_merged,
-                               int64_t T, int64_t C, int64_t n, void* stream) {
-  if (T < 0 || C <= 0 || n != 4) return FMHC_ERR_INVALID_ARGUMENT;
+                               void* workspace, int64_t workspace_bytes, int64_t T, int64_t C, int64_t n,
+                               void* stream) {
+  if (T < 0 || C <= 0 || n != 4 || !param_dtype_ok(param_dtype)) return FMHC_ERR_INVALID_ARGUMENT;
   if (T == 0) return FMHC_OK;
   if (!x || !W || !alpha_pre || !alpha_post || !alpha_res || !bias || !perm || !layer_input || !proj ||
       !inv_rms || !h_pre || !h_post || !H_merged)
     return FMHC_ERR_INVALID_ARGUMENT;
-  int st = fmhc_k1_fwd(x, W, proj, inv_rms, T, n * C, 32, stream);
+  int st = fmhc_k1_fwd_ws(x, W, proj, inv_rms, workspace, workspace_bytes, T, n * C, 32, stream);
   if (st == FMHC_OK)
-    st = fmhc_k2_fwd(proj, alpha_pre, alpha_post, alpha_res, bias, perm, h_pre, h_post, H_merged, T, n, stream);
+    st = fmhc_k2_fwd(proj, alpha_pre, alpha_post, alpha_res, bias, perm, param_dtype, h_pre, h_post, H_merged, T,
+                     n, stream);
   if (st == FMHC_OK) st = fmhc_k3_fwd(x, h_pre, layer_input, T, C, n, stream);
   return st;
 }
@@ -68,17 +79,18 @@ extern "C" int64_t fmhc_premap_bwd_workspace_bytes(int64_t T, int64_t C) {
   return premap_ws(T, C).total;
 }
 
-extern "C" int fmhc_premap_bwd(const uint16_t* x, const uint16_t* W, const float* alpha_pre,
-                               const float* alpha_post, const float* alpha_res, const float* bias,
-                               const float* perm, const float* h_pre, const uint16_t* proj,
+extern "C" int fmhc_premap_bwd(const uint16_t* x, const uint16_t* W, const void* alpha_pre,
+                               const void* alpha_post, const void* alpha_res, const void* bias,
+                               const void* perm, int param_dtype, const float* h_pre, const uint16_t* proj,
                                const float* inv_rms, const uint16_t* grad_layer_input,
                                const float* grad_h_post, const float* grad_H_merged,
                                const uint16_t* grad_x_in, uint16_t* grad_x,
-                               uint16_t* grad_W, float* grad_alpha_pre, float* grad_alpha_post,
-                               float* grad_alpha_res, float* grad_bias, void* workspace,
+                               uint16_t* grad_W, void* grad_alpha_pre, void* grad_alpha_post,
+                               void* grad_alpha_res, void* grad_bias, void* workspace,
                                int64_t workspace_bytes, int64_t T, int64_t C, int64_t n, void* stream) {
   using namespace fmhc;
-  if (T < 0 || C <= 0 || C > (int64_t{1} << 24) || n != 4) return FMHC_ERR_INVALID_ARGUMENT;
+  if (T < 0 || C <= 0 || C > (int64_t{1} << 24) || n != 4 || !param_dtype_ok(param_dtype))
+    return FMHC_ERR_INVALID_ARGUMENT;
   if (!W || !alpha_pre || !alpha_post || !alpha_res || !bias || !perm || !grad_W || !grad_alpha_pre ||
       !grad_alpha_post || !grad_alpha_res || !grad_bias)
     return FMHC_ERR_INVALID_ARGUMENT;
@@ -98,7 +110,8 @@ extern "C" int fmhc_premap_bwd(const uint16_t* x, const uint16_t* W, const float
   const bool fused = T > 0 && k1_bwd_premap_fused(x, W, gp, proj, grad_x, grad_layer_input, grad_x_in, C);
   if (T > 0) st = fmhc_k3_bwd(x, h_pre, grad_layer_input, fused ? nullptr : grad_x, gh, T, C, n, stream);
   if (st == FMHC_OK)
-    st = fmhc_k2_bwd(proj, alpha_pre, alpha_post, alpha_res, bias, perm, gh, grad_h_post, grad_H_merged, gp,
+    st = fmhc_k2_bwd(proj, alpha_pre, alpha_post, alpha_res, bias, perm, param_dtype, gh, grad_h_post,
+                     grad_H_merged, gp,
                      grad_alpha_pre, grad_alpha_post, grad_alpha_res, grad_bias, T > 0 ? ws + w.k2 : nullptr,
                      T > 0 ? w.k1 - w.k2 : 0, T, n, stream);
   if (st == FMHC_OK)

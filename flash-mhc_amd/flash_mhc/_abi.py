@@ -22,18 +22,22 @@ LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libflash_mhc_hip.so"
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
+_INT = ctypes.c_int
 
 # name -> argtypes, following include/flash_mhc_hip.h and include/flash_mhc_probe.h
 SIGNATURES: dict[str, list] = {
     "fmhc_k1_fwd": [_P, _P, _P, _P, _I64, _I64, _I64, _P],
+    "fmhc_k1_fwd_ws": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
+    "fmhc_k1_fwd_workspace_bytes": [_I64, _I64],
     "fmhc_k1_bwd_dx": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
     "fmhc_k1_bwd": [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
     "fmhc_k1_bwd_workspace_bytes": [_I64, _I64],
-    "fmhc_k2_fwd": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _P],
-    "fmhc_k2_bwd": [_P] * 15 + [_I64, _I64, _I64, _P],
+    "fmhc_k2_fwd": [_P] * 6 + [_INT] + [_P] * 3 + [_I64, _I64, _P],
+    "fmhc_k2_bwd": [_P] * 6 + [_INT] + [_P] * 9 + [_I64, _I64, _I64, _P],
     "fmhc_k2_bwd_workspace_bytes": [_I64],
-    "fmhc_premap_fwd": [_P] * 13 + [_I64, _I64, _I64, _P],
-    "fmhc_premap_bwd": [_P] * 21 + [_I64, _I64, _I64, _I64, _P],
+    "fmhc_premap_fwd": [_P] * 7 + [_INT] + [_P] * 7 + [_I64, _I64, _I64, _I64, _P],
+    "fmhc_premap_fwd_workspace_bytes": [_I64, _I64],
+    "fmhc_premap_bwd": [_P] * 7 + [_INT] + [_P] * 14 + [_I64, _I64, _I64, _I64, _P],
     "fmhc_premap_bwd_workspace_bytes": [_I64, _I64],
     "fmhc_k3_fwd": [_P, _P, _P, _I64, _I64, _I64, _P],
     "fmhc_k3_bwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
@@ -46,11 +50,13 @@ SIGNATURES: dict[str, list] = {
 RESTYPES = {
     "fmhc_error_string": ctypes.c_char_p,
     "fmhc_k1_bwd_workspace_bytes": ctypes.c_int64,
+    "fmhc_k1_fwd_workspace_bytes": ctypes.c_int64,
+    "fmhc_premap_fwd_workspace_bytes": ctypes.c_int64,
     "fmhc_k2_bwd_workspace_bytes": ctypes.c_int64,
     "fmhc_premap_bwd_workspace_bytes": ctypes.c_int64,
 }
 
-ABI_VERSION = 3
+ABI_VERSION = 5
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -76,7 +76,8 @@ class _OnDevice:
 
 def k1_fwd(x_flat: torch.Tensor, W: torch.Tensor, out: torch.Tensor | None = None,
            inv_rms: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
-    """proj (T, 32) bf16 and inv_rms (T,) fp32 from x_flat (T, nC) bf16, W (32, nC) bf16."""
+    """proj (T, 32) bf16 and inv_rms (T,) fp32 from x_flat (T, nC) bf16, W (32, nC) bf16
+    (fmhc_k1_fwd_ws: few tokens split the nC axis over workgroups)."""
     dev = _device_of(x_flat)
     if x_flat.dim() != 2:
         raise ValueError(f"x_flat must be 2-D (T, nC), got shape {tuple(x_flat.shape)}")
@@ -92,9 +93,11 @@ def k1_fwd(x_flat: torch.Tensor, W: torch.Tensor, out: torch.Tensor | None = Non
     _require(out, "out", _BF16, (T, D_OUT), dev)
     _require(inv_rms, "inv_rms", _F32, (T,), dev)
     lib = _abi.load()
+    ws = _workspace(int(lib.fmhc_k1_fwd_workspace_bytes(T, nC)), dev)
     with _OnDevice(dev):
-        st = lib.fmhc_k1_fwd(x_flat.data_ptr(), W.data_ptr(), out.data_ptr(), inv_rms.data_ptr(),
-                             T, nC, D_OUT, _abi.stream_of(x_flat))
+        st = lib.fmhc_k1_fwd_ws(x_flat.data_ptr(), W.data_ptr(), out.data_ptr(), inv_rms.data_ptr(),
+                                _ptr_or_none(ws), 0 if ws is None else ws.numel(), T, nC, D_OUT,
+                                _abi.stream_of(x_flat))
     _abi.check(st, "k1_fwd")
     return out, inv_rms
 
@@ -159,11 +162,19 @@ def k1_bwd(grad_out: torch.Tensor, x_flat: torch.Tensor, W: torch.Tensor,
 N_PERM = 24  # n! at n = 4
 
 
-def _k2_params(alpha_pre, alpha_post, alpha_res, bias, perm, dev):
+PARAM_DTYPES = {_F32: 0, _BF16: 1}  # FMHC_PARAM_F32, FMHC_PARAM_BF16
+
+
+def _k2_params(alpha_pre, alpha_post, alpha_res, bias, perm, dev) -> int:
+    """Check K2's parameters (all fp32 or all bf16) and return the ABI's dtype code."""
+    dt = alpha_pre.dtype if isinstance(alpha_pre, torch.Tensor) else None
+    if dt not in PARAM_DTYPES:
+        raise TypeError(f"K2 parameters must be float32 or bfloat16, got {dt}")
     for t, name, shape in ((alpha_pre, "alpha_pre", (1,)), (alpha_post, "alpha_post", (1,)),
                            (alpha_res, "alpha_res", (1,)), (bias, "bias", (D_OUT,)),
                            (perm, "perm", (N_PERM, N_STREAMS * N_STREAMS))):
-        _require(t, name, _F32, shape, dev)
+        _require(t, name, dt, shape, dev)
+    return PARAM_DTYPES[dt]
 
 
 def k2_fwd(proj: torch.Tensor, alpha_pre: torch.Tensor, alpha_post: torch.Tensor,
@@ -171,20 +182,20 @@ def k2_fwd(proj: torch.Tensor, alpha_pre: torch.Tensor, alpha_post: torch.Tensor
            ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """(h_pre (T,4), h_post (T,4), H_merged (T,4,4)) fp32 from proj (T,32) bf16,
     with the bf16 rounding points of the reference's coefficient ops.
-    Parameters are fp32 tensors: alphas (1,), bias (32,), perm (24,16)."""
+    Parameters: alphas (1,), bias (32,), perm (24,16), all fp32 or all bf16."""
     dev = _device_of(proj)
     if proj.dim() != 2:
         raise ValueError(f"proj must be 2-D (T, 32), got shape {tuple(proj.shape)}")
     T = proj.shape[0]
     _require(proj, "proj", _BF16, (T, D_OUT), dev)
-    _k2_params(alpha_pre, alpha_post, alpha_res, bias, perm, dev)
+    pdt = _k2_params(alpha_pre, alpha_post, alpha_res, bias, perm, dev)
     h_pre = torch.empty((T, N_STREAMS), device=dev, dtype=_F32)
     h_post = torch.empty((T, N_STREAMS), device=dev, dtype=_F32)
     H = torch.empty((T, N_STREAMS, N_STREAMS), device=dev, dtype=_F32)
     lib = _abi.load()
     with _OnDevice(dev):
         st = lib.fmhc_k2_fwd(proj.data_ptr(), alpha_pre.data_ptr(), alpha_post.data_ptr(),
-                             alpha_res.data_ptr(), bias.data_ptr(), perm.data_ptr(), h_pre.data_ptr(),
+                             alpha_res.data_ptr(), bias.data_ptr(), perm.data_ptr(), pdt, h_pre.data_ptr(),
                              h_post.data_ptr(), H.data_ptr(), T, N_STREAMS, _abi.stream_of(proj))
     _abi.check(st, "k2_fwd")
     return h_pre, h_post, H
@@ -195,31 +206,31 @@ def k2_bwd(proj: torch.Tensor, alpha_pre: torch.Tensor, alpha_post: torch.Tensor
            grad_h_pre: torch.Tensor | None, grad_h_post: torch.Tensor | None,
            grad_H: torch.Tensor | None):
     """Gradients of k2_fwd: (grad_proj (T,32) bf16, grad_alpha_pre (1,),
-    grad_alpha_post (1,), grad_alpha_res (1,), grad_bias (32,)), fp32 parameter
-    gradients.  A None output gradient counts as zero."""
+    grad_alpha_post (1,), grad_alpha_res (1,), grad_bias (32,)), parameter
+    gradients in the parameters' dtype.  A None output gradient counts as zero."""
     dev = _device_of(proj)
     if proj.dim() != 2:
         raise ValueError(f"proj must be 2-D (T, 32), got shape {tuple(proj.shape)}")
     T = proj.shape[0]
     _require(proj, "proj", _BF16, (T, D_OUT), dev)
-    _k2_params(alpha_pre, alpha_post, alpha_res, bias, perm, dev)
+    pdt = _k2_params(alpha_pre, alpha_post, alpha_res, bias, perm, dev)
     for t, name, shape in ((grad_h_pre, "grad_h_pre", (T, N_STREAMS)),
                            (grad_h_post, "grad_h_post", (T, N_STREAMS)),
                            (grad_H, "grad_H_merged", (T, N_STREAMS, N_STREAMS))):
         if t is not None:
             _require(t, name, _F32, shape, dev)
     grad_proj = torch.empty((T, D_OUT), device=dev, dtype=_BF16)
-    g_ap = torch.empty((1,), device=dev, dtype=_F32)
-    g_apo = torch.empty((1,), device=dev, dtype=_F32)
-    g_ar = torch.empty((1,), device=dev, dtype=_F32)
-    g_b = torch.empty((D_OUT,), device=dev, dtype=_F32)
+    g_ap = torch.empty((1,), device=dev, dtype=alpha_pre.dtype)
+    g_apo = torch.empty((1,), device=dev, dtype=alpha_pre.dtype)
+    g_ar = torch.empty((1,), device=dev, dtype=alpha_pre.dtype)
+    g_b = torch.empty((D_OUT,), device=dev, dtype=alpha_pre.dtype)
     lib = _abi.load()
     nbytes = int(lib.fmhc_k2_bwd_workspace_bytes(T))
     ws = torch.empty((max(nbytes, 16),), device=dev, dtype=torch.uint8)
     ptr = lambda t: None if t is None else t.data_ptr()
     with _OnDevice(dev):
         st = lib.fmhc_k2_bwd(proj.data_ptr(), alpha_pre.data_ptr(), alpha_post.data_ptr(),
-                             alpha_res.data_ptr(), bias.data_ptr(), perm.data_ptr(), ptr(grad_h_pre),
+                             alpha_res.data_ptr(), bias.data_ptr(), perm.data_ptr(), pdt, ptr(grad_h_pre),
                              ptr(grad_h_post), ptr(grad_H), grad_proj.data_ptr(), g_ap.data_ptr(),
                              g_apo.data_ptr(), g_ar.data_ptr(), g_b.data_ptr(), ws.data_ptr(), ws.numel(),
                              T, N_STREAMS, _abi.stream_of(proj))
@@ -236,7 +247,7 @@ def premap_fwd(x_streams: torch.Tensor, W: torch.Tensor, alpha_pre: torch.Tensor
     dev = _device_of(x_streams)
     _require(x_streams, "x_streams", _BF16, (T, n, C), dev)
     _require(W, "W", _BF16, (D_OUT, n * C), dev)
-    _k2_params(alpha_pre, alpha_post, alpha_res, bias, perm, dev)
+    pdt = _k2_params(alpha_pre, alpha_post, alpha_res, bias, perm, dev)
     li = torch.empty((T, C), device=dev, dtype=_BF16)
     proj = torch.empty((T, D_OUT), device=dev, dtype=_BF16)
     inv = torch.empty((T,), device=dev, dtype=_F32)
@@ -244,12 +255,13 @@ def premap_fwd(x_streams: torch.Tensor, W: torch.Tensor, alpha_pre: torch.Tensor
     h_post = torch.empty((T, n), device=dev, dtype=_F32)
     H = torch.empty((T, n, n), device=dev, dtype=_F32)
     lib = _abi.load()
+    ws = _workspace(int(lib.fmhc_premap_fwd_workspace_bytes(T, C)), dev)
     with _OnDevice(dev):
         st = lib.fmhc_premap_fwd(x_streams.data_ptr(), W.data_ptr(), alpha_pre.data_ptr(),
                                  alpha_post.data_ptr(), alpha_res.data_ptr(), bias.data_ptr(),
-                                 perm.data_ptr(), li.data_ptr(), proj.data_ptr(), inv.data_ptr(),
-                                 h_pre.data_ptr(), h_post.data_ptr(), H.data_ptr(), T, C, n,
-                                 _abi.stream_of(x_streams))
+                                 perm.data_ptr(), pdt, li.data_ptr(), proj.data_ptr(), inv.data_ptr(),
+                                 h_pre.data_ptr(), h_post.data_ptr(), H.data_ptr(), _ptr_or_none(ws),
+                                 0 if ws is None else ws.numel(), T, C, n, _abi.stream_of(x_streams))
     _abi.check(st, "premap_fwd")
     return li, H, h_post, h_pre, proj, inv
 
@@ -260,13 +272,13 @@ def premap_bwd(x_streams: torch.Tensor, W: torch.Tensor, alpha_pre: torch.Tensor
                grad_layer_input: torch.Tensor, grad_h_post: torch.Tensor | None,
                grad_H: torch.Tensor | None, grad_x_in: torch.Tensor | None = None):
     """Gradients of premap_fwd's inputs: (grad_x (T,4,C) bf16, grad_W (32,4C) bf16,
-    grad_alpha_pre, grad_alpha_post, grad_alpha_res (1,), grad_bias (32,) fp32).
+    grad_alpha_pre, grad_alpha_post, grad_alpha_res (1,), grad_bias (32,) in the parameters' dtype).
     grad_x_in (T,4,C) bf16, optional: a further gradient of x, added (bf16) into grad_x."""
     T, n, C = _streams_shape(x_streams)
     dev = _device_of(x_streams)
     _require(x_streams, "x_streams", _BF16, (T, n, C), dev)
     _require(W, "W", _BF16, (D_OUT, n * C), dev)
-    _k2_params(alpha_pre, alpha_post, alpha_res, bias, perm, dev)
+    pdt = _k2_params(alpha_pre, alpha_post, alpha_res, bias, perm, dev)
     _require(h_pre, "h_pre", _F32, (T, n), dev)
     _require(proj, "proj", _BF16, (T, D_OUT), dev)
     _require(inv_rms, "inv_rms", _F32, (T,), dev)
@@ -279,8 +291,8 @@ def premap_bwd(x_streams: torch.Tensor, W: torch.Tensor, alpha_pre: torch.Tensor
         _require(grad_x_in, "grad_x_in", _BF16, (T, n, C), dev)
     gx = torch.empty_like(x_streams)
     gW = torch.empty((D_OUT, n * C), device=dev, dtype=_BF16)
-    ga = [torch.empty((1,), device=dev, dtype=_F32) for _ in range(3)]
-    gb = torch.empty((D_OUT,), device=dev, dtype=_F32)
+    ga = [torch.empty((1,), device=dev, dtype=alpha_pre.dtype) for _ in range(3)]
+    gb = torch.empty((D_OUT,), device=dev, dtype=alpha_pre.dtype)
     lib = _abi.load()
     nbytes = int(lib.fmhc_premap_bwd_workspace_bytes(T, C))
     ws = torch.empty((max(nbytes, 16),), device=dev, dtype=torch.uint8)
@@ -288,13 +300,22 @@ def premap_bwd(x_streams: torch.Tensor, W: torch.Tensor, alpha_pre: torch.Tensor
     with _OnDevice(dev):
         st = lib.fmhc_premap_bwd(x_streams.data_ptr(), W.data_ptr(), alpha_pre.data_ptr(),
                                  alpha_post.data_ptr(), alpha_res.data_ptr(), bias.data_ptr(),
-                                 perm.data_ptr(), h_pre.data_ptr(), proj.data_ptr(), inv_rms.data_ptr(),
+                                 perm.data_ptr(), pdt, h_pre.data_ptr(), proj.data_ptr(), inv_rms.data_ptr(),
                                  grad_layer_input.data_ptr(), ptr(grad_h_post), ptr(grad_H), ptr(grad_x_in),
                                  gx.data_ptr(),
                                  gW.data_ptr(), ga[0].data_ptr(), ga[1].data_ptr(), ga[2].data_ptr(),
                                  gb.data_ptr(), ws.data_ptr(), ws.numel(), T, C, n, _abi.stream_of(x_streams))
     _abi.check(st, "premap_bwd")
     return gx, gW, ga[0], ga[1], ga[2], gb
+
+
+def _workspace(nbytes: int, dev) -> torch.Tensor | None:
+    """A uint8 device buffer of nbytes (16-byte aligned: torch's allocations are), or None for 0."""
+    return torch.empty((nbytes,), device=dev, dtype=torch.uint8) if nbytes > 0 else None
+
+
+def _ptr_or_none(t: torch.Tensor | None):
+    return None if t is None else t.data_ptr()
 
 
 def _streams_shape(x: torch.Tensor) -> tuple[int, int, int]:

@@ -238,6 +238,15 @@ def _coeff(t: torch.Tensor) -> torch.Tensor:
     return t.to(torch.float32).contiguous()
 
 
+def _params(*ts: torch.Tensor) -> list[torch.Tensor]:
+    """K2's parameters (alphas, bias, perm) as the kernels take them: in their
+    own dtype when all are fp32 or all bf16 (no conversion launches), else fp32."""
+    dt = ts[0].dtype
+    if dt in (torch.float32, torch.bfloat16) and all(t.dtype == dt for t in ts):
+        return [t.contiguous() for t in ts]
+    return [_coeff(t) for t in ts]
+
+
 @torch.library.impl(_lib, "fused_rmsnorm_project", "CUDA")
 def _fused_rmsnorm_project_cuda(x_flat: torch.Tensor, W: torch.Tensor):
     return _k.k1_fwd(x_flat.contiguous(), W.contiguous())
@@ -266,8 +275,7 @@ def _check_k2(proj: torch.Tensor, perm_mat: torch.Tensor) -> None:
 @torch.library.impl(_lib, "mhc_coefficients", "CUDA")
 def _mhc_coefficients_cuda(proj, alpha_pre, alpha_post, alpha_res, bias, perm_mat):
     _check_k2(proj, perm_mat)
-    return _k.k2_fwd(proj.contiguous(), _coeff(alpha_pre), _coeff(alpha_post), _coeff(alpha_res),
-                     _coeff(bias), _coeff(perm_mat))
+    return _k.k2_fwd(proj.contiguous(), *_params(alpha_pre, alpha_post, alpha_res, bias, perm_mat))
 
 
 @torch.library.impl(_lib, "mhc_coefficients_backward", "CUDA")
@@ -275,8 +283,8 @@ def _mhc_coefficients_backward_cuda(grad_h_pre, grad_h_post, grad_H_merged, proj
                                     alpha_post, alpha_res, bias, perm_mat):
     _check_k2(proj, perm_mat)
     g = [None if t is None else _coeff(t) for t in (grad_h_pre, grad_h_post, grad_H_merged)]
-    gp, ga1, ga2, ga3, gb = _k.k2_bwd(proj.contiguous(), _coeff(alpha_pre), _coeff(alpha_post),
-                                      _coeff(alpha_res), _coeff(bias), _coeff(perm_mat), *g)
+    gp, ga1, ga2, ga3, gb = _k.k2_bwd(proj.contiguous(), *_params(alpha_pre, alpha_post, alpha_res, bias,
+                                                                 perm_mat), *g)
     # Parameter gradients in the parameters' dtype (exact: the values are bf16).
     return (gp, ga1.to(alpha_pre.dtype), ga2.to(alpha_post.dtype), ga3.to(alpha_res.dtype),
             gb.to(bias.dtype))
@@ -286,8 +294,8 @@ def _mhc_coefficients_backward_cuda(grad_h_pre, grad_h_post, grad_H_merged, proj
 def _mhc_pre_map_cuda(x_streams, W, alpha_pre, alpha_post, alpha_res, bias, perm_mat):
     _check_n4(x_streams, "flash_mhc::mhc_pre_map supports n=4 only")
     _check_k2(x_streams.new_empty((0, W.shape[0])), perm_mat)
-    outs = _k.premap_fwd(x_streams.contiguous(), W.to(x_streams.dtype).contiguous(), _coeff(alpha_pre),
-                         _coeff(alpha_post), _coeff(alpha_res), _coeff(bias), _coeff(perm_mat))
+    outs = _k.premap_fwd(x_streams.contiguous(), W.to(x_streams.dtype).contiguous(),
+                         *_params(alpha_pre, alpha_post, alpha_res, bias, perm_mat))
     return (*outs, _x_sink(x_streams))
 
 
@@ -299,7 +307,7 @@ def _mhc_pre_map_backward_cuda(grad_layer_input, grad_H_merged, grad_h_post, gra
     x = x_streams.contiguous()
     T, n, C = x.shape
     Wc = W.to(x.dtype).contiguous()
-    coeffs = [_coeff(t) for t in (alpha_pre, alpha_post, alpha_res, bias, perm_mat)]
+    coeffs = _params(alpha_pre, alpha_post, alpha_res, bias, perm_mat)
     g_li = (torch.zeros((T, C), device=x.device, dtype=x.dtype) if grad_layer_input is None
             else grad_layer_input.to(x.dtype).contiguous())
     g_hp = None if grad_h_post is None else _coeff(grad_h_post)

@@ -35,7 +35,12 @@ extern "C" {
 #define FMHC_ERR_INVALID_ARGUMENT 1 /* negative size, n != 4, D_out != 32, null pointer */
 #define FMHC_ERR_HIP_BASE 1000      /* + hipError_t from the launch */
 
-#define FMHC_ABI_VERSION 3
+#define FMHC_ABI_VERSION 5
+
+/* Storage dtype of the block parameters K2 reads (alpha_pre, alpha_post,
+ * alpha_res, bias, perm: all five the same) and of their gradients. */
+#define FMHC_PARAM_F32 0
+#define FMHC_PARAM_BF16 1
 
 /* K1 forward: fused RMSNorm + projection.
  *   inv_rms[t] = rsqrt(sum_k x[t,k]^2 / nC + 1e-6)
@@ -45,6 +50,16 @@ extern "C" {
  *           src/flash_mhc/kernels.py:250-303 (_fused_rmsnorm_project_fwd_kernel). */
 int fmhc_k1_fwd(const uint16_t* x_flat, const uint16_t* W, uint16_t* out, float* inv_rms,
                 int64_t T, int64_t nC, int64_t D_out, void* stream);
+/* fmhc_k1_fwd with a workspace: for few tokens (T < 8192) the nC axis is split
+ * over up to 64 workgroups per 16-token block, whose fp32 partial sums (in
+ * `workspace`) a second kernel adds in a fixed order.  `workspace`: at least
+ * fmhc_k1_fwd_workspace_bytes(T, nC) bytes, 16-byte aligned (may be NULL when
+ * that is 0).  Results equal fmhc_k1_fwd's up to fp32 summation order.  No
+ * counterpart in the reference (its kernel has one program per token tile). */
+int fmhc_k1_fwd_ws(const uint16_t* x_flat, const uint16_t* W, uint16_t* out, float* inv_rms,
+                   void* workspace, int64_t workspace_bytes, int64_t T, int64_t nC, int64_t D_out,
+                   void* stream);
+int64_t fmhc_k1_fwd_workspace_bytes(int64_t T, int64_t nC);
 
 /* K1 backward, grad of x_flat:
  *   scale[t]    = (sum_d go[t,d] * proj_out[t,d]) * inv_rms[t]^2 / nC
@@ -81,13 +96,15 @@ int64_t fmhc_k1_bwd_workspace_bytes(int64_t T, int64_t nC);
  *   a[m]          = bf16(softmax_m(bf16(bf16(a_res * p[8+m]) + b[8+m])))
  *   H_merged[t,i,j] = bf16(bf16(sum_m a[m] perm[m, 4i+j]) - bf16(h_post[t,i] h_pre[t,j]))
  * with p = proj[t,:] (T, 32) bf16, a_* = bf16(alpha_*[0]), b = bf16(bias) (32,),
- * perm (24, 16) fp32 (the block's perm_mat).  Outputs are fp32 (the values are
+ * perm (24, 16) (the block's perm_mat), the five parameters in param_dtype
+ * (FMHC_PARAM_F32 or FMHC_PARAM_BF16; rounded to bf16 on use either way, as
+ * the reference's .to(bf16) does).  Outputs are fp32 (the values are
  * bf16), 16-byte aligned: h_pre (T, 4), h_post (T, 4), H_merged (T, 4, 4).
  * n must be 4.
  * Replaces: src/flash_mhc/block.py:161-170 (_mhc_coeffs_triton's PyTorch ops)
  *           and the .float() casts of block.py:176-177. */
-int fmhc_k2_fwd(const uint16_t* proj, const float* alpha_pre, const float* alpha_post,
-                const float* alpha_res, const float* bias, const float* perm,
+int fmhc_k2_fwd(const uint16_t* proj, const void* alpha_pre, const void* alpha_post,
+                const void* alpha_res, const void* bias, const void* perm, int param_dtype,
                 float* h_pre, float* h_post, float* H_merged, int64_t T, int64_t n, void* stream);
 /* K2 backward: autograd of the chain above with the rounding points of
  * PyTorch's GPU kernels (the incoming fp32 gradients are rounded to bf16 first,
@@ -95,38 +112,42 @@ int fmhc_k2_fwd(const uint16_t* proj, const float* alpha_pre, const float* alpha
  * round their intermediate products to bf16 as the bf16 GPU kernels do:
  * rb(rb(g rb(1 - y)) y) and rb(gy - y sum(gy)), gy = rb(g y)).  grad_h_pre / grad_h_post / grad_H_merged may be NULL
  * (zero).  Writes grad_proj (T, 32) bf16 and the parameter gradients
- * grad_alpha_pre, grad_alpha_post, grad_alpha_res (one fp32 each) and
- * grad_bias (32 fp32): sums over tokens, accumulated in fp32 in a fixed
- * order and rounded once to bf16.  `workspace`: at least
+ * grad_alpha_pre, grad_alpha_post, grad_alpha_res (one each) and grad_bias
+ * (32), in param_dtype: sums over tokens, accumulated in fp32 in a fixed order
+ * and rounded once to bf16.  `workspace`: at least
  * fmhc_k2_bwd_workspace_bytes(T) bytes of device memory for per-block partials.
  * Replaces: autograd through src/flash_mhc/block.py:161-170 and :176-177. */
-int fmhc_k2_bwd(const uint16_t* proj, const float* alpha_pre, const float* alpha_post,
-                const float* alpha_res, const float* bias, const float* perm,
+int fmhc_k2_bwd(const uint16_t* proj, const void* alpha_pre, const void* alpha_post,
+                const void* alpha_res, const void* bias, const void* perm, int param_dtype,
                 const float* grad_h_pre, const float* grad_h_post, const float* grad_H_merged,
-                uint16_t* grad_proj, float* grad_alpha_pre, float* grad_alpha_post,
-                float* grad_alpha_res, float* grad_bias, void* workspace, int64_t workspace_bytes,
+                uint16_t* grad_proj, void* grad_alpha_pre, void* grad_alpha_post,
+                void* grad_alpha_res, void* grad_bias, void* workspace, int64_t workspace_bytes,
                 int64_t T, int64_t n, void* stream);
 /* Workspace bytes fmhc_k2_bwd needs for T tokens.  No counterpart in the reference. */
 int64_t fmhc_k2_bwd_workspace_bytes(int64_t T);
-/* Pre-map forward: K1, K2 and K3 of the same tokens (fmhc_k1_fwd, fmhc_k2_fwd,
- * fmhc_k3_fwd in order, on `stream`).  Outputs: layer_input (T, C) bf16,
+/* Pre-map forward: K1, K2 and K3 of the same tokens (fmhc_k1_fwd_ws, fmhc_k2_fwd,
+ * fmhc_k3_fwd in order, on `stream`; `workspace` as fmhc_k1_fwd_ws for n C).  Outputs: layer_input (T, C) bf16,
  * proj (T, 32) bf16, inv_rms (T,) fp32, h_pre, h_post (T, 4) and
  * H_merged (T, 4, 4) fp32 (16-byte aligned).  x (T, n, C) bf16, W (32, n C)
- * bf16, alphas / bias / perm as fmhc_k2_fwd; n must be 4.
+ * bf16, alphas / bias / perm / param_dtype as fmhc_k2_fwd; n must be 4.
  * Replaces: src/flash_mhc/block.py:157-177 (_mhc_pre_map_triton: the K1 launch,
  *           the K2 PyTorch ops and the K3 launch). */
-int fmhc_premap_fwd(const uint16_t* x, const uint16_t* W, const float* alpha_pre,
-                    const float* alpha_post, const float* alpha_res, const float* bias,
-                    const float* perm, uint16_t* layer_input, uint16_t* proj, float* inv_rms,
-                    float* h_pre, float* h_post, float* H_merged, int64_t T, int64_t C, int64_t n,
-                    void* stream);
+int fmhc_premap_fwd(const uint16_t* x, const uint16_t* W, const void* alpha_pre,
+                    const void* alpha_post, const void* alpha_res, const void* bias,
+                    const void* perm, int param_dtype, uint16_t* layer_input, uint16_t* proj,
+                    float* inv_rms,
+                    float* h_pre, float* h_post, float* H_merged, void* workspace,
+                    int64_t workspace_bytes, int64_t T, int64_t C, int64_t n, void* stream);
+/* Workspace bytes fmhc_premap_fwd needs (fmhc_k1_fwd_workspace_bytes(T, 4 C);
+ * 0: workspace may be NULL).  No counterpart in the reference. */
+int64_t fmhc_premap_fwd_workspace_bytes(int64_t T, int64_t C);
 /* Pre-map backward: the gradients of fmhc_premap_fwd's inputs from those of
  * layer_input (T, C) bf16, h_post (T, 4) and H_merged (T, 4, 4) fp32 (the
  * latter two may be NULL: zero):
  *   grad_x = bf16(K3's h_pre[t,j] * grad_layer_input[t,c] + K1's dx)
  *            (each term rounded to bf16 first, as autograd sums them),
  *   grad_W (32, n C) bf16 as fmhc_k1_bwd, the alpha / bias gradients as
- *   fmhc_k2_bwd.
+ *   fmhc_k2_bwd (in param_dtype).
  * grad_x_in (T, n, C) bf16 may be NULL; otherwise it is a further gradient of
  * x (in a block: post-res's H_merged^T grad_out) and
  *   grad_x = bf16(grad_x_in + the bf16 value above)
@@ -135,14 +156,13 @@ int fmhc_premap_fwd(const uint16_t* x, const uint16_t* W, const float* alpha_pre
  * fmhc_premap_bwd_workspace_bytes(T, C) bytes, 16-byte aligned.
  * Replaces: autograd through src/flash_mhc/block.py:157-177 (the K3, K2 and K1
  *           backward launches, and the addition of x's gradients). */
-int fmhc_premap_bwd(const uint16_t* x, const uint16_t* W, const float* alpha_pre,
-                    const float* alpha_post, const float* alpha_res, const float* bias,
-                    const float* perm, const float* h_pre, const uint16_t* proj, const float* inv_rms,
-                    const uint16_t* grad_layer_input, const float* grad_h_post,
+int fmhc_premap_bwd(const uint16_t* x, const uint16_t* W, const void* alpha_pre,
+                    const void* alpha_post, const void* alpha_res, const void* bias,
+                    const void* perm, int param_dtype, const float* h_pre, const uint16_t* proj,
+                    const float* inv_rms, const uint16_t* grad_layer_input, const float* grad_h_post,
                     const float* grad_H_merged, const uint16_t* grad_x_in, uint16_t* grad_x,
-                    uint16_t* grad_W,
-                    float* grad_alpha_pre, float* grad_alpha_post, float* grad_alpha_res,
-                    float* grad_bias, void* workspace, int64_t workspace_bytes, int64_t T, int64_t C,
+                    uint16_t* grad_W, void* grad_alpha_pre, void* grad_alpha_post, void* grad_alpha_res,
+                    void* grad_bias, void* workspace, int64_t workspace_bytes, int64_t T, int64_t C,
                     int64_t n, void* stream);
 /* Workspace bytes fmhc_premap_bwd needs.  No counterpart in the reference. */
 int64_t fmhc_premap_bwd_workspace_bytes(int64_t T, int64_t C);

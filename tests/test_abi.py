@@ -55,6 +55,9 @@ def test_loads_and_reports_version():
     assert lib.fmhc_error_string(123) == b"unknown flash_mhc status"
 
 
+_FAKE = 4096  # a non-null address that the host-side checks never dereference
+
+
 @pytest.mark.parametrize(
     "call",
     [
@@ -68,6 +71,11 @@ def test_loads_and_reports_version():
         lambda L: L.fmhc_k1_fwd(None, None, None, None, 8, 64, 31, None),  # D_out != 32
         lambda L: L.fmhc_k1_fwd(None, None, None, None, 8, 64, 32, None),  # null pointers
         lambda L: L.fmhc_k1_bwd_dx(None, None, None, None, None, None, 8, 0, 32, None),
+        lambda L: L.fmhc_k1_fwd_ws(None, None, None, None, None, 0, 8, 64, 32, None),  # null pointers
+        # K2 parameter dtype other than FMHC_PARAM_F32 (0) / FMHC_PARAM_BF16 (1)
+        lambda L: L.fmhc_k2_fwd(*[_FAKE] * 6, 2, *[_FAKE] * 3, 8, 4, None),
+        lambda L: L.fmhc_k2_fwd(*[None] * 6, 0, *[None] * 3, 8, 4, None),  # null parameters
+        lambda L: L.fmhc_premap_fwd(*[_FAKE] * 7, -1, *[_FAKE] * 6, None, 0, 8, 16, 4, None),
     ],
 )
 def test_invalid_arguments_rejected_before_launch(call):

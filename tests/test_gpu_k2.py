@@ -191,3 +191,34 @@ def test_k2_matches_torch_gpu_chain():
                            ("grad_alpha_res", ga3, a[2].grad), ("grad_bias", gb, b.grad)):
         u = ref.double().cpu()
         assert bool(((got.double().cpu() - u).abs() <= 2.0 ** -7 * u.abs() + 1e-6).all()), name
+
+
+def test_k2_bf16_parameters_equal_fp32():
+    """Parameters stored in bf16 (a bf16 block) are read as they are, with no
+    conversion launches: outputs and gradients equal those from the same values
+    in fp32 (the kernels round every parameter to bf16 on use), and the
+    parameter gradients come back in bf16, the fp32 ones' values rounded."""
+    T = 3000
+    proj, alphas, bias, grads = _case(T, 80)
+    p32 = [t.to(BF16).float() for t in (*alphas, bias, PERM)]  # bf16-representable values
+    p16 = [t.to(BF16) for t in p32]
+    a = K.k2_fwd(*_dev([proj, *p32]))
+    b = K.k2_fwd(*_dev([proj, *p16]))
+    assert all(torch.equal(u, v) for u, v in zip(a, b))
+    ga = K.k2_bwd(*_dev([proj, *p32, *grads]))
+    gb = K.k2_bwd(*_dev([proj, *p16, *grads]))
+    assert torch.equal(ga[0], gb[0])
+    for u, v in zip(ga[1:], gb[1:]):
+        assert v.dtype == BF16 and torch.equal(u, v.float())
+    x = (torch.randn(T, 4, 256, generator=torch.Generator().manual_seed(81))).to(BF16).to(DEV)
+    W = (torch.randn(32, 1024, generator=torch.Generator().manual_seed(82)) * 0.02).to(BF16).to(DEV)
+    fa = K.premap_fwd(x, W, *_dev(p32))
+    fb = K.premap_fwd(x, W, *_dev(p16))
+    assert all(torch.equal(u, v) for u, v in zip(fa, fb))
+    li, H, hq, hp, pj, inv = fa
+    g_li = torch.randn(T, 256, generator=torch.Generator().manual_seed(83)).to(BF16).to(DEV)
+    ba = K.premap_bwd(x, W, *_dev(p32), hp, pj, inv, g_li, *_dev(grads[1:]))
+    bb = K.premap_bwd(x, W, *_dev(p16), hp, pj, inv, g_li, *_dev(grads[1:]))
+    assert torch.equal(ba[0], bb[0]) and torch.equal(ba[1], bb[1])
+    for u, v in zip(ba[2:], bb[2:]):
+        assert v.dtype == BF16 and torch.equal(u, v.float())

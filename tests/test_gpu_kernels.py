@@ -87,6 +87,43 @@ def test_k1_fwd_misaligned(T, C):
     check_rel("k1 inv_rms (misaligned x)", inv, invR, rtol=1e-5)
 
 
+@pytest.mark.parametrize("T,C", [(1, 1024), (100, 4096), (4095, 1024), (8191, 256), (8192, 1024), (3, 16384)])
+def test_k1_fwd_split_columns(T, C):
+    """Few tokens: fmhc_k1_fwd_ws splits the nC axis over workgroups and adds
+    the fp32 partials in a fixed order.  Both it and the one-pass fmhc_k1_fwd
+    meet the oracle's bound; the split result is deterministic; where no split
+    is planned (workspace size 0, always from T = 8192 on) the two entry
+    points run the same kernel."""
+    from flash_mhc import _abi
+
+    nC = 4 * C
+    x, W = _k1_inputs(T, C, seed=90 + T, stress=True)
+    xd, Wd = x.to(DEV), W.to(DEV)
+    lib = _abi.load()
+    nbytes = int(lib.fmhc_k1_fwd_workspace_bytes(T, nC))
+    assert nbytes > 0 if T <= 256 else True  # few tokens always split
+    assert nbytes == 0 if T >= 8192 else True
+    a = K.k1_fwd(xd, Wd)
+    b = K.k1_fwd(xd, Wd)
+    one = (torch.empty(T, 32, dtype=torch.bfloat16, device=DEV), torch.empty(T, device=DEV))
+    st = lib.fmhc_k1_fwd(xd.data_ptr(), Wd.data_ptr(), one[0].data_ptr(), one[1].data_ptr(), T, nC, 32,
+                         _abi.stream_of(xd))
+    assert st == 0
+    torch.cuda.synchronize()
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+    R, S, invR = O.k1_fwd(x, W)
+    for name, (out, inv) in (("split", a), ("one-pass", one)):
+        check_bf16(f"k1 proj ({name})", out, R, S, nC)
+        check_rel(f"k1 inv_rms ({name})", inv, invR, rtol=4 * nC ** 0.5 * 2.0**-24 + 4 * 2.0**-24)
+    if nbytes == 0:
+        assert torch.equal(a[0], one[0]) and torch.equal(a[1], one[1])
+    else:  # a workspace one byte short is refused before any launch
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+        st = lib.fmhc_k1_fwd_ws(xd.data_ptr(), Wd.data_ptr(), one[0].data_ptr(), one[1].data_ptr(),
+                                ws.data_ptr(), nbytes - 1, T, nC, 32, _abi.stream_of(xd))
+        assert st == 1  # FMHC_ERR_INVALID_ARGUMENT
+
+
 def test_k1_fwd_unit_weights():
     # Reference test distribution: W ~ N(0, 1).
     x, W = _k1_inputs(2048, 256, seed=5, w_scale=1.0)

@@ -66,9 +66,10 @@ def test_premap_fwd_stages(T, C):
     check_bf16("premap layer_input", li, R, S, 4)
 
 
-def test_premap_matches_three_kernels():
-    """Same outputs as K1 + K2 + K3 launched separately."""
-    T, C = 8192, 1024
+@pytest.mark.parametrize("T,C", [(8192, 1024), (300, 1024), (1, 4096)])
+def test_premap_matches_three_kernels(T, C):
+    """Same outputs as K1 + K2 + K3 launched separately (few tokens: both
+    take K1's column-split kernel)."""
     x = randn((T, 4, C), 3).to(DEV)
     W = randn((32, 4 * C), 4, 0.02).to(DEV)
     p = [t.to(DEV) for t in (*_params(5), PERM)]
@@ -214,7 +215,7 @@ def test_premap_bwd_rejects_overlapping_incoming_grad():
     shifted = torch.empty(x.numel() + 8, dtype=BF16, device=DEV)
     gx = shifted[8:].view(T, 4, C)
     for g_in in (gx, shifted[:-8]):  # the same buffer, and one shifted by 16 bytes
-        st = lib.fmhc_premap_bwd(P(x), P(W), *[P(t) for t in p], P(hp), P(proj), P(inv), P(g_li), None, None,
+        st = lib.fmhc_premap_bwd(P(x), P(W), *[P(t) for t in p], 0, P(hp), P(proj), P(inv), P(g_li), None, None,
                                  P(g_in), P(gx), P(gW), *[P(t) for t in ga], P(gb), P(ws), nbytes, T, C, 4,
                                  _abi.stream_of(x))
         assert st == 1  # FMHC_ERR_INVALID_ARGUMENT
