@@ -11,8 +11,10 @@ measured step time (K steps of bare launches between two events).  Per-kernel
 durations come from a second pass of K steps with an event pair around each
 launch; ``roofline`` describes the dominant kernel (largest average duration),
 timed with those HIP events on the stream it runs on.  Extra fields report
-K1's full backward (fused grad_W vs the reference's matmul) and a whole
-MHCLiteBlock forward + backward with the fused path vs the reference's rules.
+K1's full backward (fused grad_W vs the reference's matmul), a whole
+MHCLiteBlock forward + backward with the fused path vs the reference's rules,
+and the eval-mode forward latency of the inference shapes (C=4096,
+T = 1, 64, 257, 65537; eager and HIP-graph replay).
 ``cpu_baseline`` times the reference's PyTorch formulation of the same six ops
 (fp32 autograd, restated in oracle/) on the host's cores, on a bounded token
 sample, reported with the same bytes model.
@@ -195,6 +197,68 @@ def block_step(T: int, C: int, iters: int = 10) -> dict:
             else:
                 os.environ[f] = v
     out["workload"] = f"MHCLiteBlock(4, {C}, Linear({C}, {C})) forward + backward, T={T}, bf16"
+    return out
+
+
+def eval_latency(C: int = 4096, tokens=(1, 64, 257, 65537)) -> dict:
+    """Eval-mode forward latency of MHCLiteBlock(4, C, Linear(C, C)) (bf16,
+    random weights), the inference / ragged-tail shapes: eager and replayed from
+    a captured HIP graph, for the fused path and for the reference's rules
+    (K2 as PyTorch ops, separate pre-map ops; graph replay)."""
+    import flash_mhc
+
+    torch.manual_seed(0)
+    blk = flash_mhc.MHCLiteBlock(4, C, torch.nn.Linear(C, C, bias=False)).cuda().bfloat16().eval()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def timed(fn, n):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return round(e0.elapsed_time(e1) / n * 1e3, 1)
+
+    def graphed(x):
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(2):
+                blk(x)
+        torch.cuda.current_stream().wait_stream(s)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            blk(x)
+        return g
+
+    flags = ("FLASH_MHC_FUSED_K2", "FLASH_MHC_FUSED_PREMAP")
+    saved = {f: os.environ.get(f) for f in flags}
+    out = {}
+    try:
+        with torch.no_grad():
+            for T in tokens:
+                n = 50 if T < 4096 else 10
+                x = torch.randn(T, 4, C, device="cuda", dtype=torch.bfloat16)
+                row = {}
+                for name, val in (("fused", "1"), ("reference_rules", "0")):
+                    for f in flags:
+                        os.environ[f] = val
+                    if name == "fused":
+                        row["eager_us"] = timed(lambda: blk(x), n)
+                    g = graphed(x)
+                    row[("graph_us" if name == "fused" else "reference_rules_graph_us")] = timed(g.replay, n)
+                    del g
+                out[f"T={T}"] = row
+    finally:
+        for f, v in saved.items():
+            if v is None:
+                os.environ.pop(f, None)
+            else:
+                os.environ[f] = v
+    out["workload"] = f"MHCLiteBlock(4, {C}, Linear({C}, {C})) eval forward, bf16"
     return out
 
 
@@ -396,6 +460,7 @@ def main() -> None:
 
     k1_full_bwd = None if args.no_extras else k1_backward_paths(inp, T, C)
     blk = None if args.no_extras else block_step(T, C)
+    lat = None if args.no_extras else eval_latency()
     ceil = stream_ceilings()
     split = read_write_split(T, n, C, D)
     for name in KERNELS:
@@ -427,6 +492,7 @@ def main() -> None:
         "ceilings_GBps": ceil,
         "k1_backward_with_grad_W": k1_full_bwd,
         "block_step": blk,
+        "eval_latency": lat,
         "kernels": per,
         "roofline": {
             "kernel": dom,
