@@ -28,20 +28,21 @@ namespace fmhc {
 namespace {
 
 constexpr int kK2Threads = 256;
+constexpr int64_t kK2SmallT = 4096;  // forward: 32 lanes per token up to this many tokens
 
 template <bool VEC>
 __global__ __launch_bounds__(kK2Threads) void k2_fwd_kernel(
     const uint16_t* __restrict__ proj, const K2Params P, float* __restrict__ h_pre,
     float* __restrict__ h_post, float* __restrict__ H, int64_t T) {
 #pragma clang fp contract(off)
-  __shared__ f32x4 sperm[kNF * 4];
-  stage_perm<kK2Threads>(P, sperm);
+  __shared__ K2Smem sm;
+  stage_params<kK2Threads>(P, sm);
   const int64_t t = static_cast<int64_t>(blockIdx.x) * kK2Threads + threadIdx.x;
   if (t >= T) return;
   float p[kDk];
   load_proj<VEC>(proj + t * kDk, p);
   float ap, apo, ar, b[kDk];
-  load_params(P, ap, apo, ar, b);
+  load_params(sm, ap, apo, ar, b);
   K2Fwd f;
   k2_chain(p, ap, apo, ar, b, f);
   f32x4 hp = {f.hp[0], f.hp[1], f.hp[2], f.hp[3]};
@@ -49,9 +50,48 @@ __global__ __launch_bounds__(kK2Threads) void k2_fwd_kernel(
   reinterpret_cast<f32x4*>(h_pre)[t] = hp;
   reinterpret_cast<f32x4*>(h_post)[t] = hq;
   f32x4 Hm[kN];
-  k2_h_merged(f, sperm, Hm);
+  k2_h_merged(f, sm.perm, Hm);
 #pragma unroll
   for (int i = 0; i < kN; ++i) reinterpret_cast<f32x4*>(H)[t * kN + i] = Hm[i];
+}
+
+// Few tokens: 32 lanes per token.  Lane q computes logit q (q < 4: h_pre,
+// q < 8: h_post, else a softmax term), then lanes 0-15 one H_merged entry
+// each.  Every sum keeps k2_chain's / k2_h_merged's order (the softmax
+// denominator and each H_res entry are added sequentially over m), so the
+// results are bit-identical to k2_fwd_kernel's.
+__global__ __launch_bounds__(kK2Threads) void k2_fwd_small(const uint16_t* __restrict__ proj, const K2Params P,
+                                                          float* __restrict__ h_pre, float* __restrict__ h_post,
+                                                          float* __restrict__ H, int64_t T) {
+#pragma clang fp contract(off)
+  __shared__ K2Smem sm;
+  stage_params<kK2Threads>(P, sm);
+  const int q = threadIdx.x & 31;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * (kK2Threads / 32) + (threadIdx.x >> 5);
+  if (t >= T) return;  // a whole 32-lane group leaves together
+  const float alpha = q < kN ? sm.sc[0] : (q < 2 * kN ? sm.sc[1] : sm.sc[2]);
+  const float z = rb(rb(alpha * bf16_to_f32(proj[t * kDk + q])) + sm.sc[3 + q]);
+  const float y = q < 2 * kN ? rb(sigmoid_f32(z)) : 0.f;  // h_pre (q < 4), sigmoid of the post logit
+  const float hq = rb(2.f * y);                             // h_post for 4 <= q < 8
+  float mx = q >= 2 * kN ? z : -INFINITY;
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 32));
+  const float e = q >= 2 * kN ? expf(z - mx) : 0.f;
+  float sum = 0.f;
+#pragma unroll
+  for (int m = 0; m < kNF; ++m) sum = sum + __shfl(e, 2 * kN + m, 32);
+  const float a = rb(e / sum);
+  const float* pf = reinterpret_cast<const float*>(sm.perm);
+  float acc = 0.f;
+#pragma unroll
+  for (int m = 0; m < kNF; ++m) acc = acc + __shfl(a, 2 * kN + m, 32) * pf[m * kN * kN + (q & 15)];
+  const float hp_j = __shfl(y, q & 3, 32);
+  const float hq_i = __shfl(hq, kN + ((q & 15) >> 2), 32);
+  if (q < kN * kN) H[t * kN * kN + q] = rb(rb(acc) - rb(hq_i * hp_j));
+  if (q < kN)
+    h_pre[t * kN + q] = y;
+  else if (q < 2 * kN)
+    h_post[t * kN + (q - kN)] = hq;
 }
 
 // Backward of one token (autograd's rounding points on the GPU; gradients of
@@ -67,8 +107,8 @@ __global__ __launch_bounds__(kK2Threads) void k2_bwd_kernel(
     const float* __restrict__ g_H, uint16_t* __restrict__ grad_proj,
     float* __restrict__ partial, int64_t T) {
 #pragma clang fp contract(off)
-  __shared__ f32x4 sperm[kNF * 4];
-  stage_perm<kK2Threads>(P, sperm);
+  __shared__ K2Smem sm;
+  stage_params<kK2Threads>(P, sm);
   const int64_t t = static_cast<int64_t>(blockIdx.x) * kK2Threads + threadIdx.x;
   float par[kNPar];
 #pragma unroll
@@ -78,7 +118,7 @@ __global__ __launch_bounds__(kK2Threads) void k2_bwd_kernel(
     float p[kDk];
     load_proj<VEC>(proj + t * kDk, p);
     float ap, apo, ar, b[kDk];
-    load_params(P, ap, apo, ar, b);
+    load_params(sm, ap, apo, ar, b);
     K2Fwd f;
     k2_chain(p, ap, apo, ar, b, f);
 
@@ -110,7 +150,7 @@ __global__ __launch_bounds__(kK2Threads) void k2_bwd_kernel(
       float acc = 0.f;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const f32x4 pm = sperm[m * 4 + q];
+        const f32x4 pm = sm.perm[m * 4 + q];
 #pragma unroll
         for (int e = 0; e < 4; ++e) acc = acc + gH[4 * q + e] * pm[e];
       }
@@ -212,6 +252,11 @@ extern "C" int fmhc_k2_fwd(const uint16_t* proj, const void* alpha_pre, const vo
   if (!proj || !h_pre || !h_post || !H_merged) return FMHC_ERR_INVALID_ARGUMENT;
   if (!aligned16(h_pre) || !aligned16(h_post) || !aligned16(H_merged)) return FMHC_ERR_INVALID_ARGUMENT;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (T <= kK2SmallT) {
+    k2_fwd_small<<<dim3(static_cast<unsigned>((T + 7) / 8)), kK2Threads, 0, s>>>(proj, P, h_pre, h_post,
+                                                                                H_merged, T);
+    return launch_status();
+  }
   const dim3 grid(static_cast<unsigned>(k2_blocks(T)));
   if (aligned16(proj))
     k2_fwd_kernel<true><<<grid, kK2Threads, 0, s>>>(proj, P, h_pre, h_post, H_merged, T);

@@ -30,23 +30,32 @@ __device__ __forceinline__ float ld_param(const void* p, int i, bool bf16) {
   return bf16 ? bf16_to_f32(static_cast<const uint16_t*>(p)[i]) : static_cast<const float*>(p)[i];
 }
 
-// perm (24 x 16) rounded to bf16 (the reference multiplies by perm_mat.to(bf16)),
-// staged in LDS once per block; every lane then reads the same rows (broadcast).
+// All K2 parameters rounded to bf16 (the values the reference's ops see after
+// .to(bf16)), staged in LDS once per block; every lane then reads the same
+// addresses (broadcast).  perm (24 x 16) as 96 f32x4, then alpha_pre,
+// alpha_post, alpha_res and bias[32].
+struct K2Smem {
+  f32x4 perm[kNF * 4];
+  float sc[3 + kDk];
+};
+
 template <int THREADS>
-__device__ __forceinline__ void stage_perm(const K2Params& P, f32x4 sperm[kNF * 4]) {
-  float* s = reinterpret_cast<float*>(sperm);
-  for (int i = threadIdx.x; i < kNF * kN * kN; i += THREADS) s[i] = rb(ld_param(P.perm, i, P.bf16));
+__device__ __forceinline__ void stage_params(const K2Params& P, K2Smem& sm) {
+  float* pf = reinterpret_cast<float*>(sm.perm);
+  for (int i = threadIdx.x; i < kNF * kN * kN; i += THREADS) pf[i] = rb(ld_param(P.perm, i, P.bf16));
+  for (int i = threadIdx.x; i < 3 + kDk; i += THREADS) {
+    const void* src = i == 0 ? P.alpha_pre : (i == 1 ? P.alpha_post : (i == 2 ? P.alpha_res : P.bias));
+    sm.sc[i] = rb(ld_param(src, i < 3 ? 0 : i - 3, P.bf16));
+  }
   __syncthreads();
 }
 
-// bf16(alpha_pre), bf16(alpha_post), bf16(alpha_res) and bf16(bias), the
-// values the reference's ops see after .to(bf16).
-__device__ __forceinline__ void load_params(const K2Params& P, float& ap, float& apo, float& ar, float b[kDk]) {
-  ap = rb(ld_param(P.alpha_pre, 0, P.bf16));
-  apo = rb(ld_param(P.alpha_post, 0, P.bf16));
-  ar = rb(ld_param(P.alpha_res, 0, P.bf16));
+__device__ __forceinline__ void load_params(const K2Smem& sm, float& ap, float& apo, float& ar, float b[kDk]) {
+  ap = sm.sc[0];
+  apo = sm.sc[1];
+  ar = sm.sc[2];
 #pragma unroll
-  for (int k = 0; k < kDk; ++k) b[k] = rb(ld_param(P.bias, k, P.bf16));
+  for (int k = 0; k < kDk; ++k) b[k] = sm.sc[3 + k];
 }
 
 __device__ __forceinline__ float sigmoid_f32(float z) {

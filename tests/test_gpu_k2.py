@@ -222,3 +222,15 @@ def test_k2_bf16_parameters_equal_fp32():
     assert torch.equal(ba[0], bb[0]) and torch.equal(ba[1], bb[1])
     for u, v in zip(ba[2:], bb[2:]):
         assert v.dtype == BF16 and torch.equal(u, v.float())
+
+
+def test_k2_fwd_small_and_large_kernels_agree():
+    """Up to 4096 tokens the forward gives each token 32 lanes (one per logit),
+    beyond that one thread; both keep the same operation order, so the first
+    4096 tokens of a 4097-token call equal a 4096-token call bit for bit."""
+    proj, alphas, bias, _ = _case(4097, 90)
+    prm = _dev([*alphas, bias, PERM])
+    big = K.k2_fwd(proj.to(DEV), *prm)
+    small = K.k2_fwd(proj[:4096].to(DEV), *prm)
+    for u, v in zip(small, big):
+        assert torch.equal(u, v[:4096])
