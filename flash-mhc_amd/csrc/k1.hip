@@ -17,13 +17,14 @@
 // agree), each lane's eight contraction values are eight consecutive bf16 in
 // memory: one 16-byte load.
 #include "fmhc_common.h"
+#include "k1_premap.h"
 
 namespace fmhc {
 
 namespace {
 
 constexpr int kDout = 32;
-constexpr float kEps = 1e-6f;
+constexpr float kEps = kRmsEps;
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
@@ -908,6 +909,19 @@ extern "C" int fmhc_k1_bwd(const uint16_t* x_flat, const uint16_t* W, const uint
 }
 
 namespace fmhc {
+
+int k1_fwd_partials(const uint16_t* x_flat, const uint16_t* W, void* ws, int64_t ws_bytes, int64_t T,
+                    int64_t nC, hipStream_t s) {
+  if (!(nC % 8 == 0 && nC <= (int64_t{1} << 24) && aligned16(x_flat) && aligned16(W))) return 0;
+  const K1FwdSplit p = k1_fwd_split(T, nC);
+  if (p.S < 2) return 0;
+  if (!ws || ws_bytes < p.bytes || !aligned16(ws)) return -FMHC_ERR_INVALID_ARGUMENT;
+  const dim3 grid(blocks_for(T, 16 * kSplitR), p.S);
+  k1_fwd_mfma<kSplitR, kFwdSplit, true><<<grid, kWave * kFwdSplit, 0, s>>>(
+      x_flat, W, nullptr, nullptr, static_cast<float*>(ws), T, static_cast<int>(nC), p.cps);
+  const int st = launch_status();
+  return st == FMHC_OK ? p.S : -st;
+}
 
 // K1 backward of the pre-map region (premap.hip): grad_W as fmhc_k1_bwd and
 // grad_x = bf16(bf16(h_pre[t, j] go3[t, c]) + bf16(dx)).  On the MFMA path the

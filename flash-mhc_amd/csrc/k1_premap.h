@@ -1,4 +1,4 @@
-// K1 backward entry used by the pre-map backward (premap.hip); defined in k1.hip.
+// K1 pieces used by the pre-map region (premap.hip); defined in k1.hip.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -6,6 +6,17 @@
 #include <cstdint>
 
 namespace fmhc {
+
+constexpr float kRmsEps = 1e-6f;  // K1's RMSNorm epsilon (kernels.py:279 of the reference)
+
+// The first kernel of K1's column-split forward alone: when T tokens take that
+// path (few tokens, MFMA-eligible pointers) it writes the fp32 partial sums to
+// `ws` as part[t][33][S4] (32 projections, then the sum of squares; S4 = S
+// rounded up to 4) and returns the number of splits S >= 2; it returns 0 when
+// the tokens do not take that path and -status on an error.  The second stage
+// (k1_fwd_finish in k1.hip) adds the S partials of each value in split order.
+int k1_fwd_partials(const uint16_t* x_flat, const uint16_t* W, void* ws, int64_t ws_bytes, int64_t T,
+                    int64_t nC, hipStream_t s);
 
 // True when k1_bwd_premap computes the K3 term of grad_x itself (MFMA path);
 // otherwise grad_x must hold it on entry.  gi: the incoming gradient or null.

@@ -69,29 +69,7 @@ __global__ __launch_bounds__(kK2Threads) void k2_fwd_small(const uint16_t* __res
   const int q = threadIdx.x & 31;
   const int64_t t = static_cast<int64_t>(blockIdx.x) * (kK2Threads / 32) + (threadIdx.x >> 5);
   if (t >= T) return;  // a whole 32-lane group leaves together
-  const float alpha = q < kN ? sm.sc[0] : (q < 2 * kN ? sm.sc[1] : sm.sc[2]);
-  const float z = rb(rb(alpha * bf16_to_f32(proj[t * kDk + q])) + sm.sc[3 + q]);
-  const float y = q < 2 * kN ? rb(sigmoid_f32(z)) : 0.f;  // h_pre (q < 4), sigmoid of the post logit
-  const float hq = rb(2.f * y);                             // h_post for 4 <= q < 8
-  float mx = q >= 2 * kN ? z : -INFINITY;
-#pragma unroll
-  for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 32));
-  const float e = q >= 2 * kN ? expf(z - mx) : 0.f;
-  float sum = 0.f;
-#pragma unroll
-  for (int m = 0; m < kNF; ++m) sum = sum + __shfl(e, 2 * kN + m, 32);
-  const float a = rb(e / sum);
-  const float* pf = reinterpret_cast<const float*>(sm.perm);
-  float acc = 0.f;
-#pragma unroll
-  for (int m = 0; m < kNF; ++m) acc = acc + __shfl(a, 2 * kN + m, 32) * pf[m * kN * kN + (q & 15)];
-  const float hp_j = __shfl(y, q & 3, 32);
-  const float hq_i = __shfl(hq, kN + ((q & 15) >> 2), 32);
-  if (q < kN * kN) H[t * kN * kN + q] = rb(rb(acc) - rb(hq_i * hp_j));
-  if (q < kN)
-    h_pre[t * kN + q] = y;
-  else if (q < 2 * kN)
-    h_post[t * kN + (q - kN)] = hq;
+  k2_token32(sm, bf16_to_f32(proj[t * kDk + q]), q, t, h_pre, h_post, H);
 }
 
 // Backward of one token (autograd's rounding points on the GPU; gradients of

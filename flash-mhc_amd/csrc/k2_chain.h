@@ -133,4 +133,38 @@ __device__ __forceinline__ void k2_h_merged(const K2Fwd& f, const f32x4 sperm[kN
     for (int j = 0; j < kN; ++j) H[i][j] = rb(rb(acc[i * kN + j]) - rb(f.hq[i] * f.hp[j]));
 }
 
+// K2 forward of token t with 32 lanes (lane q of a 32-lane group, p = the
+// token's projection q as a bf16 value): lane q computes logit q (q < 4:
+// h_pre, q < 8: h_post, else a softmax term), then lanes 0-15 one H_merged
+// entry each.  Every sum keeps k2_chain's / k2_h_merged's order (the softmax
+// denominator and each H_res entry are added sequentially over m), so the
+// results are bit-identical to the one-thread chain's.
+__device__ __forceinline__ void k2_token32(const K2Smem& sm, float p, int q, int64_t t, float* __restrict__ h_pre,
+                                           float* __restrict__ h_post, float* __restrict__ H) {
+#pragma clang fp contract(off)
+  const float alpha = q < kN ? sm.sc[0] : (q < 2 * kN ? sm.sc[1] : sm.sc[2]);
+  const float z = rb(rb(alpha * p) + sm.sc[3 + q]);
+  const float y = q < 2 * kN ? rb(sigmoid_f32(z)) : 0.f;  // h_pre (q < 4), sigmoid of the post logit
+  const float hq = rb(2.f * y);                             // h_post for 4 <= q < 8
+  float mx = q >= 2 * kN ? z : -INFINITY;
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 32));
+  const float e = q >= 2 * kN ? expf(z - mx) : 0.f;
+  float sum = 0.f;
+#pragma unroll
+  for (int m = 0; m < kNF; ++m) sum = sum + __shfl(e, 2 * kN + m, 32);
+  const float a = rb(e / sum);
+  const float* pf = reinterpret_cast<const float*>(sm.perm);
+  float acc = 0.f;
+#pragma unroll
+  for (int m = 0; m < kNF; ++m) acc = acc + __shfl(a, 2 * kN + m, 32) * pf[m * kN * kN + (q & 15)];
+  const float hp_j = __shfl(y, q & 3, 32);
+  const float hq_i = __shfl(hq, kN + ((q & 15) >> 2), 32);
+  if (q < kN * kN) H[t * kN * kN + q] = rb(rb(acc) - rb(hq_i * hp_j));
+  if (q < kN)
+    h_pre[t * kN + q] = y;
+  else if (q < 2 * kN)
+    h_post[t * kN + (q - kN)] = hq;
+}
+
 }  // namespace fmhc

@@ -11,8 +11,9 @@
 // (bf16(grad_x_in + pre-map gradient), autograd's sum), which replaces
 // autograd's separate accumulation pass (1.5 x T x nC x 2 bytes).
 //
-// Forward: K1 -> K2 -> K3, the three kernels of k1.hip, k2.hip, k3.hip (K1
-// split over the columns for few tokens, with the caller's workspace).  A
+// Forward: K1 -> K2 -> K3, the three kernels of k1.hip, k2.hip, k3.hip.  For
+// few tokens K1 is split over the columns (partial sums in the caller's
+// workspace), and its second stage runs inside the K2 kernel (k1_finish_k2).  A
 // one-pass variant that kept each token tile of x in LDS between K1 and K3
 // (saving K3's read of x) was built and measured slower on gfx950 at
 // C <= 1024: with tiles of 8-16 tokens every tile re-reads the whole of W
@@ -25,14 +26,54 @@
 #include "flash_mhc_hip.h"
 #include "fmhc_common.h"
 #include "k1_premap.h"
+#include "k2_chain.h"
 
 namespace {
+
+using namespace fmhc;
 
 constexpr int64_t kAlign = 256;
 int64_t round_up(int64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 // Checked before the first launch, so that a bad dtype leaves no partial outputs.
 bool param_dtype_ok(int d) { return d == FMHC_PARAM_F32 || d == FMHC_PARAM_BF16; }
+
+constexpr int kFinishThreads = 256;  // 8 tokens of 32 lanes
+
+// Few tokens: K1's second stage and K2 in one kernel, 32 lanes per token.
+// Lane q adds the S partials of projection q and those of the sum of squares
+// in split order (as k1_fwd_finish does), stores proj[t, q] =
+// bf16(sum * inv_rms) and inv_rms, then runs K2 on that bf16 value
+// (k2_token32): the same values as K1's finish kernel followed by K2.
+__global__ __launch_bounds__(kFinishThreads) void k1_finish_k2(
+    const float* __restrict__ part, int S, int nC, const K2Params P, uint16_t* __restrict__ proj,
+    float* __restrict__ inv_rms, float* __restrict__ h_pre, float* __restrict__ h_post, float* __restrict__ H,
+    int64_t T) {
+  __shared__ K2Smem sm;
+  stage_params<kFinishThreads>(P, sm);
+  const int q = threadIdx.x & 31;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * (kFinishThreads / 32) + (threadIdx.x >> 5);
+  if (t >= T) return;  // a whole 32-lane group leaves together
+  const int s4 = (S + 3) & ~3;
+  auto add = [&](int v) {
+    const f32x4* p = reinterpret_cast<const f32x4*>(part + (t * (kDk + 1) + v) * s4);
+    float acc = 0.f;
+    for (int i = 0; i < s4 / 4; ++i) {
+      const f32x4 w = p[i];
+      acc += w[0];  // 4 i < S always
+      if (4 * i + 1 < S) acc += w[1];
+      if (4 * i + 2 < S) acc += w[2];
+      if (4 * i + 3 < S) acc += w[3];
+    }
+    return acc;
+  };
+  const float v = add(q);
+  const float inv = rsqrtf(add(kDk) / static_cast<float>(nC) + kRmsEps);
+  const uint16_t pj = f32_to_bf16(v * inv);
+  proj[t * kDk + q] = pj;
+  if (q == 0) inv_rms[t] = inv;
+  k2_token32(sm, bf16_to_f32(pj), q, t, h_pre, h_post, H);
+}
 
 struct PremapWs {
   int64_t gh, gp, k2, k1, total;  // byte offsets / sizes
@@ -66,10 +107,23 @@ extern "C" int fmhc_premap_fwd(const uint16_t* x, const uint16_t* W, const void*
   if (!x || !W || !alpha_pre || !alpha_post || !alpha_res || !bias || !perm || !layer_input || !proj ||
       !inv_rms || !h_pre || !h_post || !H_merged)
     return FMHC_ERR_INVALID_ARGUMENT;
-  int st = fmhc_k1_fwd_ws(x, W, proj, inv_rms, workspace, workspace_bytes, T, n * C, 32, stream);
-  if (st == FMHC_OK)
-    st = fmhc_k2_fwd(proj, alpha_pre, alpha_post, alpha_res, bias, perm, param_dtype, h_pre, h_post, H_merged, T,
-                     n, stream);
+  if (!aligned16(h_pre) || !aligned16(h_post) || !aligned16(H_merged)) return FMHC_ERR_INVALID_ARGUMENT;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int S = fmhc::k1_fwd_partials(x, W, workspace, workspace_bytes, T, n * C, s);
+  if (S < 0) return -S;
+  int st = FMHC_OK;
+  if (S >= 2) {
+    const fmhc::K2Params P{alpha_pre, alpha_post, alpha_res, bias, perm, param_dtype == FMHC_PARAM_BF16};
+    k1_finish_k2<<<dim3(static_cast<unsigned>((T + 7) / 8)), kFinishThreads, 0, s>>>(
+        static_cast<const float*>(workspace), S, static_cast<int>(n * C), P, proj, inv_rms, h_pre, h_post,
+        H_merged, T);
+    st = fmhc::launch_status();
+  } else {
+    st = fmhc_k1_fwd_ws(x, W, proj, inv_rms, workspace, workspace_bytes, T, n * C, 32, stream);
+    if (st == FMHC_OK)
+      st = fmhc_k2_fwd(proj, alpha_pre, alpha_post, alpha_res, bias, perm, param_dtype, h_pre, h_post, H_merged,
+                       T, n, stream);
+  }
   if (st == FMHC_OK) st = fmhc_k3_fwd(x, h_pre, layer_input, T, C, n, stream);
   return st;
 }
