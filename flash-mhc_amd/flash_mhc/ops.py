@@ -165,9 +165,11 @@ def x_sink_like(x_streams: torch.Tensor) -> torch.Tensor:
 
 
 def _x_sink(x_streams: torch.Tensor) -> torch.Tensor:
-    """x_sink_like with its one element set to zero (a one-element fill, not T n C)."""
+    """x_sink_like with its one element set to zero (a one-element fill, not
+    T n C); an empty batch's sink has no storage to fill."""
     sink = x_sink_like(x_streams)
-    sink.as_strided((1,), (1,)).zero_()
+    if sink.numel() > 0:
+        sink.as_strided((1,), (1,)).zero_()
     return sink
 
 

@@ -60,7 +60,8 @@ def _pre_map(x, W, ap, apo, ar, b, perm):
     proj, inv = _k1(x.reshape(T, n * C), W.to(x.dtype))
     h_pre, h_post, H = _k2(proj, ap, apo, ar, b, perm)
     sink = x.new_empty_strided(tuple(x.shape), (0,) * x.dim())  # mhc_pre_map's x_sink
-    sink.as_strided((1,), (1,)).zero_()
+    if sink.numel() > 0:
+        sink.as_strided((1,), (1,)).zero_()
     return _k3(x, h_pre), H, h_post, h_pre, proj, inv, sink
 
 

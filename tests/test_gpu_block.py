@@ -324,3 +324,21 @@ def test_graph_capture_eval_forward(T):
             eager = blk(x)  # eager work between replays
             torch.cuda.synchronize()
             assert torch.equal(eager, ref)
+
+
+@pytest.mark.parametrize("ckpt", [False, True])
+def test_empty_batch_forward_backward(ckpt):
+    """T = 0 through the fused block, training and eval: empty outputs, an empty
+    x gradient and zero parameter gradients."""
+    torch.manual_seed(0)
+    C = 256
+    blk = flash_mhc.MHCLiteBlock(4, C, torch.nn.Linear(C, C, bias=False), activation_checkpointing=ckpt).to(DEV, BF16)
+    x = torch.empty((0, 4, C), device=DEV, dtype=BF16, requires_grad=True)
+    out = blk(x)
+    assert out.shape == (0, 4, C)
+    out.float().sum().backward()
+    assert x.grad.shape == (0, 4, C)
+    for name, p in blk.named_parameters():
+        assert p.grad is None or float(p.grad.float().abs().sum()) == 0.0, name
+    with torch.no_grad():
+        assert blk.eval()(x.detach()).shape == (0, 4, C)

@@ -393,3 +393,14 @@ def test_xgrad_sink_equals_autograd_sum_on_cpu(cpu_kernels, monkeypatch, ckpt):
     assert torch.equal(gx1, gx0)
     for n in gp0:
         assert torch.equal(gp1[n], gp0[n]), n
+
+
+def test_pre_map_empty_batch_on_cpu(cpu_kernels):
+    """T = 0 through the block's fused path: empty outputs and gradients (the
+    sink of an empty batch has no storage to fill)."""
+    blk = _block(C=32)
+    x = rnd((0, 4, 32), 48).requires_grad_(True)
+    out = blk._forward_triton(x)
+    assert out.shape == (0, 4, 32)
+    out.float().sum().backward()
+    assert x.grad.shape == (0, 4, 32)
