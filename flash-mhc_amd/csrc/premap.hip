@@ -104,8 +104,8 @@ extern "C" int fmhc_premap_fwd(const uint16_t* x, const uint16_t* W, const void*
                                void* stream) {
   if (T < 0 || C <= 0 || n != 4 || !param_dtype_ok(param_dtype)) return FMHC_ERR_INVALID_ARGUMENT;
   if (T == 0) return FMHC_OK;
-  if (!x || !W || !alpha_pre || !alpha_post || !alpha_res || !bias || !perm || !layer_input || !proj ||
-      !inv_rms || !h_pre || !h_post || !H_merged)
+  if (!x || !W || !alpha_pre || !alpha_post || !alpha_res || !bias || !perm || !proj || !inv_rms || !h_pre ||
+      !h_post || !H_merged)
     return FMHC_ERR_INVALID_ARGUMENT;
   if (!aligned16(h_pre) || !aligned16(h_post) || !aligned16(H_merged)) return FMHC_ERR_INVALID_ARGUMENT;
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -124,7 +124,7 @@ extern "C" int fmhc_premap_fwd(const uint16_t* x, const uint16_t* W, const void*
       st = fmhc_k2_fwd(proj, alpha_pre, alpha_post, alpha_res, bias, perm, param_dtype, h_pre, h_post, H_merged,
                        T, n, stream);
   }
-  if (st == FMHC_OK) st = fmhc_k3_fwd(x, h_pre, layer_input, T, C, n, stream);
+  if (st == FMHC_OK && layer_input) st = fmhc_k3_fwd(x, h_pre, layer_input, T, C, n, stream);
   return st;
 }
 

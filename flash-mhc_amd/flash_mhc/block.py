@@ -154,9 +154,17 @@ class MHCLiteBlock(nn.Module):
         )
 
     def _forward_pytorch(self, x_streams: torch.Tensor, **kwargs) -> torch.Tensor:
-        return self._run(
-            x_streams, self._mhc_pre_map_pytorch, self._mhc_post_res_pytorch, nullcontext(), kwargs
-        )
+        def pre_map(x, use_ckpt):
+            return self._pre_map_region(self._mhc_pre_map_pytorch, x, use_ckpt)
+
+        return self._run(x_streams, pre_map, self._mhc_post_res_pytorch, nullcontext(), kwargs)
+
+    @staticmethod
+    def _pre_map_region(fn, x_streams: torch.Tensor, use_ckpt: bool):
+        """fn(x_streams), recomputed in the backward under activation checkpointing."""
+        if use_ckpt:
+            return _checkpoint(fn, x_streams, use_reentrant=False)
+        return fn(x_streams)
 
     # -- fused HIP path (block.py:150-219) ------------------------------------
 
@@ -178,17 +186,28 @@ class MHCLiteBlock(nn.Module):
         """K1 + K2 as the reference's PyTorch ops: bf16 (h_pre, h_post, H_merged)."""
         return self._coefficients(self._project_triton(x_streams), x_streams.dtype)
 
-    def _mhc_pre_map_triton(self, x_streams: torch.Tensor):
+    def _mhc_pre_map_triton(self, x_streams: torch.Tensor, use_ckpt: bool = False):
         if _ops.fused_premap_enabled():
-            # K1 + K2 + K3 in one op.  With x_sink, post-res's x-gradient is
-            # added in K1's backward store rather than by autograd.
-            layer_input, H_merged, h_post, _h_pre, _proj, _inv_rms, x_sink = torch.ops.flash_mhc.mhc_pre_map(
+            # K1 + K2 as one op, K3 as a second one whose backward hands the
+            # layer input's gradient to the first (the fused pre-map backward).
+            # Checkpointing recomputes K3 alone: the layer input is the one
+            # large tensor of the region.  With x_sink, post-res's x-gradient
+            # is added in K1's backward store rather than by autograd.
+            H_merged, h_post, h_pre, _proj, _inv_rms, x_sink, li_sink = torch.ops.flash_mhc.mhc_pre_map_coeffs(
                 x_streams, self._projection_weight(x_streams.dtype), self.alpha_pre,
                 self.alpha_post, self.alpha_res, self.W_all.bias, self.perm_mat,
             )
+            mix = torch.ops.flash_mhc.mhc_pre_map_mix
+            if use_ckpt:
+                layer_input = _checkpoint(mix, x_streams, h_pre, li_sink, use_reentrant=False)
+            else:
+                layer_input = mix(x_streams, h_pre, li_sink)
             if _ops.fused_xgrad_enabled():
                 return layer_input, H_merged, h_post, x_sink
             return layer_input, H_merged, h_post
+        return self._pre_map_region(self._mhc_pre_map_triton_ops, x_streams, use_ckpt)
+
+    def _mhc_pre_map_triton_ops(self, x_streams: torch.Tensor):
         if _ops.fused_k2_enabled():
             # One kernel for K2, same values as the ops below (fp32 outputs).
             h_pre, h_post, H_merged = torch.ops.flash_mhc.mhc_coefficients(
@@ -207,7 +226,7 @@ class MHCLiteBlock(nn.Module):
         return torch.ops.flash_mhc.fused_post_res(x_streams, layer_output, H_merged, h_post)
 
     def _forward_triton(self, x_streams: torch.Tensor, **kwargs) -> torch.Tensor:
-        """Fused path: K1/K2/K3/K4 on the HIP kernels (K1 + K2 + K3 as one pass)."""
+        """Fused path: K1/K2/K3/K4 on the HIP kernels."""
         ctx = nullcontext() if self.training else _ops.disable_autotune_temporarily()
         # Only the pre-map region is checkpointed: post-res's backward needs
         # exactly the inputs a checkpoint would keep (x, layer_output,
@@ -220,12 +239,10 @@ class MHCLiteBlock(nn.Module):
     def _run(self, x_streams, pre_map, post_res, ctx, kwargs, checkpoint_post_res=True) -> torch.Tensor:
         use_ckpt = self._use_activation_checkpointing(x_streams)
         with ctx:
-            # pre_map returns (layer_input, H_merged, h_post, *extra); post_res
+            # pre_map(x, use_ckpt) returns (layer_input, H_merged, h_post, *extra)
+            # and applies the checkpointing of its region itself; post_res
             # takes (x_streams, layer_output, H_merged, h_post, *extra).
-            if use_ckpt:
-                layer_input, *coeffs = _checkpoint(pre_map, x_streams, use_reentrant=False)
-            else:
-                layer_input, *coeffs = pre_map(x_streams)
+            layer_input, *coeffs = pre_map(x_streams, use_ckpt)
 
             layer_output = self.layer(layer_input, **kwargs)
 

@@ -240,15 +240,16 @@ def k2_bwd(proj: torch.Tensor, alpha_pre: torch.Tensor, alpha_post: torch.Tensor
 
 def premap_fwd(x_streams: torch.Tensor, W: torch.Tensor, alpha_pre: torch.Tensor,
                alpha_post: torch.Tensor, alpha_res: torch.Tensor, bias: torch.Tensor,
-               perm: torch.Tensor):
+               perm: torch.Tensor, layer_input: bool = True):
     """K1 + K2 + K3: (layer_input (T,C) bf16, H_merged (T,4,4), h_post (T,4),
-    h_pre (T,4) fp32, proj (T,32) bf16, inv_rms (T,) fp32)."""
+    h_pre (T,4) fp32, proj (T,32) bf16, inv_rms (T,) fp32).  layer_input=False:
+    K1 + K2 only, the first output is None."""
     T, n, C = _streams_shape(x_streams)
     dev = _device_of(x_streams)
     _require(x_streams, "x_streams", _BF16, (T, n, C), dev)
     _require(W, "W", _BF16, (D_OUT, n * C), dev)
     pdt = _k2_params(alpha_pre, alpha_post, alpha_res, bias, perm, dev)
-    li = torch.empty((T, C), device=dev, dtype=_BF16)
+    li = torch.empty((T, C), device=dev, dtype=_BF16) if layer_input else None
     proj = torch.empty((T, D_OUT), device=dev, dtype=_BF16)
     inv = torch.empty((T,), device=dev, dtype=_F32)
     h_pre = torch.empty((T, n), device=dev, dtype=_F32)
@@ -259,7 +260,7 @@ def premap_fwd(x_streams: torch.Tensor, W: torch.Tensor, alpha_pre: torch.Tensor
     with _OnDevice(dev):
         st = lib.fmhc_premap_fwd(x_streams.data_ptr(), W.data_ptr(), alpha_pre.data_ptr(),
                                  alpha_post.data_ptr(), alpha_res.data_ptr(), bias.data_ptr(),
-                                 perm.data_ptr(), pdt, li.data_ptr(), proj.data_ptr(), inv.data_ptr(),
+                                 perm.data_ptr(), pdt, _ptr_or_none(li), proj.data_ptr(), inv.data_ptr(),
                                  h_pre.data_ptr(), h_post.data_ptr(), H.data_ptr(), _ptr_or_none(ws),
                                  0 if ws is None else ws.numel(), T, C, n, _abi.stream_of(x_streams))
     _abi.check(st, "premap_fwd")

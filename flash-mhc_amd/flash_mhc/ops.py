@@ -78,6 +78,17 @@ _lib.define(
 _lib.define(
     "mhc_pre_map_backward(Tensor? grad_layer_input, Tensor? grad_H_merged, Tensor? grad_h_post, Tensor? grad_h_pre, Tensor? grad_proj, Tensor? grad_x_sink, Tensor x_streams, Tensor W, Tensor alpha_pre, Tensor alpha_post, Tensor alpha_res, Tensor bias, Tensor perm_mat, Tensor h_pre, Tensor proj, Tensor inv_rms) -> (Tensor grad_x, Tensor grad_W, Tensor grad_alpha_pre, Tensor grad_alpha_post, Tensor grad_alpha_res, Tensor grad_bias)"
 )
+# Not in the reference: mhc_pre_map in two ops, so that activation
+# checkpointing can recompute K3 alone (the layer input is the one large
+# tensor of the region; K1's and K2's outputs are 84 bytes per token).
+# mhc_pre_map_coeffs runs K1 + K2 and returns, besides x_sink, li_sink: a
+# zero-stride (T, C) placeholder passed to mhc_pre_map_mix (K3).  mix's
+# backward hands the layer input's gradient to li_sink unchanged, and
+# mhc_pre_map_coeffs's backward is mhc_pre_map's fused backward.
+_lib.define(
+    "mhc_pre_map_coeffs(Tensor x_streams, Tensor W, Tensor alpha_pre, Tensor alpha_post, Tensor alpha_res, Tensor bias, Tensor perm_mat) -> (Tensor H_merged, Tensor h_post, Tensor h_pre, Tensor proj, Tensor inv_rms, Tensor x_sink, Tensor li_sink)"
+)
+_lib.define("mhc_pre_map_mix(Tensor x_streams, Tensor h_pre, Tensor li_sink) -> Tensor layer_input")
 # Not in the reference: fused_post_res whose x-gradient goes to x_sink (an
 # output of mhc_pre_map for the same x) instead of x.  Same forward.
 _lib.define(
@@ -164,13 +175,17 @@ def x_sink_like(x_streams: torch.Tensor) -> torch.Tensor:
     return x_streams.new_empty_strided(tuple(x_streams.shape), (0,) * x_streams.dim())
 
 
-def _x_sink(x_streams: torch.Tensor) -> torch.Tensor:
-    """x_sink_like with its one element set to zero (a one-element fill, not
-    T n C); an empty batch's sink has no storage to fill."""
-    sink = x_sink_like(x_streams)
+def _zero_sink(sink: torch.Tensor) -> torch.Tensor:
+    """Set a zero-stride placeholder's one element to zero (a one-element
+    fill, not numel); an empty one has no storage to fill."""
     if sink.numel() > 0:
         sink.as_strided((1,), (1,)).zero_()
     return sink
+
+
+def _x_sink(x_streams: torch.Tensor) -> torch.Tensor:
+    """mhc_pre_map's x_sink, its element zeroed."""
+    return _zero_sink(x_sink_like(x_streams))
 
 
 @torch.library.register_fake("flash_mhc::mhc_pre_map")
@@ -181,6 +196,22 @@ def _mhc_pre_map_fake(x_streams, W, alpha_pre, alpha_post, alpha_res, bias, perm
             x_streams.new_empty((T, n), dtype=f32), x_streams.new_empty((T, n), dtype=f32),
             x_streams.new_empty((T, W.shape[0])), x_streams.new_empty((T,), dtype=f32),
             x_sink_like(x_streams))
+
+
+@torch.library.register_fake("flash_mhc::mhc_pre_map_coeffs")
+def _mhc_pre_map_coeffs_fake(x_streams, W, alpha_pre, alpha_post, alpha_res, bias, perm_mat):
+    T, n, C = x_streams.shape
+    f32 = torch.float32
+    return (x_streams.new_empty((T, n, n), dtype=f32), x_streams.new_empty((T, n), dtype=f32),
+            x_streams.new_empty((T, n), dtype=f32), x_streams.new_empty((T, W.shape[0])),
+            x_streams.new_empty((T,), dtype=f32), x_sink_like(x_streams),
+            x_streams.new_empty_strided((T, C), (0, 0)))
+
+
+@torch.library.register_fake("flash_mhc::mhc_pre_map_mix")
+def _mhc_pre_map_mix_fake(x_streams, h_pre, li_sink):
+    T, n, C = x_streams.shape
+    return x_streams.new_empty((T, C))
 
 
 @torch.library.register_fake("flash_mhc::mhc_pre_map_backward")
@@ -299,6 +330,24 @@ def _mhc_pre_map_cuda(x_streams, W, alpha_pre, alpha_post, alpha_res, bias, perm
     outs = _k.premap_fwd(x_streams.contiguous(), W.to(x_streams.dtype).contiguous(),
                          *_params(alpha_pre, alpha_post, alpha_res, bias, perm_mat))
     return (*outs, _x_sink(x_streams))
+
+
+@torch.library.impl(_lib, "mhc_pre_map_coeffs", "CUDA")
+def _mhc_pre_map_coeffs_cuda(x_streams, W, alpha_pre, alpha_post, alpha_res, bias, perm_mat):
+    _check_n4(x_streams, "flash_mhc::mhc_pre_map_coeffs supports n=4 only")
+    _check_k2(x_streams.new_empty((0, W.shape[0])), perm_mat)
+    _li, H, h_post, h_pre, proj, inv = _k.premap_fwd(
+        x_streams.contiguous(), W.to(x_streams.dtype).contiguous(),
+        *_params(alpha_pre, alpha_post, alpha_res, bias, perm_mat), layer_input=False)
+    T, n, C = x_streams.shape
+    li_sink = _zero_sink(x_streams.new_empty_strided((T, C), (0, 0)))
+    return H, h_post, h_pre, proj, inv, _x_sink(x_streams), li_sink
+
+
+@torch.library.impl(_lib, "mhc_pre_map_mix", "CUDA")
+def _mhc_pre_map_mix_cuda(x_streams, h_pre, li_sink):
+    _check_n4(x_streams, "flash_mhc::mhc_pre_map_mix supports n=4 only")
+    return _k.k3_fwd(x_streams.contiguous(), _coeff(h_pre))
 
 
 @torch.library.impl(_lib, "mhc_pre_map_backward", "CUDA")
@@ -488,6 +537,39 @@ torch.library.register_autograd(
     "flash_mhc::mhc_pre_map",
     _mhc_pre_map_backward,
     setup_context=_setup_pre_map,
+)
+
+
+def _setup_pre_map_coeffs(ctx, inputs, output):
+    _H, _hp, h_pre, proj, inv_rms, _xs, _ls = output
+    ctx.save_for_backward(*inputs, h_pre, proj, inv_rms)
+    ctx.set_materialize_grads(False)
+
+
+def _mhc_pre_map_coeffs_backward(ctx, g_H, g_hp, g_hpre, g_proj, _g_inv_rms, g_xsink, g_lisink):
+    # g_lisink is the layer input's gradient, handed over by mhc_pre_map_mix.
+    x, W, ap, apo, ar, b, perm, h_pre, proj, inv_rms = ctx.saved_tensors
+    grads = torch.ops.flash_mhc.mhc_pre_map_backward(
+        g_lisink, g_H, g_hp, g_hpre, g_proj, g_xsink, x, W, ap, apo, ar, b, perm, h_pre, proj, inv_rms
+    )
+    return (*grads, None)
+
+
+def _mhc_pre_map_mix_backward(ctx, g_li):
+    # K3's gradients with respect to x and h_pre are formed in
+    # mhc_pre_map_coeffs's backward from the layer input's gradient.
+    return None, None, g_li
+
+
+torch.library.register_autograd(
+    "flash_mhc::mhc_pre_map_coeffs",
+    _mhc_pre_map_coeffs_backward,
+    setup_context=_setup_pre_map_coeffs,
+)
+torch.library.register_autograd(
+    "flash_mhc::mhc_pre_map_mix",
+    _mhc_pre_map_mix_backward,
+    setup_context=lambda ctx, inputs, output: None,
 )
 torch.library.register_autograd(
     "flash_mhc::fused_pre_map",

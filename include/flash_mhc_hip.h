@@ -130,6 +130,7 @@ int64_t fmhc_k2_bwd_workspace_bytes(int64_t T);
  * proj (T, 32) bf16, inv_rms (T,) fp32, h_pre, h_post (T, 4) and
  * H_merged (T, 4, 4) fp32 (16-byte aligned).  x (T, n, C) bf16, W (32, n C)
  * bf16, alphas / bias / perm / param_dtype as fmhc_k2_fwd; n must be 4.
+ * layer_input may be NULL: K1 and K2 only (the coefficients), K3 skipped.
  * Replaces: src/flash_mhc/block.py:157-177 (_mhc_pre_map_triton: the K1 launch,
  *           the K2 PyTorch ops and the K3 launch). */
 int fmhc_premap_fwd(const uint16_t* x, const uint16_t* W, const void* alpha_pre,

@@ -65,6 +65,21 @@ def _pre_map(x, W, ap, apo, ar, b, perm):
     return _k3(x, h_pre), H, h_post, h_pre, proj, inv, sink
 
 
+def _pre_map_coeffs(x, W, ap, apo, ar, b, perm):
+    T, n, C = x.shape
+    proj, inv = _k1(x.reshape(T, n * C), W.to(x.dtype))
+    h_pre, h_post, H = _k2(proj, ap, apo, ar, b, perm)
+    sinks = [x.new_empty_strided(shape, (0,) * len(shape)) for shape in (tuple(x.shape), (T, C))]
+    for sink in sinks:  # x_sink and li_sink, one zeroed element each
+        if sink.numel() > 0:
+            sink.as_strided((1,), (1,)).zero_()
+    return H, h_post, h_pre, proj, inv, sinks[0], sinks[1]
+
+
+def _pre_map_mix(x, h_pre, li_sink):
+    return _k3(x, h_pre)
+
+
 def _pre_map_bwd(g_li, g_H, g_hp, g_hpre, g_proj, g_sink, x, W, ap, apo, ar, b, perm, h_pre, proj, inv):
     T, n, C = x.shape
     if g_li is None:
@@ -117,6 +132,8 @@ IMPLS = {
     "mhc_coefficients_backward": _k2_bwd,
     "mhc_pre_map": _pre_map,
     "mhc_pre_map_backward": _pre_map_bwd,
+    "mhc_pre_map_coeffs": _pre_map_coeffs,
+    "mhc_pre_map_mix": _pre_map_mix,
     "fused_pre_map": _k3,
     "fused_pre_map_backward": _k3_bwd,
     "fused_post_res": _k4,

@@ -63,6 +63,8 @@ ADDED_SCHEMAS = {
     "mhc_pre_map": "mhc_pre_map(Tensor x_streams, Tensor W, Tensor alpha_pre, Tensor alpha_post, Tensor alpha_res, Tensor bias, Tensor perm_mat) -> (Tensor layer_input, Tensor H_merged, Tensor h_post, Tensor h_pre, Tensor proj, Tensor inv_rms, Tensor x_sink)",
     "mhc_pre_map_backward": "mhc_pre_map_backward(Tensor? grad_layer_input, Tensor? grad_H_merged, Tensor? grad_h_post, Tensor? grad_h_pre, Tensor? grad_proj, Tensor? grad_x_sink, Tensor x_streams, Tensor W, Tensor alpha_pre, Tensor alpha_post, Tensor alpha_res, Tensor bias, Tensor perm_mat, Tensor h_pre, Tensor proj, Tensor inv_rms) -> (Tensor grad_x, Tensor grad_W, Tensor grad_alpha_pre, Tensor grad_alpha_post, Tensor grad_alpha_res, Tensor grad_bias)",
     "mhc_post_res": "mhc_post_res(Tensor x_streams, Tensor x_sink, Tensor layer_output, Tensor H_merged, Tensor h_post) -> Tensor out",
+    "mhc_pre_map_coeffs": "mhc_pre_map_coeffs(Tensor x_streams, Tensor W, Tensor alpha_pre, Tensor alpha_post, Tensor alpha_res, Tensor bias, Tensor perm_mat) -> (Tensor H_merged, Tensor h_post, Tensor h_pre, Tensor proj, Tensor inv_rms, Tensor x_sink, Tensor li_sink)",
+    "mhc_pre_map_mix": "mhc_pre_map_mix(Tensor x_streams, Tensor h_pre, Tensor li_sink) -> Tensor layer_input",
 }
 
 
@@ -218,7 +220,15 @@ def test_opcheck_all_ops(cpu_kernels):
         (torch.ops.flash_mhc.mhc_post_res.default,
          (x.clone().requires_grad_(True), sink.clone().requires_grad_(True), lo.clone().requires_grad_(True),
           H.clone().requires_grad_(True), hp.clone().requires_grad_(True))),
+        (torch.ops.flash_mhc.mhc_pre_map_coeffs.default,
+         (x.clone().requires_grad_(True), W.clone().requires_grad_(True),
+          *[t.clone().requires_grad_(True) for t in k2p], perm)),
     ]
+    outs = torch.ops.flash_mhc.mhc_pre_map_coeffs(x, W, *k2p, perm)
+    assert outs[6].shape == (T, C) and outs[6].stride() == (0, 0)
+    cases.append((torch.ops.flash_mhc.mhc_pre_map_mix.default,
+                  (x.clone().requires_grad_(True), outs[2].clone().requires_grad_(True),
+                   outs[6].clone().requires_grad_(True))))
     for op, args in cases:
         torch.library.opcheck(op, args)
 
