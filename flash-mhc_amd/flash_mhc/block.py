@@ -188,20 +188,20 @@ class MHCLiteBlock(nn.Module):
 
     def _mhc_pre_map_triton(self, x_streams: torch.Tensor, use_ckpt: bool = False):
         if _ops.fused_premap_enabled():
-            # K1 + K2 as one op, K3 as a second one whose backward hands the
-            # layer input's gradient to the first (the fused pre-map backward).
-            # Checkpointing recomputes K3 alone: the layer input is the one
-            # large tensor of the region.  With x_sink, post-res's x-gradient
-            # is added in K1's backward store rather than by autograd.
-            H_merged, h_post, h_pre, _proj, _inv_rms, x_sink, li_sink = torch.ops.flash_mhc.mhc_pre_map_coeffs(
-                x_streams, self._projection_weight(x_streams.dtype), self.alpha_pre,
-                self.alpha_post, self.alpha_res, self.W_all.bias, self.perm_mat,
-            )
-            mix = torch.ops.flash_mhc.mhc_pre_map_mix
+            # With x_sink, post-res's x-gradient is added in K1's backward
+            # store rather than by autograd.
+            args = (x_streams, self._projection_weight(x_streams.dtype), self.alpha_pre, self.alpha_post,
+                    self.alpha_res, self.W_all.bias, self.perm_mat)
             if use_ckpt:
-                layer_input = _checkpoint(mix, x_streams, h_pre, li_sink, use_reentrant=False)
+                # K1 + K2 as one op, K3 as a second one whose backward hands
+                # the layer input's gradient to the first (the fused pre-map
+                # backward); the checkpoint recomputes K3 alone, the layer
+                # input being the one large tensor of the region.
+                H_merged, h_post, h_pre, _proj, _inv, x_sink, li_sink = torch.ops.flash_mhc.mhc_pre_map_coeffs(*args)
+                layer_input = _checkpoint(torch.ops.flash_mhc.mhc_pre_map_mix, x_streams, h_pre, li_sink,
+                                          use_reentrant=False)
             else:
-                layer_input = mix(x_streams, h_pre, li_sink)
+                layer_input, H_merged, h_post, _h_pre, _proj, _inv, x_sink = torch.ops.flash_mhc.mhc_pre_map(*args)
             if _ops.fused_xgrad_enabled():
                 return layer_input, H_merged, h_post, x_sink
             return layer_input, H_merged, h_post
