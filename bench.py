@@ -158,7 +158,7 @@ def k1_backward_paths(inp: dict, T: int, C: int, iters: int = 20) -> dict:
     return out
 
 
-def block_step(T: int, C: int, iters: int = 10) -> dict:
+def block_step(T: int, C: int, iters: int = 10, variants=("fused", "reference_rules")) -> dict:
     """MHCLiteBlock(4, C, Linear(C, C)) forward + backward (bf16, random
     weights) with the fused path as shipped, and with the reference's rules
     (K2 as PyTorch ops, K1's grad_W as a matmul, separate pre-map ops)."""
@@ -173,6 +173,8 @@ def block_step(T: int, C: int, iters: int = 10) -> dict:
     out = {}
     try:
         for name, val in (("fused", "1"), ("reference_rules", "0")):
+            if name not in variants:
+                continue
             for f in flags:
                 os.environ[f] = val
 
@@ -200,7 +202,7 @@ def block_step(T: int, C: int, iters: int = 10) -> dict:
     return out
 
 
-def eval_latency(C: int = 4096, tokens=(1, 64, 257, 65537)) -> dict:
+def eval_latency(C: int = 4096, tokens=(1, 64, 257, 65537), variants=("fused", "reference_rules")) -> dict:
     """Eval-mode forward latency of MHCLiteBlock(4, C, Linear(C, C)) (bf16,
     random weights), the inference / ragged-tail shapes: eager and replayed from
     a captured HIP graph, for the fused path and for the reference's rules
@@ -244,6 +246,8 @@ def eval_latency(C: int = 4096, tokens=(1, 64, 257, 65537)) -> dict:
                 x = torch.randn(T, 4, C, device="cuda", dtype=torch.bfloat16)
                 row = {}
                 for name, val in (("fused", "1"), ("reference_rules", "0")):
+                    if name not in variants:
+                        continue
                     for f in flags:
                         os.environ[f] = val
                     if name == "fused":
@@ -376,6 +380,10 @@ def main() -> None:
                     help="skip the K1-backward and block-step fields (profiler runs: only the six kernels)")
     ap.add_argument("--traffic", type=str, default=str(ROOT / "profiles" / "traffic_k4_bwd_T65536_C1024.json"),
                     help="measured HBM traffic summary (rocprofv3 --pmc) for the dominant kernel")
+    ap.add_argument("--only", choices=("block", "eval"), default=None,
+                    help="run one extra alone, fused path only, and print its JSON (profiler runs of the "
+                         "block step at --T/--C for --steps iterations, or of the eval latency at --eval-T)")
+    ap.add_argument("--eval-T", type=str, default="1,64,257,65537", help="token counts of the eval latency")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -391,6 +399,14 @@ def main() -> None:
     from flash_mhc import _abi
 
     _abi.load()  # fail loudly if the extension is missing
+    eval_tokens = tuple(int(t) for t in args.eval_T.split(","))
+    if args.only == "block":
+        print(json.dumps({"block_step": block_step(args.T, args.C, iters=args.steps, variants=("fused",))}),
+              flush=True)
+        return
+    if args.only == "eval":
+        print(json.dumps({"eval_latency": eval_latency(tokens=eval_tokens, variants=("fused",))}), flush=True)
+        return
     T, C, n, D = args.T, args.C, 4, 32
     inp = make_inputs(T, C)
     launch = make_step(inp, T, C)
@@ -460,7 +476,7 @@ def main() -> None:
 
     k1_full_bwd = None if args.no_extras else k1_backward_paths(inp, T, C)
     blk = None if args.no_extras else block_step(T, C)
-    lat = None if args.no_extras else eval_latency()
+    lat = None if args.no_extras else eval_latency(tokens=eval_tokens)
     ceil = stream_ceilings()
     split = read_write_split(T, n, C, D)
     for name in KERNELS:

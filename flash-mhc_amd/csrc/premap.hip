@@ -54,21 +54,31 @@ __global__ __launch_bounds__(kFinishThreads) void k1_finish_k2(
   const int q = threadIdx.x & 31;
   const int64_t t = static_cast<int64_t>(blockIdx.x) * (kFinishThreads / 32) + (threadIdx.x >> 5);
   if (t >= T) return;  // a whole 32-lane group leaves together
+  // Projection q and the sum of squares, each added over the S partials in
+  // split order; the loads of both run ahead together.
   const int s4 = (S + 3) & ~3;
-  auto add = [&](int v) {
-    const f32x4* p = reinterpret_cast<const f32x4*>(part + (t * (kDk + 1) + v) * s4);
-    float acc = 0.f;
-    for (int i = 0; i < s4 / 4; ++i) {
-      const f32x4 w = p[i];
-      acc += w[0];  // 4 i < S always
-      if (4 * i + 1 < S) acc += w[1];
-      if (4 * i + 2 < S) acc += w[2];
-      if (4 * i + 3 < S) acc += w[3];
+  const f32x4* pv = reinterpret_cast<const f32x4*>(part + (t * (kDk + 1) + q) * s4);
+  const f32x4* ps = reinterpret_cast<const f32x4*>(part + (t * (kDk + 1) + kDk) * s4);
+  float v = 0.f, ss = 0.f;
+#pragma unroll 8
+  for (int i = 0; i < s4 / 4; ++i) {
+    const f32x4 a = pv[i], b = ps[i];
+    v += a[0];  // 4 i < S always
+    ss += b[0];
+    if (4 * i + 1 < S) {
+      v += a[1];
+      ss += b[1];
     }
-    return acc;
-  };
-  const float v = add(q);
-  const float inv = rsqrtf(add(kDk) / static_cast<float>(nC) + kRmsEps);
+    if (4 * i + 2 < S) {
+      v += a[2];
+      ss += b[2];
+    }
+    if (4 * i + 3 < S) {
+      v += a[3];
+      ss += b[3];
+    }
+  }
+  const float inv = rsqrtf(ss / static_cast<float>(nC) + kRmsEps);
   const uint16_t pj = f32_to_bf16(v * inv);
   proj[t * kDk + q] = pj;
   if (q == 0) inv_rms[t] = inv;
