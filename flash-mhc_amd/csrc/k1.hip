@@ -1,5 +1,12 @@
 // K1: fused RMSNorm over the flattened n*C stream + the D_out = 32 wide
-// coefficient projection, and the x-gradient of that op.
+// coefficient projection, and its backward.
+//
+// Kernels: k1_fwd_mfma (one pass over x per 128-token workgroup, or, for few
+// tokens, a column split whose partial sums k1_fwd_finish adds),
+// k1_bwd_mfma (dx; with DW also grad_W's per-run partials, which
+// k1_dw_reduce adds; with EPI / GI the pre-map backward's extra terms of
+// grad_x in the same store), and element-wise kernels for shapes off the
+// matrix-core path (nC % 8 != 0, unaligned pointers).
 //
 //   forward   inv_rms[t] = rsqrt(sum_k x[t,k]^2 / nC + 1e-6)
 //             out[t,d]   = bf16(inv_rms[t] * sum_k x[t,k] * W[d,k])
