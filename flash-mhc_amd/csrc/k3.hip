@@ -88,12 +88,19 @@ __global__ __launch_bounds__(kBlock) void k3_bwd_kernel(const uint16_t* __restri
                                                         uint16_t* __restrict__ grad_x,
                                                         float* __restrict__ grad_h_pre,
                                                         int64_t T, int C) {
+  constexpr int WPT = LPT > kWave ? LPT / kWave : 1;  // waves per token
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t tok = token_of_lane<LPT>(lane);
-  if (tok >= T) return;
-  const int sub = lane % LPT;
+  // With several waves per token every wave reaches the barrier below.
+  if constexpr (WPT == 1) {
+    if (tok >= T) return;
+  }
+  const bool live = tok < T;
+  const int sub = sub_of_lane<LPT>();
   const int ng = C / VEC;
 
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+  if (live) {
   const float* hp = h_pre + tok * 4;
   const float h0 = hp[0], h1 = hp[1], h2 = hp[2], h3 = hp[3];
   const uint16_t* x0 = x + tok * 4 * C;
@@ -106,7 +113,6 @@ __global__ __launch_bounds__(kBlock) void k3_bwd_kernel(const uint16_t* __restri
   uint16_t* gx2 = gx1 + C;
   uint16_t* gx3 = gx2 + C;
 
-  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
 #pragma unroll 2
   for (int g = sub; g < ng; g += LPT) {
     float q[VEC], a[VEC], b[VEC], c[VEC], d[VEC], o[VEC];
@@ -137,11 +143,34 @@ __global__ __launch_bounds__(kBlock) void k3_bwd_kernel(const uint16_t* __restri
       s3 = __builtin_fmaf(d[e], q[e], s3);
     }
   }
-  s0 = group_sum<LPT>(s0);
-  s1 = group_sum<LPT>(s1);
-  s2 = group_sum<LPT>(s2);
-  s3 = group_sum<LPT>(s3);
-  if (sub == 0) {
+  }
+  constexpr int GS = LPT < kWave ? LPT : kWave;
+  s0 = group_sum<GS>(s0);
+  s1 = group_sum<GS>(s1);
+  s2 = group_sum<GS>(s2);
+  s3 = group_sum<GS>(s3);
+  if constexpr (WPT > 1) {
+    // The token's waves add their sums in wave order (deterministic).
+    __shared__ float red[kBlock / kWave][4];
+    const int wave = static_cast<int>(threadIdx.x) >> 6;
+    if (lane == 0) {
+      red[wave][0] = s0;
+      red[wave][1] = s1;
+      red[wave][2] = s2;
+      red[wave][3] = s3;
+    }
+    __syncthreads();
+    if (live && sub == 0) {
+      float t[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int w = 0; w < WPT; ++w)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) t[k] += red[wave + w][k];
+      float* dst = grad_h_pre + tok * 4;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) dst[k] = t[k];
+    }
+  } else if (sub == 0) {
     float* dst = grad_h_pre + tok * 4;
     dst[0] = s0;
     dst[1] = s1;
@@ -151,24 +180,30 @@ __global__ __launch_bounds__(kBlock) void k3_bwd_kernel(const uint16_t* __restri
 }
 
 // Lanes per token: a full wave for wide rows, fewer lanes (more tokens per
-// wave) when a row would leave most of a wave idle.
+// wave) when a row would leave most of a wave idle.  A full wave from one
+// 8-element group per lane on: at C = 512 the backward kernels are 5% (K3)
+// and 20% (K4) faster with 64 lanes than with 32.
 template <int VEC>
 int pick_lpt(int C) {
   const int groups = C / VEC;
-  if (groups >= 128) return 64;
+  if (groups >= 64) return 64;
   if (groups >= 32) return 32;
   if (groups >= 16) return 16;
   return 8;
 }
 
-// Forward kernels with few tokens spread a token over more lanes (up to a
-// workgroup), so that each lane has one or two 8-element groups per stream
-// instead of a loop: latency, not bandwidth, bounds that regime.
+// The forward kernel spreads a token over more lanes (up to a workgroup),
+// so that each lane has one or two 8-element groups per stream instead of a
+// loop over them.  Measured at T x C = 64 Mi elements: with 256 lanes per
+// token from C = 2048 on the kernel is 13-17% faster than with one wave;
+// at C = 1024 K3 is 2% faster with one wave.  Few tokens always take the
+// wide layout (latency, not bandwidth, bounds that regime).
 template <int VEC>
 int pick_lpt_fwd(int C, int64_t T) {
   const int lpt = pick_lpt<VEC>(C);
   const int groups = C / VEC;
-  if (T * lpt < int64_t{256} * kBlock && groups >= 128) return groups >= 256 ? 256 : 128;
+  if (groups >= 256) return 256;
+  if (groups >= 128) return T * lpt < int64_t{256} * kBlock ? 128 : lpt;
   return lpt;
 }
 
@@ -189,13 +224,23 @@ int launch_k3_fwd(const uint16_t* x, const float* h_pre, uint16_t* out, int64_t 
   return launch_status();
 }
 
+// Backward: a workgroup per token from C = 2048 on (the four per-token sums
+// then finish across the waves in LDS): 14-24% faster there than one wave
+// per token at T x C = 64 Mi elements.  At C = 1024 two waves per token are
+// 16% slower than one, which stays the choice below C = 2048.
+template <int VEC>
+int pick_lpt_bwd(int C) {
+  return C / VEC >= 256 ? 256 : pick_lpt<VEC>(C);
+}
+
 template <int VEC, bool GX>
 int launch_k3_bwd(const uint16_t* x, const float* h_pre, const uint16_t* go, uint16_t* grad_x,
                   float* grad_h_pre, int64_t T, int C, hipStream_t s) {
-  const int lpt = pick_lpt<VEC>(C);
-  const int64_t tokens_per_block = (kBlock / kWave) * (kWave / lpt);
+  const int lpt = pick_lpt_bwd<VEC>(C);
+  const int64_t tokens_per_block = lpt > kWave ? kBlock / lpt : (kBlock / kWave) * (kWave / lpt);
   const dim3 grid(blocks_for(T, tokens_per_block));
   switch (lpt) {
+    case 256: k3_bwd_kernel<VEC, 256, GX><<<grid, kBlock, 0, s>>>(x, h_pre, go, grad_x, grad_h_pre, T, C); break;
     case 64: k3_bwd_kernel<VEC, 64, GX><<<grid, kBlock, 0, s>>>(x, h_pre, go, grad_x, grad_h_pre, T, C); break;
     case 32: k3_bwd_kernel<VEC, 32, GX><<<grid, kBlock, 0, s>>>(x, h_pre, go, grad_x, grad_h_pre, T, C); break;
     case 16: k3_bwd_kernel<VEC, 16, GX><<<grid, kBlock, 0, s>>>(x, h_pre, go, grad_x, grad_h_pre, T, C); break;

@@ -108,12 +108,25 @@ __global__ __launch_bounds__(kBlock) void k4_bwd_kernel(const uint16_t* __restri
                                                         float* __restrict__ grad_H,
                                                         float* __restrict__ grad_hp,
                                                         int64_t T, int C) {
+  constexpr int WPT = LPT > kWave ? LPT / kWave : 1;  // waves per token
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t tok = token_of_lane<LPT>(lane);
-  if (tok >= T) return;
-  const int sub = lane % LPT;
+  // With several waves per token every wave reaches the barrier below.
+  if constexpr (WPT == 1) {
+    if (tok >= T) return;
+  }
+  const bool live = tok < T;
+  const int sub = sub_of_lane<LPT>();
   const int ng = C / VEC;
 
+  float shp[4] = {0.f, 0.f, 0.f, 0.f};
+  float sH[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sH[i][j] = 0.f;
+
+  if (live) {
   float h[4][4], p[4];
   {
     const float* Ht = H + tok * 16;
@@ -139,13 +152,6 @@ __global__ __launch_bounds__(kBlock) void k4_bwd_kernel(const uint16_t* __restri
   }
   const uint16_t* lrow = lo + tok * C;
   uint16_t* glrow = grad_lo + tok * C;
-
-  float shp[4] = {0.f, 0.f, 0.f, 0.f};
-  float sH[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) sH[i][j] = 0.f;
 
 #pragma unroll 2
   for (int g = sub; g < ng; g += LPT) {
@@ -190,14 +196,44 @@ __global__ __launch_bounds__(kBlock) void k4_bwd_kernel(const uint16_t* __restri
       Lanes<VEC>::store(gxr[j], g, o);
     }
   }
+  }
 
+  constexpr int GS = LPT < kWave ? LPT : kWave;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    shp[i] = group_sum<LPT>(shp[i]);
+    shp[i] = group_sum<GS>(shp[i]);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) sH[i][j] = group_sum<LPT>(sH[i][j]);
+    for (int j = 0; j < 4; ++j) sH[i][j] = group_sum<GS>(sH[i][j]);
   }
-  if (sub == 0) {
+  if constexpr (WPT > 1) {
+    // The token's waves add their 20 sums in wave order (deterministic).
+    __shared__ float red[kBlock / kWave][20];
+    const int wave = static_cast<int>(threadIdx.x) >> 6;
+    if (lane == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        red[wave][16 + i] = shp[i];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) red[wave][i * 4 + j] = sH[i][j];
+      }
+    }
+    __syncthreads();
+    if (live && sub == 0) {
+      float t[20];
+#pragma unroll
+      for (int k = 0; k < 20; ++k) t[k] = 0.f;
+#pragma unroll
+      for (int w = 0; w < WPT; ++w)
+#pragma unroll
+        for (int k = 0; k < 20; ++k) t[k] += red[wave + w][k];
+      float* dH = grad_H + tok * 16;
+      float* dp = grad_hp + tok * 4;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) dH[k] = t[k];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dp[i] = t[16 + i];
+    }
+  } else if (sub == 0) {
     float* dH = grad_H + tok * 16;
     float* dp = grad_hp + tok * 4;
 #pragma unroll
@@ -209,30 +245,45 @@ __global__ __launch_bounds__(kBlock) void k4_bwd_kernel(const uint16_t* __restri
   }
 }
 
+// Lanes per token: a full wave from one 8-element group per lane on (at
+// C = 512, 64 lanes make the backward 20% and the forward 4% faster than 32),
+// fewer lanes (more tokens per wave) for narrower rows.
 template <int VEC>
 int pick_lpt(int C) {
   const int groups = C / VEC;
-  if (groups >= 128) return 64;
+  if (groups >= 64) return 64;
   if (groups >= 32) return 32;
   if (groups >= 16) return 16;
   return 8;
 }
 
-// Forward kernels with few tokens spread a token over more lanes (up to a
-// workgroup), so that each lane has one or two 8-element groups per stream
-// instead of a loop: latency, not bandwidth, bounds that regime.
+// The forward kernel spreads a token over more lanes (up to a workgroup),
+// so that each lane has one or two 8-element groups per stream instead of a
+// loop over them.  Measured at T x C = 64 Mi elements: with 256 lanes per
+// token from C = 2048 on the kernel is 13-17% faster than with one wave, and
+// at C = 1024 2% faster with 128 lanes; few tokens gain most (latency bounds
+// that regime).
 template <int VEC>
-int pick_lpt_fwd(int C, int64_t T) {
-  const int lpt = pick_lpt<VEC>(C);
+int pick_lpt_fwd(int C) {
   const int groups = C / VEC;
-  if (T * lpt < int64_t{256} * kBlock && groups >= 128) return groups >= 256 ? 256 : 128;
-  return lpt;
+  if (groups >= 256) return 256;
+  if (groups >= 128) return 128;
+  return pick_lpt<VEC>(C);
+}
+
+// Backward: a workgroup per token from C = 2048 on (the 20 per-token sums
+// then finish across the waves in LDS): 13% faster there than one wave per
+// token at T x C = 64 Mi elements; at C = 1024 two waves per token gain
+// under 1%, so one wave stays the choice below C = 2048.
+template <int VEC>
+int pick_lpt_bwd(int C) {
+  return C / VEC >= 256 ? 256 : pick_lpt<VEC>(C);
 }
 
 template <int VEC>
 int launch_k4_fwd(const uint16_t* x, const uint16_t* lo, const float* H, const float* hp,
                   uint16_t* out, int64_t T, int C, hipStream_t s) {
-  const int lpt = pick_lpt_fwd<VEC>(C, T);
+  const int lpt = pick_lpt_fwd<VEC>(C);
   const int64_t tokens_per_block = lpt > kWave ? kBlock / lpt : (kBlock / kWave) * (kWave / lpt);
   const dim3 grid(blocks_for(T, tokens_per_block));
   switch (lpt) {
@@ -250,10 +301,12 @@ template <int VEC>
 int launch_k4_bwd(const uint16_t* x, const uint16_t* lo, const float* H, const float* hp,
                   const uint16_t* go, uint16_t* gx, uint16_t* glo, float* gH, float* ghp,
                   int64_t T, int C, hipStream_t s) {
-  const int lpt = pick_lpt<VEC>(C);
-  const int64_t tokens_per_block = (kBlock / kWave) * (kWave / lpt);
+  const int lpt = pick_lpt_bwd<VEC>(C);
+  const int64_t tokens_per_block = lpt > kWave ? kBlock / lpt : (kBlock / kWave) * (kWave / lpt);
   const dim3 grid(blocks_for(T, tokens_per_block));
   switch (lpt) {
+    case 256: k4_bwd_kernel<VEC, 256><<<grid, kBlock, 0, s>>>(x, lo, H, hp, go, gx, glo, gH, ghp, T, C); break;
+    case 128: k4_bwd_kernel<VEC, 128><<<grid, kBlock, 0, s>>>(x, lo, H, hp, go, gx, glo, gH, ghp, T, C); break;
     case 64: k4_bwd_kernel<VEC, 64><<<grid, kBlock, 0, s>>>(x, lo, H, hp, go, gx, glo, gH, ghp, T, C); break;
     case 32: k4_bwd_kernel<VEC, 32><<<grid, kBlock, 0, s>>>(x, lo, H, hp, go, gx, glo, gH, ghp, T, C); break;
     case 16: k4_bwd_kernel<VEC, 16><<<grid, kBlock, 0, s>>>(x, lo, H, hp, go, gx, glo, gH, ghp, T, C); break;

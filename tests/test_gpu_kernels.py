@@ -50,8 +50,11 @@ def misaligned(t: torch.Tensor) -> torch.Tensor:
 
 # (T, C) pairs; nC = 4C.  C=24 / 100 / 1000 exercise ragged tails of the
 # vector paths (K1: nC % 64 != 0; K3/K4: C/8 not a multiple of the lanes per
-# token); C=25 forces the element-wise paths (C % 8 != 0, nC % 8 != 0).
-SHAPES = [(2048, 256), (257, 1024), (1, 4096), (64, 4096), (333, 100), (129, 1000), (31, 24), (17, 25)]
+# token); C=25 forces the element-wise paths (C % 8 != 0, nC % 8 != 0).  C=300
+# and 2050 run the element-wise K3/K4 paths with a workgroup per token (256
+# lanes, the per-token sums finished across waves).
+SHAPES = [(2048, 256), (257, 1024), (1, 4096), (64, 4096), (333, 100), (129, 1000), (31, 24), (17, 25),
+          (7, 300), (5, 2050)]
 
 
 # ---------------------------------------------------------------------------
