@@ -10,8 +10,9 @@ Prints ONE JSON line.  ``value`` = sum of the six kernels' algorithmic bytes /
 measured step time (K steps of bare launches between two events).  Per-kernel
 durations come from a second pass of K steps with an event pair around each
 launch; ``roofline`` describes the dominant kernel (largest average duration),
-timed with those HIP events on the stream it runs on.  Extra fields report
-K1's full backward (fused grad_W vs the reference's matmul), a whole
+timed with those HIP events on the stream it runs on.  ``kernels_isolated``
+times each kernel alone (repeated launches of that kernel).
+Extra fields report K1's full backward (fused grad_W vs the reference's matmul), a whole
 MHCLiteBlock forward + backward with the fused path vs the reference's rules,
 and the eval-mode forward latency of the inference shapes (C=4096,
 T = 1, 64, 257, 65537; eager and HIP-graph replay).
@@ -155,6 +156,31 @@ def k1_backward_paths(inp: dict, T: int, C: int, iters: int = 20) -> dict:
         us = e0.elapsed_time(e1) / iters * 1e3
         out[name] = {"avg_us": round(us, 2), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
     out["bytes"] = nbytes
+    return out
+
+
+def isolated_kernels(launch: dict, bm: dict, iters: int = 20, warmup: int = 5) -> dict:
+    """Each kernel alone: ``iters`` back-to-back launches of the same kernel
+    between two events.  The reference's microbenchmark times one launch per
+    event pair with a synchronize after each (scripts/benchmark_kernels.py:43-57);
+    here that pair also spans the host's launch of the kernel after an idle
+    GPU (K1 bwd-dx: 199 us that way, 167 us in the step), so repeats are timed
+    as a batch.  In the six-kernel step each kernel instead starts while the
+    memory-side cache still holds the previous kernel's dirty lines."""
+    out = {}
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for name in KERNELS:
+        for _ in range(warmup):
+            launch[name]()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(iters):
+            launch[name]()
+        e1.record()
+        torch.cuda.synchronize()
+        avg = e0.elapsed_time(e1) / iters
+        out[name] = {"avg_us": round(avg * 1e3, 2), "GBps": round(bm[name] / (avg * 1e-3) / 1e9, 1),
+                     "frac": round(bm[name] / (avg * 1e-3) / 1e9 / PEAK_GBPS, 4)}
     return out
 
 
@@ -474,6 +500,7 @@ def main() -> None:
         except (OSError, ValueError):
             traffic = None
 
+    alone = None if args.no_extras else isolated_kernels(launch, bm)
     k1_full_bwd = None if args.no_extras else k1_backward_paths(inp, T, C)
     blk = None if args.no_extras else block_step(T, C)
     lat = None if args.no_extras else eval_latency(tokens=eval_tokens)
@@ -510,6 +537,7 @@ def main() -> None:
         "block_step": blk,
         "eval_latency": lat,
         "kernels": per,
+        "kernels_isolated": alone,
         "roofline": {
             "kernel": dom,
             "bound": "hbm",
