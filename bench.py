@@ -239,16 +239,21 @@ def eval_latency(C: int = 4096, tokens=(1, 64, 257, 65537), variants=("fused", "
     blk = flash_mhc.MHCLiteBlock(4, C, torch.nn.Linear(C, C, bias=False)).cuda().bfloat16().eval()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
-    def timed(fn, n):
+    def timed(fn, n, batches=5):
+        # Median over batches of n back-to-back calls: one slow batch (host
+        # or clock hiccup) does not move a latency of a few tens of us.
         for _ in range(3):
             fn()
         torch.cuda.synchronize()
-        e0.record()
-        for _ in range(n):
-            fn()
-        e1.record()
-        torch.cuda.synchronize()
-        return round(e0.elapsed_time(e1) / n * 1e3, 1)
+        per = []
+        for _ in range(batches):
+            e0.record()
+            for _ in range(n):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            per.append(e0.elapsed_time(e1) / n)
+        return round(statistics.median(per) * 1e3, 1)
 
     def graphed(x):
         s = torch.cuda.Stream()
@@ -268,7 +273,7 @@ def eval_latency(C: int = 4096, tokens=(1, 64, 257, 65537), variants=("fused", "
     try:
         with torch.no_grad():
             for T in tokens:
-                n = 50 if T < 4096 else 10
+                n = 20 if T < 4096 else 4
                 x = torch.randn(T, 4, C, device="cuda", dtype=torch.bfloat16)
                 row = {}
                 for name, val in (("fused", "1"), ("reference_rules", "0")):

@@ -730,14 +730,23 @@ __global__ __launch_bounds__(256) void k1_bwd_scalar(const uint16_t* __restrict_
   }
 }
 
-constexpr int kFwdR = 8;      // token blocks of 16 per workgroup
 constexpr int kFwdSplit = 4;  // waves per workgroup (split of the nC axis)
+// One-pass forward: 16-token blocks per workgroup, kFwdR from kFwdLargeT
+// tokens on, kFwdRSmall below.  Measured against 128-token tiles (one
+// workgroup per CU): equal at T = 65536, C = 1024; 2% faster at T = 262144,
+// C = 4096; 5-7% at T = 65537 (a smaller last tile); 25-50% where 128-token
+// tiles leave CUs idle (T = 8192 ... 32768).
+constexpr int kFwdR = 4;
+constexpr int kFwdRSmall = 2;
+constexpr int64_t kFwdLargeT = 16384;
 // Split forward for few tokens: one 16-token block per workgroup and up to
-// kSplitMax column ranges per block, aiming at kSplitTarget workgroups.
+// kSplitMax column ranges per block, aiming at kSplitTarget workgroups; taken
+// when the plan has at least kSplitMinS ranges (T <= 2048): from there on the
+// one-pass kernel with 32-token tiles is faster (T = 3000 ... 6000: 20-40%).
 constexpr int kSplitR = 1;
 constexpr int64_t kSplitTarget = 512;
 constexpr int64_t kSplitMax = 64;
-constexpr int64_t kSplitMaxT = 8192;
+constexpr int64_t kSplitMinS = 4;
 constexpr int kBwdNTB = 16;   // token blocks of 16 per wave (dx only)
 constexpr int kBwdDwNTB = 64; // token blocks of 16 per wave when grad_W is fused
 
@@ -761,9 +770,10 @@ struct K1FwdSplit {
 K1FwdSplit k1_fwd_split(int64_t T, int64_t nC) {
   K1FwdSplit p;
   const int64_t nall = nC >> 6;
-  if (T <= 0 || T >= kSplitMaxT || nC % 8 != 0 || nC > (int64_t{1} << 24) || nall < 2) return p;
+  if (T <= 0 || nC % 8 != 0 || nC > (int64_t{1} << 24) || nall < 2) return p;
   const int64_t nblk = (T + 16 * kSplitR - 1) / (16 * kSplitR);
   int64_t S = (kSplitTarget + nblk - 1) / nblk;
+  if (S < kSplitMinS) return p;
   S = S < kSplitMax ? S : kSplitMax;
   S = S < nall ? S : nall;
   if (S < 2) return p;
@@ -794,10 +804,14 @@ int k1_fwd_run(const uint16_t* x_flat, const uint16_t* W, uint16_t* out, float* 
       const int st = launch_status();
       if (st != FMHC_OK) return st;
       k1_fwd_finish<<<dim3(blocks_for(T, 4)), 256, 0, s>>>(part, out, inv_rms, T, nc, p.S);
-    } else {
+    } else if (T >= kFwdLargeT) {
       const dim3 grid(blocks_for(T, 16 * kFwdR));
       k1_fwd_mfma<kFwdR, kFwdSplit, false><<<grid, kWave * kFwdSplit, 0, s>>>(x_flat, W, out, inv_rms, nullptr,
                                                                              T, nc, 0);
+    } else {
+      const dim3 grid(blocks_for(T, 16 * kFwdRSmall));
+      k1_fwd_mfma<kFwdRSmall, kFwdSplit, false><<<grid, kWave * kFwdSplit, 0, s>>>(x_flat, W, out, inv_rms,
+                                                                                  nullptr, T, nc, 0);
     }
   } else {
     const dim3 grid(blocks_for(T, 4));

@@ -90,13 +90,15 @@ def test_k1_fwd_misaligned(T, C):
     check_rel("k1 inv_rms (misaligned x)", inv, invR, rtol=1e-5)
 
 
-@pytest.mark.parametrize("T,C", [(1, 1024), (100, 4096), (4095, 1024), (8191, 256), (8192, 1024), (3, 16384)])
+@pytest.mark.parametrize("T,C", [(1, 1024), (100, 4096), (2048, 1024), (4095, 1024), (8191, 256), (8192, 1024),
+                                 (16417, 1024), (3, 16384)])
 def test_k1_fwd_split_columns(T, C):
     """Few tokens: fmhc_k1_fwd_ws splits the nC axis over workgroups and adds
     the fp32 partials in a fixed order.  Both it and the one-pass fmhc_k1_fwd
     meet the oracle's bound; the split result is deterministic; where no split
     is planned (workspace size 0, always from T = 8192 on) the two entry
-    points run the same kernel."""
+    points run the same kernel: 32-token tiles below T = 16384 (T = 4095:
+    a ragged last tile), 64-token tiles from there (T = 16417: ragged)."""
     from flash_mhc import _abi
 
     nC = 4 * C
