@@ -300,8 +300,9 @@ __global__ __launch_bounds__(256) void k1_fwd_finish(const float* __restrict__ p
 // K1 backward dx, matrix-core path (nC % 8 == 0, 16-byte aligned x / W / go /
 // proj_out / inv_rms / grad_x).
 //
-// Each wave owns a 128-wide slice of the nC axis and walks NTB blocks of 16
-// tokens (strided by the number of runs, see below).  Per token block, eight MFMAs (tiles m = 0..7) compute
+// Each wave owns a 128-wide slice of the nC axis and walks one run of blocks
+// of 16 tokens (strided by the number of runs, see below; the host picks the
+// run count, k1_bwd_nruns).  Per token block, eight MFMAs (tiles m = 0..7) compute
 //   D_m (16 tokens x 16 columns) = go[tokens, 0:32] (A) * W[0:32, cols_m] (B)
 // i.e. the whole D_out = 32 contraction in one instruction per tile, where
 // column j of tile m stands for k = k_slice + 8 * j + m.  With D's layout
@@ -343,7 +344,7 @@ struct BwdFrag {
 // operand takes the kernel to one wave per SIMD; it is still bound by HBM
 // (measured: +80 us at T=65536, C=1024 for the 512 MiB it reads, against
 // 260 us for the separate accumulation pass it replaces).
-template <int NTB, bool DW, bool FULLK, bool EPI, bool GI>
+template <bool DW, bool FULLK, bool EPI, bool GI>
 __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ x,
                                                    const uint16_t* __restrict__ W,
                                                    const uint16_t* __restrict__ go,
@@ -354,7 +355,7 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
                                                    const uint16_t* __restrict__ go3,
                                                    const float* __restrict__ h_pre,
                                                    const uint16_t* __restrict__ gi,
-                                                   int64_t T, int nC, int nslices, int C) {
+                                                   int64_t T, int nC, int nslices, int64_t nruns, int C) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
   const int col = lane & 15;  // A row (token) for the loads of go, B/D column
@@ -377,8 +378,7 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
   // Token blocks run, run + nruns, run + 2 * nruns, ...: the waves resident at
   // one time work on neighbouring blocks, so the concurrent reads and writes
   // cover contiguous memory instead of addresses a power-of-two apart.
-  const int64_t nblocks = (T + 15) / 16;
-  const int64_t nruns = (nblocks + NTB - 1) / NTB;  // <= nblocks
+  const int64_t nblocks = (T + 15) / 16;  // nruns <= nblocks
   if (run >= nruns) return;
   const int kl = slice * 128 + 8 * col;  // this lane's 8 consecutive k
   const bool kok = FULLK || kl < nC;     // nC % 8 == 0: all 8 valid or none
@@ -429,8 +429,7 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
   // Token blocks of this wave, two per trip with double-buffered fragments:
   // the next block's go / proj_out / inv_rms / x are in flight while the
   // current block computes (same structure as the forward kernel).
-  const int64_t left = (nblocks - run + nruns - 1) / nruns;
-  const int nb = static_cast<int>(left < NTB ? left : NTB);
+  const int nb = static_cast<int>((nblocks - run + nruns - 1) / nruns);
   auto pos = [&](int i) { return i < nb ? i : nb - 1; };
   auto block_base = [&](int tb) { return (run + static_cast<int64_t>(tb) * nruns) * 16; };
   // Valid rows of the block starting at tbase (16 except in the last block).
@@ -590,7 +589,7 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
   }
 }
 
-// Sums the per-run partials of k1_bwd_mfma<NTB, true, ...> in run order and
+// Sums the per-run partials of k1_bwd_mfma<true, ...> in run order and
 // writes grad_W (32, nC) bf16.  Partial element
 // i = (((slice * 8 + m) * 2 + h) * 4 + r) * 64 + lane stands for
 // d = 16 h + (lane & 15), k = 128 slice + 8 (4 (lane >> 4) + r) + m; each
@@ -747,8 +746,14 @@ constexpr int kSplitR = 1;
 constexpr int64_t kSplitTarget = 512;
 constexpr int64_t kSplitMax = 64;
 constexpr int64_t kSplitMinS = 4;
-constexpr int kBwdNTB = 16;   // token blocks of 16 per wave (dx only)
-constexpr int kBwdDwNTB = 64; // token blocks of 16 per wave when grad_W is fused
+// Runs of k1_bwd_mfma: up to kBwdNTB blocks of 16 tokens per run for dx
+// alone, kBwdDwNTB with grad_W (fewer runs, fewer grad_W partials); with few
+// tokens, runs as short as kBwdDwMinNTB blocks with grad_W (its partials then
+// stay below x's bytes) or one block without.
+constexpr int kBwdNTB = 16;
+constexpr int kBwdDwNTB = 64;
+constexpr int kBwdDwMinNTB = 4;
+constexpr int64_t kBwdFillWaves = 1024;  // one wave per SIMD of 256 CUs
 
 bool bad_sizes(int64_t T, int64_t nC, int64_t D_out) {
   return T < 0 || nC <= 0 || nC > (int64_t{1} << 30) || D_out != kDout;
@@ -820,18 +825,36 @@ int k1_fwd_run(const uint16_t* x_flat, const uint16_t* W, uint16_t* out, float* 
   return launch_status();
 }
 
-template <int NTB, bool DW, bool EPI = false, bool GI = false>
-void launch_k1_bwd_mfma(dim3 grid, hipStream_t s, const uint16_t* x, const uint16_t* W,
-                        const uint16_t* go, const uint16_t* proj, const float* inv_rms, uint16_t* gx,
-                        float* partial, int64_t T, int nC, int nslices,
-                        const uint16_t* go3 = nullptr, const float* h_pre = nullptr, int C = 1,
-                        const uint16_t* gi = nullptr) {
+// Number of runs of k1_bwd_mfma for T tokens (nblocks blocks of 16) and
+// nC / 128 slices: ceil(nblocks / max_blocks) runs, or, when those leave SIMDs
+// without a wave, more and shorter runs (down to min_blocks blocks) until
+// there is one wave per SIMD (kBwdFillWaves).  Measured with grad_W: T = 1024,
+// C = 1024 63 -> 14 us, T = 8192 70 -> 40 us; dx alone at T = 1024 16 -> 6 us.
+// Filling two waves per SIMD instead, or rounding large run counts to whole
+// rounds of resident waves, was slower at C = 4096.
+int64_t k1_bwd_nruns(int64_t T, int64_t nC, int64_t max_blocks, int64_t min_blocks) {
+  const int64_t nblocks = (T + 15) / 16;
+  if (nblocks <= 0) return 1;
+  const int64_t nslices = (nC + 127) / 128;
+  const int64_t fill = kBwdFillWaves / nslices > 1 ? kBwdFillWaves / nslices : 1;
+  const int64_t nmin = (nblocks + max_blocks - 1) / max_blocks;
+  int64_t n = nblocks / min_blocks;
+  n = n < fill ? n : fill;
+  return n > nmin ? n : nmin;
+}
+
+template <bool DW, bool EPI = false, bool GI = false>
+void launch_k1_bwd_mfma(hipStream_t s, const uint16_t* x, const uint16_t* W, const uint16_t* go,
+                        const uint16_t* proj, const float* inv_rms, uint16_t* gx, float* partial, int64_t T, int nC,
+                        int nslices, int64_t nruns, const uint16_t* go3 = nullptr, const float* h_pre = nullptr,
+                        int C = 1, const uint16_t* gi = nullptr) {
+  const dim3 grid(blocks_for(nruns * nslices, 4));
   if (nC % 128 == 0)
-    k1_bwd_mfma<NTB, DW, true, EPI, GI><<<grid, 256, 0, s>>>(x, W, go, proj, inv_rms, gx, partial, go3, h_pre,
-                                                             gi, T, nC, nslices, C);
+    k1_bwd_mfma<DW, true, EPI, GI><<<grid, 256, 0, s>>>(x, W, go, proj, inv_rms, gx, partial, go3, h_pre, gi, T,
+                                                        nC, nslices, nruns, C);
   else
-    k1_bwd_mfma<NTB, DW, false, EPI, GI><<<grid, 256, 0, s>>>(x, W, go, proj, inv_rms, gx, partial, go3, h_pre,
-                                                              gi, T, nC, nslices, C);
+    k1_bwd_mfma<DW, false, EPI, GI><<<grid, 256, 0, s>>>(x, W, go, proj, inv_rms, gx, partial, go3, h_pre, gi, T,
+                                                         nC, nslices, nruns, C);
 }
 
 }  // namespace
@@ -873,9 +896,8 @@ extern "C" int fmhc_k1_bwd_dx(const uint16_t* x_flat, const uint16_t* W, const u
   const int nc = static_cast<int>(nC);
   if (k1_bwd_mfma_path(x_flat, W, grad_out, proj_out, grad_x, nC)) {
     const int nslices = static_cast<int>((nC + 127) / 128);
-    const int64_t nruns = (T + 16 * kBwdNTB - 1) / (16 * kBwdNTB);
-    launch_k1_bwd_mfma<kBwdNTB, false>(dim3(blocks_for(nruns * nslices, 4)), s, x_flat, W, grad_out,
-                                       proj_out, inv_rms, grad_x, nullptr, T, nc, nslices);
+    const int64_t nruns = k1_bwd_nruns(T, nC, kBwdNTB, 1);
+    launch_k1_bwd_mfma<false>(s, x_flat, W, grad_out, proj_out, inv_rms, grad_x, nullptr, T, nc, nslices, nruns);
   } else {
     const dim3 grid(blocks_for(T, 4));
     k1_bwd_scalar<false><<<grid, 256, 0, s>>>(x_flat, W, grad_out, proj_out, inv_rms, grad_x, nullptr, T, nc);
@@ -885,7 +907,8 @@ extern "C" int fmhc_k1_bwd_dx(const uint16_t* x_flat, const uint16_t* W, const u
 
 namespace fmhc {
 namespace {
-int64_t k1_bwd_runs(int64_t T) { return ((T + 15) / 16 + kBwdDwNTB - 1) / kBwdDwNTB; }
+// Runs with grad_W fused.
+int64_t k1_bwd_runs(int64_t T, int64_t nC) { return k1_bwd_nruns(T, nC, kBwdDwNTB, kBwdDwMinNTB); }
 }  // namespace
 }  // namespace fmhc
 
@@ -893,7 +916,7 @@ extern "C" int64_t fmhc_k1_bwd_workspace_bytes(int64_t T, int64_t nC) {
   using namespace fmhc;
   if (T <= 0 || nC <= 0 || nC % 8 != 0 || nC > (int64_t{1} << 26)) return 0;  // no MFMA path: no workspace
   const int64_t nslices = (nC + 127) / 128;
-  return k1_bwd_runs(T) * nslices * (8 * 2 * 4 * kWave) * static_cast<int64_t>(sizeof(float));
+  return k1_bwd_runs(T, nC) * nslices * (8 * 2 * 4 * kWave) * static_cast<int64_t>(sizeof(float));
 }
 
 extern "C" int fmhc_k1_bwd(const uint16_t* x_flat, const uint16_t* W, const uint16_t* grad_out,
@@ -914,10 +937,9 @@ extern "C" int fmhc_k1_bwd(const uint16_t* x_flat, const uint16_t* W, const uint
     const int64_t need = fmhc_k1_bwd_workspace_bytes(T, nC);
     if (!workspace || workspace_bytes < need || !aligned16(workspace)) return FMHC_ERR_INVALID_ARGUMENT;
     const int nslices = static_cast<int>((nC + 127) / 128);
-    const int64_t nruns = k1_bwd_runs(T);
+    const int64_t nruns = k1_bwd_runs(T, nC);
     float* partial = static_cast<float*>(workspace);
-    launch_k1_bwd_mfma<kBwdDwNTB, true>(dim3(blocks_for(nruns * nslices, 4)), s, x_flat, W, grad_out,
-                                        proj_out, inv_rms, grad_x, partial, T, nc, nslices);
+    launch_k1_bwd_mfma<true>(s, x_flat, W, grad_out, proj_out, inv_rms, grad_x, partial, T, nc, nslices, nruns);
     const int st = launch_status();
     if (st != FMHC_OK) return st;
     const int64_t per_part = static_cast<int64_t>(nslices) * (8 * 2 * 4 * kWave);
@@ -969,16 +991,14 @@ int k1_bwd_premap(const uint16_t* x_flat, const uint16_t* W, const uint16_t* gra
     if (!workspace || workspace_bytes < fmhc_k1_bwd_workspace_bytes(T, nC) || !aligned16(workspace))
       return FMHC_ERR_INVALID_ARGUMENT;
     const int nslices = static_cast<int>((nC + 127) / 128);
-    const int64_t nruns = k1_bwd_runs(T);
+    const int64_t nruns = k1_bwd_runs(T, nC);
     float* partial = static_cast<float*>(workspace);
-    const dim3 grid(blocks_for(nruns * nslices, 4));
     if (grad_x_in)
-      launch_k1_bwd_mfma<kBwdDwNTB, true, true, true>(grid, s, x_flat, W, grad_proj, proj, inv_rms, grad_x,
-                                                      partial, T, nc, nslices, go3, h_pre, static_cast<int>(C),
-                                                      grad_x_in);
+      launch_k1_bwd_mfma<true, true, true>(s, x_flat, W, grad_proj, proj, inv_rms, grad_x, partial, T, nc, nslices,
+                                           nruns, go3, h_pre, static_cast<int>(C), grad_x_in);
     else
-      launch_k1_bwd_mfma<kBwdDwNTB, true, true>(grid, s, x_flat, W, grad_proj, proj, inv_rms, grad_x, partial,
-                                                T, nc, nslices, go3, h_pre, static_cast<int>(C));
+      launch_k1_bwd_mfma<true, true>(s, x_flat, W, grad_proj, proj, inv_rms, grad_x, partial, T, nc, nslices,
+                                     nruns, go3, h_pre, static_cast<int>(C));
     const int st = launch_status();
     if (st != FMHC_OK) return st;
     const int64_t per_part = static_cast<int64_t>(nslices) * (8 * 2 * 4 * kWave);
