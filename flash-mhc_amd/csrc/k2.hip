@@ -33,9 +33,10 @@ constexpr int64_t kK2SmallT = 4096;  // forward: 32 lanes per token up to this m
 template <bool VEC>
 __global__ __launch_bounds__(kK2Threads) void k2_fwd_kernel(
     const uint16_t* __restrict__ proj, const K2Params P, float* __restrict__ h_pre,
-    float* __restrict__ h_post, float* __restrict__ H, int64_t T) {
+    float* __restrict__ h_post, float* __restrict__ H, int64_t T, const ZeroWords z) {
 #pragma clang fp contract(off)
   __shared__ K2Smem sm;
+  zero_words(z);
   stage_params<kK2Threads>(P, sm);
   const int64_t t = static_cast<int64_t>(blockIdx.x) * kK2Threads + threadIdx.x;
   if (t >= T) return;
@@ -62,9 +63,10 @@ __global__ __launch_bounds__(kK2Threads) void k2_fwd_kernel(
 // results are bit-identical to k2_fwd_kernel's.
 __global__ __launch_bounds__(kK2Threads) void k2_fwd_small(const uint16_t* __restrict__ proj, const K2Params P,
                                                           float* __restrict__ h_pre, float* __restrict__ h_post,
-                                                          float* __restrict__ H, int64_t T) {
+                                                          float* __restrict__ H, int64_t T, const ZeroWords z) {
 #pragma clang fp contract(off)
   __shared__ K2Smem sm;
+  zero_words(z);
   stage_params<kK2Threads>(P, sm);
   const int q = threadIdx.x & 31;
   const int64_t t = static_cast<int64_t>(blockIdx.x) * (kK2Threads / 32) + (threadIdx.x >> 5);
@@ -207,15 +209,32 @@ __global__ __launch_bounds__(kWave) void k2_param_reduce(const float* __restrict
 
 bool k2_bad(int64_t T, int64_t n) { return T < 0 || n != kN; }
 
+int64_t k2_blocks(int64_t T) { return (T + kK2Threads - 1) / kK2Threads; }
+
+}  // namespace
+
 bool k2_params(const void* ap, const void* apo, const void* ar, const void* bias, const void* perm, int dtype,
                K2Params& P) {
   if (!ap || !apo || !ar || !bias || !perm || (dtype != FMHC_PARAM_F32 && dtype != FMHC_PARAM_BF16)) return false;
   P = K2Params{ap, apo, ar, bias, perm, dtype == FMHC_PARAM_BF16};
   return true;
 }
-int64_t k2_blocks(int64_t T) { return (T + kK2Threads - 1) / kK2Threads; }
 
-}  // namespace
+int k2_fwd_launch(const uint16_t* proj, const K2Params& P, float* h_pre, float* h_post, float* H_merged, int64_t T,
+                  ZeroWords z, hipStream_t s) {
+  if (T <= kK2SmallT) {
+    k2_fwd_small<<<dim3(static_cast<unsigned>((T + 7) / 8)), kK2Threads, 0, s>>>(proj, P, h_pre, h_post,
+                                                                                H_merged, T, z);
+    return launch_status();
+  }
+  const dim3 grid(static_cast<unsigned>(k2_blocks(T)));
+  if (aligned16(proj))
+    k2_fwd_kernel<true><<<grid, kK2Threads, 0, s>>>(proj, P, h_pre, h_post, H_merged, T, z);
+  else
+    k2_fwd_kernel<false><<<grid, kK2Threads, 0, s>>>(proj, P, h_pre, h_post, H_merged, T, z);
+  return launch_status();
+}
+
 }  // namespace fmhc
 
 extern "C" int fmhc_k2_fwd(const uint16_t* proj, const void* alpha_pre, const void* alpha_post,
@@ -229,18 +248,7 @@ extern "C" int fmhc_k2_fwd(const uint16_t* proj, const void* alpha_pre, const vo
   if (T == 0) return FMHC_OK;
   if (!proj || !h_pre || !h_post || !H_merged) return FMHC_ERR_INVALID_ARGUMENT;
   if (!aligned16(h_pre) || !aligned16(h_post) || !aligned16(H_merged)) return FMHC_ERR_INVALID_ARGUMENT;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (T <= kK2SmallT) {
-    k2_fwd_small<<<dim3(static_cast<unsigned>((T + 7) / 8)), kK2Threads, 0, s>>>(proj, P, h_pre, h_post,
-                                                                                H_merged, T);
-    return launch_status();
-  }
-  const dim3 grid(static_cast<unsigned>(k2_blocks(T)));
-  if (aligned16(proj))
-    k2_fwd_kernel<true><<<grid, kK2Threads, 0, s>>>(proj, P, h_pre, h_post, H_merged, T);
-  else
-    k2_fwd_kernel<false><<<grid, kK2Threads, 0, s>>>(proj, P, h_pre, h_post, H_merged, T);
-  return launch_status();
+  return k2_fwd_launch(proj, P, h_pre, h_post, H_merged, T, ZeroWords{}, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int64_t fmhc_k2_bwd_workspace_bytes(int64_t T) {

@@ -26,6 +26,21 @@ struct K2Params {
   bool bf16;
 };
 
+// Up to two 16-bit words a forward launch also sets to zero (the pre-map
+// ops' zero-stride gradient placeholders, whose one stored element would
+// otherwise need a fill kernel of its own); null pointers are skipped.
+struct ZeroWords {
+  uint16_t* a = nullptr;
+  uint16_t* b = nullptr;
+};
+
+__device__ __forceinline__ void zero_words(const ZeroWords& z) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    if (z.a) *z.a = 0;
+    if (z.b) *z.b = 0;
+  }
+}
+
 __device__ __forceinline__ float ld_param(const void* p, int i, bool bf16) {
   return bf16 ? bf16_to_f32(static_cast<const uint16_t*>(p)[i]) : static_cast<const float*>(p)[i];
 }
@@ -166,5 +181,12 @@ __device__ __forceinline__ void k2_token32(const K2Smem& sm, float p, int q, int
   else if (q < 2 * kN)
     h_post[t * kN + (q - kN)] = hq;
 }
+
+// K2 forward for T tokens (k2.hip), also zeroing z: fmhc_k2_fwd's launch
+// after its checks.  k2_params validates and packs the parameters.
+bool k2_params(const void* ap, const void* apo, const void* ar, const void* bias, const void* perm, int dtype,
+               K2Params& P);
+int k2_fwd_launch(const uint16_t* proj, const K2Params& P, float* h_pre, float* h_post, float* H_merged, int64_t T,
+                  ZeroWords z, hipStream_t s);
 
 }  // namespace fmhc

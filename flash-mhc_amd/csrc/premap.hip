@@ -48,8 +48,9 @@ constexpr int kFinishThreads = 256;  // 8 tokens of 32 lanes
 __global__ __launch_bounds__(kFinishThreads) void k1_finish_k2(
     const float* __restrict__ part, int S, int nC, const K2Params P, uint16_t* __restrict__ proj,
     float* __restrict__ inv_rms, float* __restrict__ h_pre, float* __restrict__ h_post, float* __restrict__ H,
-    int64_t T) {
+    int64_t T, const ZeroWords z) {
   __shared__ K2Smem sm;
+  zero_words(z);
   stage_params<kFinishThreads>(P, sm);
   const int q = threadIdx.x & 31;
   const int64_t t = static_cast<int64_t>(blockIdx.x) * (kFinishThreads / 32) + (threadIdx.x >> 5);
@@ -110,29 +111,30 @@ extern "C" int fmhc_premap_fwd(const uint16_t* x, const uint16_t* W, const void*
                                const void* alpha_post, const void* alpha_res, const void* bias,
                                const void* perm, int param_dtype, uint16_t* layer_input, uint16_t* proj,
                                float* inv_rms, float* h_pre, float* h_post, float* H_merged,
-                               void* workspace, int64_t workspace_bytes, int64_t T, int64_t C, int64_t n,
-                               void* stream) {
+                               uint16_t* zero_word_a, uint16_t* zero_word_b, void* workspace,
+                               int64_t workspace_bytes, int64_t T, int64_t C, int64_t n, void* stream) {
   if (T < 0 || C <= 0 || n != 4 || !param_dtype_ok(param_dtype)) return FMHC_ERR_INVALID_ARGUMENT;
   if (T == 0) return FMHC_OK;
   if (!x || !W || !alpha_pre || !alpha_post || !alpha_res || !bias || !perm || !proj || !inv_rms || !h_pre ||
       !h_post || !H_merged)
     return FMHC_ERR_INVALID_ARGUMENT;
   if (!aligned16(h_pre) || !aligned16(h_post) || !aligned16(H_merged)) return FMHC_ERR_INVALID_ARGUMENT;
+  fmhc::K2Params P;
+  if (!fmhc::k2_params(alpha_pre, alpha_post, alpha_res, bias, perm, param_dtype, P))
+    return FMHC_ERR_INVALID_ARGUMENT;
+  const fmhc::ZeroWords z{zero_word_a, zero_word_b};
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int S = fmhc::k1_fwd_partials(x, W, workspace, workspace_bytes, T, n * C, s);
   if (S < 0) return -S;
   int st = FMHC_OK;
   if (S >= 2) {
-    const fmhc::K2Params P{alpha_pre, alpha_post, alpha_res, bias, perm, param_dtype == FMHC_PARAM_BF16};
     k1_finish_k2<<<dim3(static_cast<unsigned>((T + 7) / 8)), kFinishThreads, 0, s>>>(
         static_cast<const float*>(workspace), S, static_cast<int>(n * C), P, proj, inv_rms, h_pre, h_post,
-        H_merged, T);
+        H_merged, T, z);
     st = fmhc::launch_status();
   } else {
     st = fmhc_k1_fwd_ws(x, W, proj, inv_rms, workspace, workspace_bytes, T, n * C, 32, stream);
-    if (st == FMHC_OK)
-      st = fmhc_k2_fwd(proj, alpha_pre, alpha_post, alpha_res, bias, perm, param_dtype, h_pre, h_post, H_merged,
-                       T, n, stream);
+    if (st == FMHC_OK) st = fmhc::k2_fwd_launch(proj, P, h_pre, h_post, H_merged, T, z, s);
   }
   if (st == FMHC_OK && layer_input) st = fmhc_k3_fwd(x, h_pre, layer_input, T, C, n, stream);
   return st;

@@ -35,7 +35,7 @@ SIGNATURES: dict[str, list] = {
     "fmhc_k2_fwd": [_P] * 6 + [_INT] + [_P] * 3 + [_I64, _I64, _P],
     "fmhc_k2_bwd": [_P] * 6 + [_INT] + [_P] * 9 + [_I64, _I64, _I64, _P],
     "fmhc_k2_bwd_workspace_bytes": [_I64],
-    "fmhc_premap_fwd": [_P] * 7 + [_INT] + [_P] * 7 + [_I64, _I64, _I64, _I64, _P],
+    "fmhc_premap_fwd": [_P] * 7 + [_INT] + [_P] * 9 + [_I64, _I64, _I64, _I64, _P],
     "fmhc_premap_fwd_workspace_bytes": [_I64, _I64],
     "fmhc_premap_bwd": [_P] * 7 + [_INT] + [_P] * 14 + [_I64, _I64, _I64, _I64, _P],
     "fmhc_premap_bwd_workspace_bytes": [_I64, _I64],
@@ -56,7 +56,7 @@ RESTYPES = {
     "fmhc_premap_bwd_workspace_bytes": ctypes.c_int64,
 }
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

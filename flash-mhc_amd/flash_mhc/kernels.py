@@ -240,10 +240,15 @@ def k2_bwd(proj: torch.Tensor, alpha_pre: torch.Tensor, alpha_post: torch.Tensor
 
 def premap_fwd(x_streams: torch.Tensor, W: torch.Tensor, alpha_pre: torch.Tensor,
                alpha_post: torch.Tensor, alpha_res: torch.Tensor, bias: torch.Tensor,
-               perm: torch.Tensor, layer_input: bool = True):
+               perm: torch.Tensor, layer_input: bool = True, zero: tuple = ()):
     """K1 + K2 + K3: (layer_input (T,C) bf16, H_merged (T,4,4), h_post (T,4),
     h_pre (T,4) fp32, proj (T,32) bf16, inv_rms (T,) fp32).  layer_input=False:
-    K1 + K2 only, the first output is None."""
+    K1 + K2 only, the first output is None.  zero: up to two 16-bit tensors
+    whose first stored element the same launches set to zero (zero-stride
+    placeholders; empty ones are skipped)."""
+    if len(zero) > 2 or any(z.element_size() != 2 for z in zero):
+        raise ValueError("premap_fwd: zero takes up to two 16-bit tensors")
+    zw = [z.data_ptr() if z.numel() > 0 else None for z in zero] + [None, None]
     T, n, C = _streams_shape(x_streams)
     dev = _device_of(x_streams)
     _require(x_streams, "x_streams", _BF16, (T, n, C), dev)
@@ -261,8 +266,9 @@ def premap_fwd(x_streams: torch.Tensor, W: torch.Tensor, alpha_pre: torch.Tensor
         st = lib.fmhc_premap_fwd(x_streams.data_ptr(), W.data_ptr(), alpha_pre.data_ptr(),
                                  alpha_post.data_ptr(), alpha_res.data_ptr(), bias.data_ptr(),
                                  perm.data_ptr(), pdt, _ptr_or_none(li), proj.data_ptr(), inv.data_ptr(),
-                                 h_pre.data_ptr(), h_post.data_ptr(), H.data_ptr(), _ptr_or_none(ws),
-                                 0 if ws is None else ws.numel(), T, C, n, _abi.stream_of(x_streams))
+                                 h_pre.data_ptr(), h_post.data_ptr(), H.data_ptr(), zw[0], zw[1],
+                                 _ptr_or_none(ws), 0 if ws is None else ws.numel(), T, C, n,
+                                 _abi.stream_of(x_streams))
     _abi.check(st, "premap_fwd")
     return li, H, h_post, h_pre, proj, inv
 

@@ -175,19 +175,6 @@ def x_sink_like(x_streams: torch.Tensor) -> torch.Tensor:
     return x_streams.new_empty_strided(tuple(x_streams.shape), (0,) * x_streams.dim())
 
 
-def _zero_sink(sink: torch.Tensor) -> torch.Tensor:
-    """Set a zero-stride placeholder's one element to zero (a one-element
-    fill, not numel); an empty one has no storage to fill."""
-    if sink.numel() > 0:
-        sink.as_strided((1,), (1,)).zero_()
-    return sink
-
-
-def _x_sink(x_streams: torch.Tensor) -> torch.Tensor:
-    """mhc_pre_map's x_sink, its element zeroed."""
-    return _zero_sink(x_sink_like(x_streams))
-
-
 @torch.library.register_fake("flash_mhc::mhc_pre_map")
 def _mhc_pre_map_fake(x_streams, W, alpha_pre, alpha_post, alpha_res, bias, perm_mat):
     T, n, C = x_streams.shape
@@ -327,21 +314,24 @@ def _mhc_coefficients_backward_cuda(grad_h_pre, grad_h_post, grad_H_merged, proj
 def _mhc_pre_map_cuda(x_streams, W, alpha_pre, alpha_post, alpha_res, bias, perm_mat):
     _check_n4(x_streams, "flash_mhc::mhc_pre_map supports n=4 only")
     _check_k2(x_streams.new_empty((0, W.shape[0])), perm_mat)
+    # The sink's one element is zeroed by the same launches (no fill kernel).
+    x_sink = x_sink_like(x_streams)
     outs = _k.premap_fwd(x_streams.contiguous(), W.to(x_streams.dtype).contiguous(),
-                         *_params(alpha_pre, alpha_post, alpha_res, bias, perm_mat))
-    return (*outs, _x_sink(x_streams))
+                         *_params(alpha_pre, alpha_post, alpha_res, bias, perm_mat), zero=(x_sink,))
+    return (*outs, x_sink)
 
 
 @torch.library.impl(_lib, "mhc_pre_map_coeffs", "CUDA")
 def _mhc_pre_map_coeffs_cuda(x_streams, W, alpha_pre, alpha_post, alpha_res, bias, perm_mat):
     _check_n4(x_streams, "flash_mhc::mhc_pre_map_coeffs supports n=4 only")
     _check_k2(x_streams.new_empty((0, W.shape[0])), perm_mat)
+    T, n, C = x_streams.shape
+    x_sink = x_sink_like(x_streams)
+    li_sink = x_streams.new_empty_strided((T, C), (0, 0))
     _li, H, h_post, h_pre, proj, inv = _k.premap_fwd(
         x_streams.contiguous(), W.to(x_streams.dtype).contiguous(),
-        *_params(alpha_pre, alpha_post, alpha_res, bias, perm_mat), layer_input=False)
-    T, n, C = x_streams.shape
-    li_sink = _zero_sink(x_streams.new_empty_strided((T, C), (0, 0)))
-    return H, h_post, h_pre, proj, inv, _x_sink(x_streams), li_sink
+        *_params(alpha_pre, alpha_post, alpha_res, bias, perm_mat), layer_input=False, zero=(x_sink, li_sink))
+    return H, h_post, h_pre, proj, inv, x_sink, li_sink
 
 
 @torch.library.impl(_lib, "mhc_pre_map_mix", "CUDA")

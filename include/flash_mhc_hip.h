@@ -35,7 +35,7 @@ extern "C" {
 #define FMHC_ERR_INVALID_ARGUMENT 1 /* negative size, n != 4, D_out != 32, null pointer */
 #define FMHC_ERR_HIP_BASE 1000      /* + hipError_t from the launch */
 
-#define FMHC_ABI_VERSION 5
+#define FMHC_ABI_VERSION 6
 
 /* Storage dtype of the block parameters K2 reads (alpha_pre, alpha_post,
  * alpha_res, bias, perm: all five the same) and of their gradients. */
@@ -131,13 +131,16 @@ int64_t fmhc_k2_bwd_workspace_bytes(int64_t T);
  * H_merged (T, 4, 4) fp32 (16-byte aligned).  x (T, n, C) bf16, W (32, n C)
  * bf16, alphas / bias / perm / param_dtype as fmhc_k2_fwd; n must be 4.
  * layer_input may be NULL: K1 and K2 only (the coefficients), K3 skipped.
+ * zero_word_a, zero_word_b: NULL, or 16-bit words the call also sets to zero
+ * (inside K2's launch, for T > 0): the single stored element of a caller's
+ * zero-stride placeholder tensor, which would otherwise need a fill of its own.
  * Replaces: src/flash_mhc/block.py:157-177 (_mhc_pre_map_triton: the K1 launch,
  *           the K2 PyTorch ops and the K3 launch). */
 int fmhc_premap_fwd(const uint16_t* x, const uint16_t* W, const void* alpha_pre,
                     const void* alpha_post, const void* alpha_res, const void* bias,
                     const void* perm, int param_dtype, uint16_t* layer_input, uint16_t* proj,
-                    float* inv_rms,
-                    float* h_pre, float* h_post, float* H_merged, void* workspace,
+                    float* inv_rms, float* h_pre, float* h_post, float* H_merged,
+                    uint16_t* zero_word_a, uint16_t* zero_word_b, void* workspace,
                     int64_t workspace_bytes, int64_t T, int64_t C, int64_t n, void* stream);
 /* Workspace bytes fmhc_premap_fwd needs (fmhc_k1_fwd_workspace_bytes(T, 4 C);
  * 0: workspace may be NULL).  No counterpart in the reference. */

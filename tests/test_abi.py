@@ -75,7 +75,7 @@ _FAKE = 4096  # a non-null address that the host-side checks never dereference
         # K2 parameter dtype other than FMHC_PARAM_F32 (0) / FMHC_PARAM_BF16 (1)
         lambda L: L.fmhc_k2_fwd(*[_FAKE] * 6, 2, *[_FAKE] * 3, 8, 4, None),
         lambda L: L.fmhc_k2_fwd(*[None] * 6, 0, *[None] * 3, 8, 4, None),  # null parameters
-        lambda L: L.fmhc_premap_fwd(*[_FAKE] * 7, -1, *[_FAKE] * 6, None, 0, 8, 16, 4, None),
+        lambda L: L.fmhc_premap_fwd(*[_FAKE] * 7, -1, *[_FAKE] * 6, None, None, None, 0, 8, 16, 4, None),
     ],
 )
 def test_invalid_arguments_rejected_before_launch(call):

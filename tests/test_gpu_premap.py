@@ -81,6 +81,27 @@ def test_premap_matches_three_kernels(T, C):
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("T,C", [(1, 4096), (300, 1024), (8192, 256)])
+def test_premap_ops_zero_their_sinks(T, C):
+    """mhc_pre_map and mhc_pre_map_coeffs return zero-stride gradient sinks
+    whose one stored element the pre-map launches set to zero (no fill kernel
+    of their own): zero even when the allocator hands out memory that held
+    other values (few tokens: K1's split path; T = 8192: the one-pass path)."""
+    x = randn((T, 4, C), 11).to(DEV)
+    W = randn((32, 4 * C), 12, 0.02).to(DEV)
+    p = [t.to(DEV) for t in (*_params(13), PERM)]
+    for _ in range(2):
+        junk = torch.full((1 << 16,), -3.0, device=DEV, dtype=BF16)  # dirty blocks for the next allocations
+        del junk
+        x_sink = torch.ops.flash_mhc.mhc_pre_map(x, W, *p)[-1]
+        outs = torch.ops.flash_mhc.mhc_pre_map_coeffs(x, W, *p)
+        torch.cuda.synchronize()
+        for name, sink, shape in (("mhc_pre_map x_sink", x_sink, (T, 4, C)),
+                                  ("coeffs x_sink", outs[-2], (T, 4, C)), ("coeffs li_sink", outs[-1], (T, C))):
+            assert tuple(sink.shape) == shape and all(st == 0 for st in sink.stride()), name
+            assert float(sink.as_strided((1,), (1,)).float().item()) == 0.0, name
+
+
 def _block_run(flag, T, C, ckpt=False, seed=80):
     old = os.environ.get("FLASH_MHC_FUSED_PREMAP")
     os.environ["FLASH_MHC_FUSED_PREMAP"] = flag
