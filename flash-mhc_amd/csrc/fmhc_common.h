@@ -120,6 +120,35 @@ struct Lanes<1> {
   }
 };
 
+// K3 forward of one token: out[c] = bf16(h0 x0[c] + h1 x1[c] + h2 x2[c] +
+// h3 x3[c]), the products added in stream order with fused multiply-adds;
+// element groups g = first, first + step, ... below C / VEC.  Shared by the
+// K3 kernel and the pre-map's few-token kernel, which must agree bit for bit.
+template <int VEC>
+__device__ __forceinline__ void k3_token(const uint16_t* __restrict__ x0, const float h[4],
+                                         uint16_t* __restrict__ orow, int first, int step, int C) {
+  const uint16_t* x1 = x0 + C;
+  const uint16_t* x2 = x1 + C;
+  const uint16_t* x3 = x2 + C;
+  const int ng = C / VEC;
+#pragma unroll 2
+  for (int g = first; g < ng; g += step) {
+    float a[VEC], b[VEC], c[VEC], d[VEC], o[VEC];
+    Lanes<VEC>::load(x0, g, a);
+    Lanes<VEC>::load(x1, g, b);
+    Lanes<VEC>::load(x2, g, c);
+    Lanes<VEC>::load(x3, g, d);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      float acc = h[0] * a[e];
+      acc = __builtin_fmaf(h[1], b[e], acc);
+      acc = __builtin_fmaf(h[2], c[e], acc);
+      o[e] = __builtin_fmaf(h[3], d[e], acc);
+    }
+    Lanes<VEC>::store(orow, g, o);
+  }
+}
+
 // Sum over the LPT consecutive lanes that share one token (LPT a power of
 // two <= 64).  Every lane of the group receives the total.
 template <int LPT>

@@ -51,32 +51,9 @@ __global__ __launch_bounds__(kBlock) void k3_fwd_kernel(const uint16_t* __restri
   const int64_t tok = token_of_lane<LPT>(lane);
   if (tok >= T) return;
   const int sub = sub_of_lane<LPT>();
-  const int ng = C / VEC;
-
   const float* hp = h_pre + tok * 4;
-  const float h0 = hp[0], h1 = hp[1], h2 = hp[2], h3 = hp[3];
-  const uint16_t* x0 = x + tok * 4 * C;
-  const uint16_t* x1 = x0 + C;
-  const uint16_t* x2 = x1 + C;
-  const uint16_t* x3 = x2 + C;
-  uint16_t* orow = out + tok * C;
-
-#pragma unroll 2
-  for (int g = sub; g < ng; g += LPT) {
-    float a[VEC], b[VEC], c[VEC], d[VEC], o[VEC];
-    Lanes<VEC>::load(x0, g, a);
-    Lanes<VEC>::load(x1, g, b);
-    Lanes<VEC>::load(x2, g, c);
-    Lanes<VEC>::load(x3, g, d);
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      float acc = h0 * a[e];
-      acc = __builtin_fmaf(h1, b[e], acc);
-      acc = __builtin_fmaf(h2, c[e], acc);
-      o[e] = __builtin_fmaf(h3, d[e], acc);
-    }
-    Lanes<VEC>::store(orow, g, o);
-  }
+  const float h[4] = {hp[0], hp[1], hp[2], hp[3]};
+  k3_token<VEC>(x + tok * 4 * C, h, out + tok * C, sub, LPT, C);
 }
 
 // GX = false: grad_h_pre only (the pre-map backward adds h_pre * go into K1's

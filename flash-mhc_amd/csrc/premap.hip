@@ -45,18 +45,12 @@ constexpr int kFinishThreads = 256;  // 8 tokens of 32 lanes
 // in split order (as k1_fwd_finish does), stores proj[t, q] =
 // bf16(sum * inv_rms) and inv_rms, then runs K2 on that bf16 value
 // (k2_token32): the same values as K1's finish kernel followed by K2.
-__global__ __launch_bounds__(kFinishThreads) void k1_finish_k2(
-    const float* __restrict__ part, int S, int nC, const K2Params P, uint16_t* __restrict__ proj,
-    float* __restrict__ inv_rms, float* __restrict__ h_pre, float* __restrict__ h_post, float* __restrict__ H,
-    int64_t T, const ZeroWords z) {
-  __shared__ K2Smem sm;
-  zero_words(z);
-  stage_params<kFinishThreads>(P, sm);
-  const int q = threadIdx.x & 31;
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * (kFinishThreads / 32) + (threadIdx.x >> 5);
-  if (t >= T) return;  // a whole 32-lane group leaves together
-  // Projection q and the sum of squares, each added over the S partials in
-  // split order; the loads of both run ahead together.
+// K1's second stage for token t in 32 lanes: lane q adds the S partials of
+// projection q and of the sum of squares in split order, stores proj[t, q]
+// and (lane 0) inv_rms[t], and returns the stored bf16 projection as fp32.
+__device__ __forceinline__ float finish_token32(const float* __restrict__ part, int S, int nC, int q, int64_t t,
+                                                uint16_t* __restrict__ proj, float* __restrict__ inv_rms) {
+  // The loads of both sums run ahead together.
   const int s4 = (S + 3) & ~3;
   const f32x4* pv = reinterpret_cast<const f32x4*>(part + (t * (kDk + 1) + q) * s4);
   const f32x4* ps = reinterpret_cast<const f32x4*>(part + (t * (kDk + 1) + kDk) * s4);
@@ -83,7 +77,45 @@ __global__ __launch_bounds__(kFinishThreads) void k1_finish_k2(
   const uint16_t pj = f32_to_bf16(v * inv);
   proj[t * kDk + q] = pj;
   if (q == 0) inv_rms[t] = inv;
-  k2_token32(sm, bf16_to_f32(pj), q, t, h_pre, h_post, H);
+  return bf16_to_f32(pj);
+}
+
+__global__ __launch_bounds__(kFinishThreads) void k1_finish_k2(
+    const float* __restrict__ part, int S, int nC, const K2Params P, uint16_t* __restrict__ proj,
+    float* __restrict__ inv_rms, float* __restrict__ h_pre, float* __restrict__ h_post, float* __restrict__ H,
+    int64_t T, const ZeroWords z) {
+  __shared__ K2Smem sm;
+  zero_words(z);
+  stage_params<kFinishThreads>(P, sm);
+  const int q = threadIdx.x & 31;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * (kFinishThreads / 32) + (threadIdx.x >> 5);
+  if (t >= T) return;  // a whole 32-lane group leaves together
+  const float p = finish_token32(part, S, nC, q, t, proj, inv_rms);
+  k2_token32(sm, p, q, t, h_pre, h_post, H);
+}
+
+// The same with K3 fused, one token per workgroup (blockIdx.x): its first 32
+// lanes finish K1 and run K2; after the barrier all 256 lanes mix the token's
+// streams into layer_input with h_pre as written (k3_token, so the values are
+// those of the separate K3 kernel).  Saves K3's launch for few tokens.
+template <int VEC>
+__global__ __launch_bounds__(kFinishThreads) void k1_finish_k2_k3(
+    const float* __restrict__ part, int S, int nC, const K2Params P, uint16_t* __restrict__ proj,
+    float* __restrict__ inv_rms, float* __restrict__ h_pre, float* __restrict__ h_post, float* __restrict__ H,
+    const ZeroWords z, const uint16_t* __restrict__ x, uint16_t* __restrict__ layer_input, int C) {
+  __shared__ K2Smem sm;
+  zero_words(z);
+  stage_params<kFinishThreads>(P, sm);
+  const int64_t t = blockIdx.x;
+  if (threadIdx.x < 32) {
+    const int q = static_cast<int>(threadIdx.x);
+    const float p = finish_token32(part, S, nC, q, t, proj, inv_rms);
+    k2_token32(sm, p, q, t, h_pre, h_post, H);
+  }
+  __syncthreads();  // h_pre[t] written by this workgroup's first lanes
+  const float* hp = h_pre + t * 4;
+  const float h[4] = {hp[0], hp[1], hp[2], hp[3]};
+  k3_token<VEC>(x + t * 4 * C, h, layer_input + t * C, static_cast<int>(threadIdx.x), kFinishThreads, C);
 }
 
 struct PremapWs {
@@ -127,10 +159,22 @@ extern "C" int fmhc_premap_fwd(const uint16_t* x, const uint16_t* W, const void*
   const int S = fmhc::k1_fwd_partials(x, W, workspace, workspace_bytes, T, n * C, s);
   if (S < 0) return -S;
   int st = FMHC_OK;
+  const float* part = static_cast<const float*>(workspace);
+  const int nc = static_cast<int>(n * C);
+  if (S >= 2 && layer_input) {
+    const dim3 grid(static_cast<unsigned>(T));
+    const int c = static_cast<int>(C);
+    if (C % 8 == 0 && aligned16(x) && aligned16(layer_input))
+      k1_finish_k2_k3<8><<<grid, kFinishThreads, 0, s>>>(part, S, nc, P, proj, inv_rms, h_pre, h_post, H_merged,
+                                                          z, x, layer_input, c);
+    else
+      k1_finish_k2_k3<1><<<grid, kFinishThreads, 0, s>>>(part, S, nc, P, proj, inv_rms, h_pre, h_post, H_merged,
+                                                          z, x, layer_input, c);
+    return fmhc::launch_status();
+  }
   if (S >= 2) {
     k1_finish_k2<<<dim3(static_cast<unsigned>((T + 7) / 8)), kFinishThreads, 0, s>>>(
-        static_cast<const float*>(workspace), S, static_cast<int>(n * C), P, proj, inv_rms, h_pre, h_post,
-        H_merged, T, z);
+        part, S, nc, P, proj, inv_rms, h_pre, h_post, H_merged, T, z);
     st = fmhc::launch_status();
   } else {
     st = fmhc_k1_fwd_ws(x, W, proj, inv_rms, workspace, workspace_bytes, T, n * C, 32, stream);
