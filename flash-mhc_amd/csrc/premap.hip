@@ -13,13 +13,14 @@
 //
 // Forward: K1 -> K2 -> K3, the three kernels of k1.hip, k2.hip, k3.hip.  For
 // few tokens K1 is split over the columns (partial sums in the caller's
-// workspace), and its second stage runs inside the K2 kernel (k1_finish_k2).  A
+// workspace), and its second stage runs inside the K2 kernel (k1_finish_k2;
+// with K3 too when the layer input is wanted, k1_finish_k2_k3).  A
 // one-pass variant that kept each token tile of x in LDS between K1 and K3
 // (saving K3's read of x) was built and measured slower on gfx950 at
 // C <= 1024: with tiles of 8-16 tokens every tile re-reads the whole of W
 // (32 x nC) from L2, and holding a wave's share of W in registers instead
 // does not fit beside the tile pipeline (register spills), whereas K1
-// amortises W over 128 tokens per workgroup.
+// amortises W over 64 tokens per workgroup.
 
 #include <hip/hip_runtime.h>
 
