@@ -17,8 +17,9 @@ MHCLiteBlock forward + backward with the fused path vs the reference's rules,
 and the eval-mode forward latency of the inference shapes (C=4096,
 T = 1, 64, 257, 65537; eager and HIP-graph replay).
 ``cpu_baseline`` times the reference's PyTorch formulation of the same six ops
-(fp32 autograd, restated in oracle/) on the host's cores, on a bounded token
-sample, reported with the same bytes model.
+(fp32 autograd, restated in oracle/) on the host's cores, by default on the
+whole workload (--cpu-tokens, --cpu-iters bound it), reported with the same
+bytes model.
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--T 65536] [--C 1024]
 """
@@ -405,7 +406,9 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--T", type=int, default=65536)
     ap.add_argument("--C", type=int, default=1024)
-    ap.add_argument("--cpu-tokens", type=int, default=8192)
+    ap.add_argument("--cpu-tokens", type=int, default=65536,
+                    help="tokens of the CPU baseline's sample (default: the whole metric workload)")
+    ap.add_argument("--cpu-iters", type=int, default=10, help="timed passes of the CPU baseline (median)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the K1-backward and block-step fields (profiler runs: only the six kernels)")
@@ -557,7 +560,7 @@ def main() -> None:
     del inp, launch
     torch.cuda.empty_cache()
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(C, args.cpu_tokens)
+        line["cpu_baseline"] = cpu_baseline(C, args.cpu_tokens, args.cpu_iters)
     print(json.dumps(line), flush=True)
 
 
