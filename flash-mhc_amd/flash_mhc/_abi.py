@@ -121,6 +121,12 @@ def ptr(t: torch.Tensor) -> int:
     return t.data_ptr()
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(t: torch.Tensor) -> int:
-    """hipStream_t of torch's current stream on ``t``'s device."""
+    """hipStream_t of torch's current stream on ``t``'s device (the raw handle
+    query avoids building a Stream object per launch)."""
+    if _raw_stream is not None:
+        return _raw_stream(t.get_device())
     return torch.cuda.current_stream(t.device).cuda_stream

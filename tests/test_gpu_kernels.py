@@ -366,8 +366,12 @@ def test_deterministic_and_stream_aware():
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
+        from flash_mhc import _abi
+
+        assert _abi.stream_of(args[0]) == s.cuda_stream  # launches go to the current stream
         c = K.k4_bwd(*args)
         p2 = K.k1_fwd(args[1].view(T, -1), W.to(DEV))
+    assert _abi.stream_of(args[0]) == torch.cuda.current_stream().cuda_stream
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     for u, v, w in zip(a, b, c):
