@@ -13,7 +13,8 @@ launch; ``roofline`` describes the dominant kernel (largest average duration),
 timed with those HIP events on the stream it runs on.  ``kernels_isolated``
 times each kernel alone (repeated launches of that kernel).
 Extra fields report K1's full backward (fused grad_W vs the reference's matmul), a whole
-MHCLiteBlock forward + backward with the fused path vs the reference's rules,
+MHCLiteBlock forward + backward with the fused path vs the reference's rules
+(at C and at 2C, i.e. the C=2048 block configuration),
 and the eval-mode forward latency of the inference shapes (C=4096,
 T = 1, 64, 257, 65537; eager and HIP-graph replay).
 ``cpu_baseline`` times the reference's PyTorch formulation of the same six ops
@@ -511,6 +512,8 @@ def main() -> None:
     alone = None if args.no_extras else isolated_kernels(launch, bm)
     k1_full_bwd = None if args.no_extras else k1_backward_paths(inp, T, C)
     blk = None if args.no_extras else block_step(T, C)
+    # The block configuration at C = 2048 (same T), with its own layer width.
+    blk2 = None if args.no_extras else block_step(T, 2 * C)
     lat = None if args.no_extras else eval_latency(tokens=eval_tokens)
     ceil = stream_ceilings()
     split = read_write_split(T, n, C, D)
@@ -543,6 +546,7 @@ def main() -> None:
         "ceilings_GBps": ceil,
         "k1_backward_with_grad_W": k1_full_bwd,
         "block_step": blk,
+        "block_step_2C": blk2,
         "eval_latency": lat,
         "kernels": per,
         "kernels_isolated": alone,
