@@ -189,6 +189,107 @@ __global__ __launch_bounds__(kK2Threads) void k2_bwd_kernel(
 // One wave per parameter gradient: lanes take blocks lane, lane + 64, ...,
 // then a butterfly; the result is rounded to bf16 (the reference sums a bf16
 // tensor) and stored in the parameter's dtype (fp32 or bf16).
+// Backward for few tokens, 32 lanes per token (lane q: logit q) and 8 tokens
+// per workgroup.  Every per-token value is k2_bwd_kernel's: the forward is
+// k2_token32's (bit-identical to the chain), and each sum over a token's
+// terms runs through shuffles in the chain's order.  The workgroup's
+// parameter partials add its 8 tokens in order (a different order over tokens
+// than k2_bwd_kernel's, still fixed).
+constexpr int kK2BwdTok = kK2Threads / 32;
+
+__global__ __launch_bounds__(kK2Threads) void k2_bwd_small(
+    const uint16_t* __restrict__ proj, const K2Params P, const float* __restrict__ g_hpre,
+    const float* __restrict__ g_hpost, const float* __restrict__ g_H, uint16_t* __restrict__ grad_proj,
+    float* __restrict__ partial, int64_t T) {
+#pragma clang fp contract(off)
+  __shared__ K2Smem sm;
+  __shared__ float red[kK2BwdTok][kNPar];
+  stage_params<kK2Threads>(P, sm);
+  const int q = threadIdx.x & 31;
+  const int slot = static_cast<int>(threadIdx.x) >> 5;
+  const int64_t tq = static_cast<int64_t>(blockIdx.x) * kK2BwdTok + slot;
+  const bool valid = tq < T;
+  const int64_t t = valid ? tq : T - 1;  // idle slots recompute the last token, store nothing
+
+  // Forward, as k2_token32: y = h_pre (q < 4) or the post sigmoid (q < 8),
+  // hq = h_post, a = the softmax weight of permutation q - 8.
+  const float p = bf16_to_f32(proj[t * kDk + q]);
+  const float alpha = q < kN ? sm.sc[0] : (q < 2 * kN ? sm.sc[1] : sm.sc[2]);
+  const float z = rb(rb(alpha * p) + sm.sc[3 + q]);
+  const float y = q < 2 * kN ? rb(sigmoid_f32(z)) : 0.f;
+  const float hq = rb(2.f * y);
+  float mx = q >= 2 * kN ? z : -INFINITY;
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 32));
+  const float e = q >= 2 * kN ? expf(z - mx) : 0.f;
+  float sum = 0.f;
+#pragma unroll
+  for (int m = 0; m < kNF; ++m) sum = sum + __shfl(e, 2 * kN + m, 32);
+  const float a = rb(e / sum);
+
+  // Incoming gradients, rounded to bf16 (the .float() casts' backward).
+  const float gh = (q < kN * kN && g_H) ? rb(g_H[t * kN * kN + q]) : 0.f;
+  // grad of h_post[i] (lanes 4 + i) and of h_pre[j] (lanes j) through
+  // H_merged = H_res - outer(h_post, h_pre), each sum in the chain's order.
+  const int i4 = (q - kN) & 3, j4 = q & 3;
+  float sq = 0.f, sp = 0.f;
+#pragma unroll
+  for (int k = 0; k < kN; ++k) {
+    sq = sq + rb(-__shfl(gh, i4 * kN + k, 32) * __shfl(y, k, 32));
+    sp = sp + rb(-__shfl(gh, k * kN + j4, 32) * __shfl(hq, kN + k, 32));
+  }
+  const float ghq = rb((g_hpost ? rb(g_hpost[t * kN + i4]) : 0.f) + rb(sq));
+  const float ghp = rb((g_hpre ? rb(g_hpre[t * kN + j4]) : 0.f) + rb(sp));
+  // Softmax backward (lanes 8 + m): gy = rb(rb(gH . perm_m) a), gz = rb(gy - a sum(gy)).
+  const int m8 = q >= 2 * kN ? q - 2 * kN : 0;
+  const float* pf = reinterpret_cast<const float*>(sm.perm);
+  float acc = 0.f;
+#pragma unroll
+  for (int k = 0; k < kN * kN; ++k) acc = acc + __shfl(gh, k, 32) * pf[m8 * kN * kN + k];
+  const float gy = q >= 2 * kN ? rb(rb(acc) * a) : 0.f;
+  float sgy = 0.f;
+#pragma unroll
+  for (int m = 0; m < kNF; ++m) sgy = sgy + __shfl(gy, 2 * kN + m, 32);
+  float gz;
+  if (q < kN) {
+    gz = rb(rb(ghp * rb(1.f - y)) * y);
+  } else if (q < 2 * kN) {
+    const float gs = rb(ghq * 2.f);
+    gz = rb(rb(gs * rb(1.f - y)) * y);
+  } else {
+    gz = rb(gy - a * sgy);
+  }
+  if (valid) grad_proj[t * kDk + q] = f32_to_bf16(rb(gz * alpha));
+
+  // This token's parameter terms: the alphas' sums over their logits in
+  // order, the bias gradients gz.
+  const float pc = rb(gz * p);
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f;
+#pragma unroll
+  for (int k = 0; k < kDk; ++k) {
+    const float v = __shfl(pc, k, 32);
+    if (k < kN)
+      s0 += v;
+    else if (k < 2 * kN)
+      s1 += v;
+    else
+      s2 += v;
+  }
+  red[slot][3 + q] = valid ? gz : 0.f;
+  if (q == 0) {
+    red[slot][0] = valid ? s0 : 0.f;
+    red[slot][1] = valid ? s1 : 0.f;
+    red[slot][2] = valid ? s2 : 0.f;
+  }
+  __syncthreads();
+  if (threadIdx.x < kNPar) {
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < kK2BwdTok; ++w) v += red[w][threadIdx.x];
+    partial[static_cast<int64_t>(blockIdx.x) * kNPar + threadIdx.x] = v;
+  }
+}
+
 __global__ __launch_bounds__(kWave) void k2_param_reduce(const float* __restrict__ partial,
                                                          int64_t nblocks, void* g_ap, void* g_apo,
                                                          void* g_ar, void* g_bias, bool bf16) {
@@ -210,6 +311,9 @@ __global__ __launch_bounds__(kWave) void k2_param_reduce(const float* __restrict
 bool k2_bad(int64_t T, int64_t n) { return T < 0 || n != kN; }
 
 int64_t k2_blocks(int64_t T) { return (T + kK2Threads - 1) / kK2Threads; }
+// Workgroups (and parameter partials) of the backward: k2_bwd_small up to
+// kK2SmallT tokens, k2_bwd_kernel above.
+int64_t k2_bwd_blocks(int64_t T) { return T <= kK2SmallT ? (T + kK2BwdTok - 1) / kK2BwdTok : k2_blocks(T); }
 
 }  // namespace
 
@@ -254,7 +358,7 @@ extern "C" int fmhc_k2_fwd(const uint16_t* proj, const void* alpha_pre, const vo
 extern "C" int64_t fmhc_k2_bwd_workspace_bytes(int64_t T) {
   using namespace fmhc;
   if (T <= 0) return 0;
-  return k2_blocks(T) * kNPar * static_cast<int64_t>(sizeof(float));
+  return k2_bwd_blocks(T) * kNPar * static_cast<int64_t>(sizeof(float));
 }
 
 extern "C" int fmhc_k2_bwd(const uint16_t* proj, const void* alpha_pre, const void* alpha_post,
@@ -270,13 +374,16 @@ extern "C" int fmhc_k2_bwd(const uint16_t* proj, const void* alpha_pre, const vo
   if (!k2_params(alpha_pre, alpha_post, alpha_res, bias, perm, param_dtype, P)) return FMHC_ERR_INVALID_ARGUMENT;
   if (!grad_alpha_pre || !grad_alpha_post || !grad_alpha_res || !grad_bias) return FMHC_ERR_INVALID_ARGUMENT;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int64_t nblocks = k2_blocks(T);
+  const int64_t nblocks = k2_bwd_blocks(T);
   float* partial = static_cast<float*>(workspace);
   if (T > 0) {
     if (!proj || !grad_proj) return FMHC_ERR_INVALID_ARGUMENT;
     if (!workspace || workspace_bytes < fmhc_k2_bwd_workspace_bytes(T)) return FMHC_ERR_INVALID_ARGUMENT;
     const dim3 grid(static_cast<unsigned>(nblocks));
-    if (aligned16(proj) && aligned16(grad_proj))
+    if (T <= kK2SmallT)
+      k2_bwd_small<<<grid, kK2Threads, 0, s>>>(proj, P, grad_h_pre, grad_h_post, grad_H_merged, grad_proj,
+                                               partial, T);
+    else if (aligned16(proj) && aligned16(grad_proj))
       k2_bwd_kernel<true><<<grid, kK2Threads, 0, s>>>(proj, P, grad_h_pre, grad_h_post, grad_H_merged,
                                                       grad_proj, partial, T);
     else

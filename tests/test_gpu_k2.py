@@ -234,3 +234,16 @@ def test_k2_fwd_small_and_large_kernels_agree():
     small = K.k2_fwd(proj[:4096].to(DEV), *prm)
     for u, v in zip(small, big):
         assert torch.equal(u, v[:4096])
+
+
+def test_k2_bwd_small_and_large_kernels_agree():
+    """The backward likewise: 32 lanes per token up to 4096 tokens, one thread
+    beyond, with the same per-token operation order, so grad_proj of the first
+    4096 tokens of a 4097-token call equals a 4096-token call bit for bit (the
+    parameter gradients add the tokens in a different, fixed, order)."""
+    proj, alphas, bias, grads = _case(4097, 91)
+    prm = _dev([*alphas, bias, PERM])
+    g = _dev(list(grads))
+    big = K.k2_bwd(proj.to(DEV), *prm, *g)
+    small = K.k2_bwd(proj[:4096].to(DEV), *prm, *[t[:4096] for t in g])
+    assert torch.equal(small[0], big[0][:4096])
