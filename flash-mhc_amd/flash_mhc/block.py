@@ -188,6 +188,7 @@ class MHCLiteBlock(nn.Module):
 
     def _mhc_pre_map_triton(self, x_streams: torch.Tensor, use_ckpt: bool = False):
         if _ops.fused_premap_enabled():
+            xgrad = _ops.fused_xgrad_flag()  # the pre-map op is on: only its own switch left
             # With x_sink, post-res's x-gradient is added in K1's backward
             # store rather than by autograd.
             args = (x_streams, self._projection_weight(x_streams.dtype), self.alpha_pre, self.alpha_post,
@@ -202,7 +203,7 @@ class MHCLiteBlock(nn.Module):
                                           use_reentrant=False)
             else:
                 layer_input, H_merged, h_post, _h_pre, _proj, _inv, x_sink = torch.ops.flash_mhc.mhc_pre_map(*args)
-            if _ops.fused_xgrad_enabled():
+            if xgrad:
                 return layer_input, H_merged, h_post, x_sink
             return layer_input, H_merged, h_post
         return self._pre_map_region(self._mhc_pre_map_triton_ops, x_streams, use_ckpt)

@@ -285,10 +285,14 @@ def _fused_rmsnorm_project_bwd_cuda(grad_out, x_flat, W, proj_out, inv_rms):
 
 
 def _check_k2(proj: torch.Tensor, perm_mat: torch.Tensor) -> None:
-    if proj.dim() != 2 or proj.shape[1] != 32 or tuple(perm_mat.shape) != (24, 16):
+    _check_k2_shapes(tuple(proj.shape), perm_mat)
+
+
+def _check_k2_shapes(proj_shape: tuple, perm_mat: torch.Tensor) -> None:
+    if len(proj_shape) != 2 or proj_shape[1] != 32 or tuple(perm_mat.shape) != (24, 16):
         raise ValueError(
             "flash_mhc::mhc_coefficients supports n=4 only: proj must be (T, 32) and "
-            f"perm_mat (24, 16), got {tuple(proj.shape)} and {tuple(perm_mat.shape)}"
+            f"perm_mat (24, 16), got {tuple(proj_shape)} and {tuple(perm_mat.shape)}"
         )
 
 
@@ -313,7 +317,7 @@ def _mhc_coefficients_backward_cuda(grad_h_pre, grad_h_post, grad_H_merged, proj
 @torch.library.impl(_lib, "mhc_pre_map", "CUDA")
 def _mhc_pre_map_cuda(x_streams, W, alpha_pre, alpha_post, alpha_res, bias, perm_mat):
     _check_n4(x_streams, "flash_mhc::mhc_pre_map supports n=4 only")
-    _check_k2(x_streams.new_empty((0, W.shape[0])), perm_mat)
+    _check_k2_shapes((0, W.shape[0]), perm_mat)
     # The sink's one element is zeroed by the same launches (no fill kernel).
     x_sink = x_sink_like(x_streams)
     outs = _k.premap_fwd(x_streams.contiguous(), W.to(x_streams.dtype).contiguous(),
@@ -324,7 +328,7 @@ def _mhc_pre_map_cuda(x_streams, W, alpha_pre, alpha_post, alpha_res, bias, perm
 @torch.library.impl(_lib, "mhc_pre_map_coeffs", "CUDA")
 def _mhc_pre_map_coeffs_cuda(x_streams, W, alpha_pre, alpha_post, alpha_res, bias, perm_mat):
     _check_n4(x_streams, "flash_mhc::mhc_pre_map_coeffs supports n=4 only")
-    _check_k2(x_streams.new_empty((0, W.shape[0])), perm_mat)
+    _check_k2_shapes((0, W.shape[0]), perm_mat)
     T, n, C = x_streams.shape
     x_sink = x_sink_like(x_streams)
     li_sink = x_streams.new_empty_strided((T, C), (0, 0))
@@ -439,10 +443,15 @@ def fused_premap_enabled() -> bool:
     return _env_flag("FLASH_MHC_FUSED_PREMAP") and fused_k2_enabled()
 
 
+def fused_xgrad_flag() -> bool:
+    """FLASH_MHC_FUSED_XGRAD alone (callers that already know the pre-map op is on)."""
+    return _env_flag("FLASH_MHC_FUSED_XGRAD")
+
+
 def fused_xgrad_enabled() -> bool:
     """With the pre-map op, MHCLiteBlock sends post-res's x-gradient through
     mhc_pre_map's x_sink (added in K1's store) unless FLASH_MHC_FUSED_XGRAD=0."""
-    return _env_flag("FLASH_MHC_FUSED_XGRAD") and fused_premap_enabled()
+    return fused_xgrad_flag() and fused_premap_enabled()
 
 
 def _fused_rmsnorm_project_backward(ctx, grad_out, grad_inv_rms):
