@@ -509,12 +509,14 @@ def main() -> None:
         except (OSError, ValueError):
             traffic = None
 
+    # The latency-bound eval shapes first: after the block steps' seconds of
+    # full-bandwidth work the same graph replays measure up to 25% slower.
+    lat = None if args.no_extras else eval_latency(tokens=eval_tokens)
     alone = None if args.no_extras else isolated_kernels(launch, bm)
     k1_full_bwd = None if args.no_extras else k1_backward_paths(inp, T, C)
     blk = None if args.no_extras else block_step(T, C)
     # The block configuration at C = 2048 (same T), with its own layer width.
     blk2 = None if args.no_extras else block_step(T, 2 * C)
-    lat = None if args.no_extras else eval_latency(tokens=eval_tokens)
     ceil = stream_ceilings()
     split = read_write_split(T, n, C, D)
     for name in KERNELS:
