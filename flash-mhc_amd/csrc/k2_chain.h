@@ -154,8 +154,9 @@ __device__ __forceinline__ void k2_h_merged(const K2Fwd& f, const f32x4 sperm[kN
 // entry each.  Every sum keeps k2_chain's / k2_h_merged's order (the softmax
 // denominator and each H_res entry are added sequentially over m), so the
 // results are bit-identical to the one-thread chain's.
-__device__ __forceinline__ void k2_token32(const K2Smem& sm, float p, int q, int64_t t, float* __restrict__ h_pre,
-                                           float* __restrict__ h_post, float* __restrict__ H) {
+// Returns lane q's sigmoid value: h_pre[t, q] for q < 4.
+__device__ __forceinline__ float k2_token32(const K2Smem& sm, float p, int q, int64_t t, float* __restrict__ h_pre,
+                                            float* __restrict__ h_post, float* __restrict__ H) {
 #pragma clang fp contract(off)
   const float alpha = q < kN ? sm.sc[0] : (q < 2 * kN ? sm.sc[1] : sm.sc[2]);
   const float z = rb(rb(alpha * p) + sm.sc[3 + q]);
@@ -180,6 +181,7 @@ __device__ __forceinline__ void k2_token32(const K2Smem& sm, float p, int q, int
     h_pre[t * kN + q] = y;
   else if (q < 2 * kN)
     h_post[t * kN + (q - kN)] = hq;
+  return y;
 }
 
 // K2 forward for T tokens (k2.hip), also zeroing z: fmhc_k2_fwd's launch

@@ -96,26 +96,28 @@ __global__ __launch_bounds__(kFinishThreads) void k1_finish_k2(
 }
 
 // The same with K3 fused, one token per workgroup (blockIdx.x): its first 32
-// lanes finish K1 and run K2; after the barrier all 256 lanes mix the token's
-// streams into layer_input with h_pre as written (k3_token, so the values are
-// those of the separate K3 kernel).  Saves K3's launch for few tokens.
+// lanes finish K1 and run K2 and leave h_pre in LDS; after the barrier all
+// 256 lanes mix the token's streams into layer_input with those values
+// (k3_token, so the results are those of the separate K3 kernel reading the
+// stored h_pre).  Saves K3's launch for few tokens.
 template <int VEC>
 __global__ __launch_bounds__(kFinishThreads) void k1_finish_k2_k3(
     const float* __restrict__ part, int S, int nC, const K2Params P, uint16_t* __restrict__ proj,
     float* __restrict__ inv_rms, float* __restrict__ h_pre, float* __restrict__ h_post, float* __restrict__ H,
     const ZeroWords z, const uint16_t* __restrict__ x, uint16_t* __restrict__ layer_input, int C) {
   __shared__ K2Smem sm;
+  __shared__ float hsh[kN];  // the token's h_pre, handed from the K2 lanes to all
   zero_words(z);
   stage_params<kFinishThreads>(P, sm);
   const int64_t t = blockIdx.x;
   if (threadIdx.x < 32) {
     const int q = static_cast<int>(threadIdx.x);
     const float p = finish_token32(part, S, nC, q, t, proj, inv_rms);
-    k2_token32(sm, p, q, t, h_pre, h_post, H);
+    const float y = k2_token32(sm, p, q, t, h_pre, h_post, H);
+    if (q < kN) hsh[q] = y;
   }
-  __syncthreads();  // h_pre[t] written by this workgroup's first lanes
-  const float* hp = h_pre + t * 4;
-  const float h[4] = {hp[0], hp[1], hp[2], hp[3]};
+  __syncthreads();
+  const float h[4] = {hsh[0], hsh[1], hsh[2], hsh[3]};
   k3_token<VEC>(x + t * 4 * C, h, layer_input + t * C, static_cast<int>(threadIdx.x), kFinishThreads, C);
 }
 
