@@ -7,13 +7,15 @@
 //
 // Follows src/flash_mhc/kernels.py:673-717 (forward) and :720-853 (fused
 // backward) of the reference, written for gfx950:
-//   * a group of LPT consecutive lanes owns one token; a wave64 holds
-//     64 / LPT tokens.  Each lane streams 16-byte vectors of all four stream
-//     rows, so every x row is read once and every output row written once;
-//   * the four per-token coefficients are wave-uniform when LPT == 64 and then
+//   * a group of LPT consecutive lanes owns one token: a wave64 holds 64 / LPT
+//     tokens, or a token spans LPT / 64 waves (LPT = 128, 256: wide rows, few
+//     tokens).  Each lane streams 16-byte vectors of all four stream rows, so
+//     every x row is read once and every output row written once;
+//   * the four per-token coefficients are wave-uniform when LPT >= 64 and then
 //     live in SGPRs;
 //   * the backward's four reductions over C finish with an in-wave butterfly
-//     (no LDS, no atomics), so grad_h_pre is deterministic.
+//     and, when a token spans several waves, an LDS sum over them in wave
+//     order (no atomics), so grad_h_pre is deterministic.
 #include "fmhc_common.h"
 
 namespace fmhc {
@@ -22,8 +24,8 @@ namespace {
 
 constexpr int kBlock = 256;  // 4 waves per workgroup
 
-// LPT <= 64: 64 / LPT tokens per wave.  LPT = 128 or 256 (forward kernels,
-// few tokens): LPT / 64 waves per token.
+// LPT <= 64: 64 / LPT tokens per wave.  LPT = 128 or 256: LPT / 64 waves per
+// token.
 template <int LPT>
 __device__ __forceinline__ int64_t token_of_lane(int lane) {
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);

@@ -12,7 +12,8 @@
 // lanes owns one token and streams 16-byte vectors of every row it touches, so
 // each input row is read once and each output row written once per launch.
 // The backward keeps its 20 per-token partial sums in registers and finishes
-// them with an in-wave butterfly: no LDS, no atomics, deterministic.
+// them with an in-wave butterfly (and, when a token spans several waves, an
+// LDS sum over them in wave order): no atomics, deterministic.
 #include "fmhc_common.h"
 
 namespace fmhc {
@@ -21,8 +22,8 @@ namespace {
 
 constexpr int kBlock = 256;  // 4 waves per workgroup
 
-// LPT <= 64: 64 / LPT tokens per wave.  LPT = 128 or 256 (forward kernels,
-// few tokens): LPT / 64 waves per token.
+// LPT <= 64: 64 / LPT tokens per wave.  LPT = 128 or 256: LPT / 64 waves per
+// token.
 template <int LPT>
 __device__ __forceinline__ int64_t token_of_lane(int lane) {
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
