@@ -23,6 +23,8 @@
 // Because the contraction index may be permuted freely (as long as A and B
 // agree), each lane's eight contraction values are eight consecutive bf16 in
 // memory: one 16-byte load.
+#include <type_traits>
+
 #include "fmhc_common.h"
 #include "k1_premap.h"
 
@@ -69,13 +71,15 @@ struct FwdFrag {
 // workgroup writes its fp32 partial sums (32 projections + sum of squares per
 // token) to part[t][33][S4] (S4 = gridDim.y rounded up to 4) instead of the
 // outputs; k1_fwd_finish adds the gridDim.y partials in order.
+// Workgroups whose tokens all lie before nt_end load x with the nontemporal
+// hint (see the chunk loop).
 template <int R, int SPLIT, bool SPLITK>
 __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __restrict__ x,
                                                              const uint16_t* __restrict__ W,
                                                              uint16_t* __restrict__ out,
                                                              float* __restrict__ inv_rms,
                                                              float* __restrict__ part,
-                                                             int64_t T, int nC, int cps) {
+                                                             int64_t T, int nC, int cps, int64_t nt_end) {
   __shared__ float red_acc[SPLIT][R][8][kWave];
   __shared__ float red_ss[SPLIT][R][16];
   __shared__ u32x4 xs[SPLIT][16 * R * 8];  // per wave: 16R tokens x 8 swizzled 16-byte slots
@@ -122,10 +126,14 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
   // concurrent reads of all workgroups over the DRAM channels instead of every
   // workgroup hitting the same column of its 8 KiB-strided rows), and
   // double-buffers: the next chunk's fragments are loaded while the MFMAs of
-  // the current one run.  x uses ordinary loads: with the nontemporal hint
-  // this kernel alone is 10% faster, but K3's forward, which reads x next,
-  // loses as much, because it no longer finds the tail of x in the
-  // memory-side cache.
+  // the current one run.  The nontemporal hint makes this kernel 10% faster
+  // alone, but the next kernel that reads x (K3's forward, K1's backward)
+  // then loses as much, because it no longer finds the tail of x in the
+  // memory-side cache.  So only the head of x, which that cache could not
+  // keep anyway, takes the hint: workgroups before nt_end (the host leaves
+  // the last kFwdCachedTail bytes of x to ordinary loads).  The flag is
+  // uniform per workgroup, and the loop is instantiated once per value: a
+  // select between the two loads would be folded into one ordinary load.
   // With SPLITK the workgroup's chunks are cbeg .. cbeg + nfull - 1 (no
   // rotation: the workgroups of one token block already cover different
   // columns), and only the last split takes the ragged chunk.
@@ -136,14 +144,20 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
   const int rot = !SPLITK && nfull > 0 ? static_cast<int>(blockIdx.x % static_cast<unsigned>(nfull)) : 0;
   FwdFrag<R> f0, f1;
   auto chunk_at = [&](int p) { return cbeg + (p + rot < nfull ? p + rot : p + rot - nfull); };
-  auto load = [&](FwdFrag<R>& f, int p) {
+  auto load = [&](FwdFrag<R>& f, int p, auto nt) {
     const int k = chunk_at(p) * 64;
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       f.wa[s] = *reinterpret_cast<const u32x4*>(w0 + k + 32 * s);
       f.wb[s] = *reinterpret_cast<const u32x4*>(w1 + k + 32 * s);
 #pragma unroll
-      for (int r = 0; r < R; ++r) f.xv[s][r] = *reinterpret_cast<const u32x4*>(xw + xoff[s * R + r] + k);
+      for (int r = 0; r < R; ++r) {
+        const u32x4* px = reinterpret_cast<const u32x4*>(xw + xoff[s * R + r] + k);
+        if constexpr (decltype(nt)::value)
+          f.xv[s][r] = __builtin_nontemporal_load(px);
+        else
+          f.xv[s][r] = *px;
+      }
     }
   };
   // Token rows -> MFMA layout (lane: token row, 8 consecutive k) through the
@@ -174,15 +188,16 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
   // the compiler keeps them ahead of the MFMAs; an odd count ends with f0.
   const int n = nfull > wave ? (nfull - wave + SPLIT - 1) / SPLIT : 0;
   auto pos = [&](int i) { return wave + SPLIT * (i < n ? i : n - 1); };
-  if (n > 0) {
-    load(f0, pos(0));
+  auto chunks = [&](auto nt) {
+    if (n <= 0) return;
+    load(f0, pos(0), nt);
     int i = 0;
     for (; i + 1 < n; i += 2) {
-      load(f1, pos(i + 1));
+      load(f1, pos(i + 1), nt);
       __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the MFMAs
       transpose(f0);
       compute(f0);
-      load(f0, pos(i + 2));
+      load(f0, pos(i + 2), nt);
       __builtin_amdgcn_sched_barrier(0);
       transpose(f1);
       compute(f1);
@@ -191,7 +206,11 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
       transpose(f0);
       compute(f0);
     }
-  }
+  };
+  if (t0 + 16 * R <= nt_end)
+    chunks(std::true_type{});
+  else
+    chunks(std::false_type{});
   // Ragged last chunk (nC % 64 != 0): 16-byte pieces past nC contribute zero.
   if ((nC & 63) != 0 && last_split && wave == nfull % SPLIT) {
     const int k = nall * 64;
@@ -738,6 +757,16 @@ constexpr int kFwdSplit = 4;  // waves per workgroup (split of the nC axis)
 constexpr int kFwdR = 4;
 constexpr int kFwdRSmall = 2;
 constexpr int64_t kFwdLargeT = 16384;
+// Bytes at the end of x that the one-pass forward reads with ordinary loads,
+// so that the next kernel over x finds them in the 256 MB memory-side cache;
+// the tokens before them take the nontemporal hint.  In the six-kernel step
+// (K1 forward, then K1's backward over the same x) against ordinary loads
+// throughout: K1 forward 99 -> 92.5 us, the step 0.8% faster at T = 65536,
+// C = 1024; the step 1.0% faster at T = 16384, C = 4096 with 384 MiB (0.5%
+// with 256).  A tail of 128 MiB or none costs K1's backward more (up to
+// 29 us) than the forward saves.
+constexpr int64_t kFwdCachedTail = int64_t{320} << 20;
+int64_t k1_fwd_nt_end(int64_t T, int64_t nC) { return T - kFwdCachedTail / (2 * nC); }
 // Split forward for few tokens: one 16-token block per workgroup and up to
 // kSplitMax column ranges per block, aiming at kSplitTarget workgroups; taken
 // when the plan has at least kSplitMinS ranges (T <= 2048): from there on the
@@ -805,18 +834,18 @@ int k1_fwd_run(const uint16_t* x_flat, const uint16_t* W, uint16_t* out, float* 
       float* part = static_cast<float*>(ws);
       const dim3 grid(blocks_for(T, 16 * kSplitR), p.S);
       k1_fwd_mfma<kSplitR, kFwdSplit, true><<<grid, kWave * kFwdSplit, 0, s>>>(x_flat, W, out, inv_rms, part,
-                                                                              T, nc, p.cps);
+                                                                              T, nc, p.cps, 0);
       const int st = launch_status();
       if (st != FMHC_OK) return st;
       k1_fwd_finish<<<dim3(blocks_for(T, 4)), 256, 0, s>>>(part, out, inv_rms, T, nc, p.S);
     } else if (T >= kFwdLargeT) {
       const dim3 grid(blocks_for(T, 16 * kFwdR));
       k1_fwd_mfma<kFwdR, kFwdSplit, false><<<grid, kWave * kFwdSplit, 0, s>>>(x_flat, W, out, inv_rms, nullptr,
-                                                                             T, nc, 0);
+                                                                             T, nc, 0, k1_fwd_nt_end(T, nC));
     } else {
       const dim3 grid(blocks_for(T, 16 * kFwdRSmall));
-      k1_fwd_mfma<kFwdRSmall, kFwdSplit, false><<<grid, kWave * kFwdSplit, 0, s>>>(x_flat, W, out, inv_rms,
-                                                                                  nullptr, T, nc, 0);
+      k1_fwd_mfma<kFwdRSmall, kFwdSplit, false><<<grid, kWave * kFwdSplit, 0, s>>>(
+          x_flat, W, out, inv_rms, nullptr, T, nc, 0, k1_fwd_nt_end(T, nC));
     }
   } else {
     const dim3 grid(blocks_for(T, 4));
@@ -963,7 +992,7 @@ int k1_fwd_partials(const uint16_t* x_flat, const uint16_t* W, void* ws, int64_t
   if (!ws || ws_bytes < p.bytes || !aligned16(ws)) return -FMHC_ERR_INVALID_ARGUMENT;
   const dim3 grid(blocks_for(T, 16 * kSplitR), p.S);
   k1_fwd_mfma<kSplitR, kFwdSplit, true><<<grid, kWave * kFwdSplit, 0, s>>>(
-      x_flat, W, nullptr, nullptr, static_cast<float*>(ws), T, static_cast<int>(nC), p.cps);
+      x_flat, W, nullptr, nullptr, static_cast<float*>(ws), T, static_cast<int>(nC), p.cps, 0);
   const int st = launch_status();
   return st == FMHC_OK ? p.S : -st;
 }

@@ -306,7 +306,12 @@ def test_metric_size_sampled():
     T, C = 65536, 1024
     nC = 4 * C
     g = torch.Generator().manual_seed(1234)
-    idx = torch.randperm(T, generator=g)[:512].sort().values
+    idx = torch.randperm(T, generator=g)[:512]
+    # K1 forward reads the tokens before T - 320 MiB / (2 nC) with the
+    # nontemporal hint and the rest with ordinary loads: sample both sides of
+    # that boundary (token 24576 here) and the last tile as well.
+    nt_end = T - (320 << 20) // (2 * nC)
+    idx = torch.cat([idx, torch.arange(nt_end - 80, nt_end + 80), torch.arange(T - 64, T)]).unique()
     x = randn((T, 4, C), 1)
     W = randn((32, nC), 2, scale=0.02)
     lo = randn((T, C), 3)
