@@ -11,7 +11,11 @@ measured step time (K steps of bare launches between two events).  Per-kernel
 durations come from a second pass of K steps with an event pair around each
 launch; ``roofline`` describes the dominant kernel (largest average duration),
 timed with those HIP events on the stream it runs on.  ``kernels_isolated``
-times each kernel alone (repeated launches of that kernel).
+times each kernel alone (repeated launches of that kernel), ``kernels_cold``
+each kernel after a flush of L2 and the memory-side cache (CacheFlush).
+``ceilings_GBps`` are 1 GiB streaming probes with the nontemporal hint, as the
+kernels' streaming loads and stores carry (ordinary-access probes beside them
+are labelled ``*_ordinary``).
 Extra fields report K1's full backward (fused grad_W vs the reference's matmul), a whole
 MHCLiteBlock forward + backward with the fused path vs the reference's rules
 (at C and at 2C, i.e. the C=2048 block configuration),
@@ -20,7 +24,8 @@ T = 1, 64, 257, 65537; eager and HIP-graph replay).
 ``cpu_baseline`` times the reference's PyTorch formulation of the same six ops
 (fp32 autograd, restated in oracle/) on the host's cores, by default on the
 whole workload (--cpu-tokens, --cpu-iters bound it), reported with the same
-bytes model.
+bytes model; ``cpu_block_config1`` the fp32 plain-path MHCLiteBlock forward +
+backward at T=4096, C=1024 on the same cores (the golden configuration).
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--T 65536] [--C 1024]
 """
@@ -314,17 +319,84 @@ def read_write_split(T: int, n: int, C: int, D: int) -> dict[str, tuple[int, int
     }
 
 
-def stream_ceilings(nbytes: int = 1 << 30, iters: int = 10) -> dict[str, float]:
-    """Measured HBM GB/s of 16-byte streaming read / write / copy (fmhc_stream_probe)."""
-    from flash_mhc import _abi
+PROBE_READ, PROBE_WRITE, PROBE_COPY, PROBE_READ_CACHED, PROBE_WRITE_CACHED = 0, 1, 2, 3, 4
 
-    lib = _abi.load()
+
+class Probe:
+    """The bandwidth probe and cache flush (include/flash_mhc_probe.h), a
+    library of its own that only this benchmark loads."""
+
+    def __init__(self):
+        import ctypes
+
+        from flash_mhc import _abi, build
+
+        path = build.PROBE_LIB_PATH
+        if not path.exists():
+            raise _abi.ExtensionMissingError(f"probe library not found at {path}; run flash_mhc.build")
+        self.lib = ctypes.CDLL(str(path))
+        self.lib.fmhc_stream_probe.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                               ctypes.c_void_p]
+        if self.lib.fmhc_probe_abi_version() != 2:
+            raise _abi.ExtensionMissingError(f"{path} is stale; rebuild it")
+        self._check = _abi.check
+
+    def run(self, kind: int, src, dst, nbytes: int) -> None:
+        st = torch.cuda.current_stream().cuda_stream
+        s = self.lib.fmhc_stream_probe(kind, None if src is None else src.data_ptr(), dst.data_ptr(), nbytes, st)
+        self._check(s, "stream_probe")
+
+
+class CacheFlush:
+    """Evicts L2 and the 256 MB memory-side cache: a 512 MiB write (ordinary
+    stores) and then a 1 GiB read (ordinary loads) of scratch buffers, so the
+    caches hold neither the next kernel's inputs nor dirty lines it would
+    have to write back."""
+
+    def __init__(self, probe: Probe, write_bytes: int = 512 << 20, read_bytes: int = 1 << 30):
+        self.probe = probe
+        self.w = torch.empty(write_bytes, dtype=torch.uint8, device="cuda")
+        self.r = torch.empty(read_bytes, dtype=torch.uint8, device="cuda").fill_(1)
+
+    def __call__(self) -> None:
+        self.probe.run(PROBE_WRITE_CACHED, None, self.w, self.w.numel())
+        self.probe.run(PROBE_READ_CACHED, self.r, self.w, self.r.numel())
+
+
+def cold_kernels(launch: dict, bm: dict, flush: CacheFlush, reps: int = 10) -> dict:
+    """Each kernel with cold caches: before every launch the caches are flushed
+    (CacheFlush), then one launch between two events (the flush is queued
+    ahead of the first event, so the pair spans the kernel alone)."""
+    out = {}
+    for name in KERNELS:
+        launch[name]()
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        torch.cuda.synchronize()
+        for e0, e1 in evs:
+            flush()
+            e0.record()
+            launch[name]()
+            e1.record()
+        torch.cuda.synchronize()
+        ts = [e0.elapsed_time(e1) for e0, e1 in evs]
+        med = statistics.median(ts)
+        out[name] = {"median_us": round(med * 1e3, 2), "min_us": round(min(ts) * 1e3, 2),
+                     "GBps": round(bm[name] / (med * 1e-3) / 1e9, 1),
+                     "frac": round(bm[name] / (med * 1e-3) / 1e9 / PEAK_GBPS, 4)}
+    return out
+
+
+def stream_ceilings(probe: Probe, nbytes: int = 1 << 30, iters: int = 10) -> dict[str, float]:
+    """Measured HBM GB/s of 16-byte streaming read / write / copy with the
+    nontemporal hint (the kernels' streaming loads and stores carry it), and
+    ordinary-load / ordinary-store read and write as labelled extras."""
     a = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
     b = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
-    st = torch.cuda.current_stream().cuda_stream
     out = {}
-    for name, kind, moved in (("read", 0, nbytes), ("write", 1, nbytes), ("copy", 2, 2 * nbytes)):
-        run = lambda: _abi.check(lib.fmhc_stream_probe(kind, a.data_ptr(), b.data_ptr(), nbytes, st), "stream_probe")  # noqa: E731
+    for name, kind, moved in (("read", PROBE_READ, nbytes), ("write", PROBE_WRITE, nbytes),
+                              ("copy", PROBE_COPY, 2 * nbytes), ("read_ordinary", PROBE_READ_CACHED, nbytes),
+                              ("write_ordinary", PROBE_WRITE_CACHED, nbytes)):
+        run = lambda: probe.run(kind, a, b, nbytes)  # noqa: E731
         for _ in range(3):
             run()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -336,6 +408,45 @@ def stream_ceilings(nbytes: int = 1 << 30, iters: int = 10) -> dict[str, float]:
         out[name] = round(moved / (e0.elapsed_time(e1) / iters * 1e-3) / 1e9, 1)
     del a, b
     return out
+
+
+def cpu_model() -> str:
+    try:
+        return next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
+    except (OSError, StopIteration):
+        return "unknown"
+
+
+def cpu_block_config1(T: int = 4096, C: int = 1024, iters: int = 5) -> dict:
+    """The golden configuration on the host: MHCLiteBlock(4, C, bias-free
+    Linear(C, C)) in fp32 on the CPU, which takes the block's plain PyTorch
+    path (the reference's fallback, block.py:82-148), x (T, 4, C) ~ N(0, 1)
+    from seed 0, forward + backward of sum(out); median wall time of `iters`
+    after one warm-up, on all host cores."""
+    import flash_mhc
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    torch.manual_seed(0)
+    blk = flash_mhc.MHCLiteBlock(4, C, torch.nn.Linear(C, C, bias=False))
+    x = torch.randn(T, 4, C, generator=torch.Generator().manual_seed(0)).requires_grad_(True)
+
+    def one():
+        blk.zero_grad(set_to_none=True)
+        x.grad = None
+        blk(x).sum().backward()
+
+    one()
+    ts = []
+    for _ in range(iters):
+        t0 = time.perf_counter()
+        one()
+        ts.append(time.perf_counter() - t0)
+    med = statistics.median(ts)
+    return {"workload": f"MHCLiteBlock(4, {C}, Linear({C}, {C})) fp32 plain path, T={T}, forward + backward "
+                        f"of sum(out), x ~ N(0,1) seed 0", "median_ms": round(med * 1e3, 2),
+            "min_ms": round(min(ts) * 1e3, 2), "tokens_per_s": round(T / med, 1), "cores": cores,
+            "cpu": cpu_model(), "iters": iters}
 
 
 def cpu_baseline(C: int, tokens: int, iters: int = 3) -> dict:
@@ -383,16 +494,12 @@ def cpu_baseline(C: int, tokens: int, iters: int = 3) -> dict:
         total += per[name]
     bm = bytes_model(T, n, C, D)
     nbytes = sum(bm.values())
-    try:
-        cpu_model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
-    except (OSError, StopIteration):
-        cpu_model = "unknown"
     return {
         "value": round(nbytes / total / 1e9, 3),
         "unit": "GB/s",
         "cores": cores,
         "kind": "port",
-        "sample": (f"T={T} tokens of the same n=4, C={C} workload, fp32 on the host CPU ({cpu_model}); "
+        "sample": (f"T={T} tokens of the same n=4, C={C} workload, fp32 on the host CPU ({cpu_model()}); "
                    f"K1/K3/K4 forward+autograd backward with the reference's PyTorch formulas; "
                    f"median of {iters} after 1 warmup; bytes from the same model as the GPU kernels"),
         "tokens_per_s": round(T / total, 1),
@@ -513,11 +620,13 @@ def main() -> None:
     # full-bandwidth work the same graph replays measure up to 25% slower.
     lat = None if args.no_extras else eval_latency(tokens=eval_tokens)
     alone = None if args.no_extras else isolated_kernels(launch, bm)
+    probe = Probe()
+    cold = None if args.no_extras else cold_kernels(launch, bm, CacheFlush(probe))
     k1_full_bwd = None if args.no_extras else k1_backward_paths(inp, T, C)
     blk = None if args.no_extras else block_step(T, C)
     # The block configuration at C = 2048 (same T), with its own layer width.
     blk2 = None if args.no_extras else block_step(T, 2 * C)
-    ceil = stream_ceilings()
+    ceil = stream_ceilings(probe)
     split = read_write_split(T, n, C, D)
     for name in KERNELS:
         rd, wr = split[name]
@@ -552,6 +661,7 @@ def main() -> None:
         "eval_latency": lat,
         "kernels": per,
         "kernels_isolated": alone,
+        "kernels_cold": cold,
         "roofline": {
             "kernel": dom,
             "bound": "hbm",
@@ -567,6 +677,7 @@ def main() -> None:
     torch.cuda.empty_cache()
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(C, args.cpu_tokens, args.cpu_iters)
+        line["cpu_block_config1"] = cpu_block_config1()
     print(json.dumps(line), flush=True)
 
 

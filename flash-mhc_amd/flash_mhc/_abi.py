@@ -24,7 +24,7 @@ _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 _INT = ctypes.c_int
 
-# name -> argtypes, following include/flash_mhc_hip.h and include/flash_mhc_probe.h
+# name -> argtypes, following include/flash_mhc_hip.h
 SIGNATURES: dict[str, list] = {
     "fmhc_k1_fwd": [_P, _P, _P, _P, _I64, _I64, _I64, _P],
     "fmhc_k1_fwd_ws": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
@@ -44,7 +44,6 @@ SIGNATURES: dict[str, list] = {
     "fmhc_k4_fwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
     "fmhc_k4_bwd": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
     "fmhc_error_string": [ctypes.c_int],
-    "fmhc_stream_probe": [ctypes.c_int, _P, _P, _I64, _P],
     "fmhc_abi_version": [],
 }
 RESTYPES = {

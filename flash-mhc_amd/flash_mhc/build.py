@@ -1,4 +1,6 @@
-"""Build the gfx950 HIP extension ``_lib/libflash_mhc_hip.so`` in-tree.
+"""Build the gfx950 HIP extension ``_lib/libflash_mhc_hip.so`` in-tree, and
+beside it ``_lib/libflash_mhc_probe.so``, the bandwidth probe and cache flush
+that only bench.py loads (include/flash_mhc_probe.h; not part of the path).
 
 Usage: ``python -m flash_mhc.build`` (run from ``flash-mhc_amd/``) or
 ``flash_mhc.build.build()``.  hipcc cross-compiles for gfx950 without a GPU.
@@ -26,8 +28,10 @@ BUILD_DIR = ROOT / "_build"
 LIB_DIR = PKG_DIR / "_lib"
 LIB_NAME = "libflash_mhc_hip.so"
 LIB_PATH = LIB_DIR / LIB_NAME
+PROBE_LIB_PATH = LIB_DIR / "libflash_mhc_probe.so"
 
-SOURCES = ("k1.hip", "k2.hip", "k3.hip", "k4.hip", "premap.hip", "abi.hip", "stream_probe.hip")
+SOURCES = ("k1.hip", "k2.hip", "k3.hip", "k4.hip", "premap.hip", "abi.hip")
+PROBE_SOURCES = ("stream_probe.hip",)
 
 ARCH = "gfx950"
 
@@ -74,25 +78,38 @@ def _run(cmd: list[str], verbose: bool) -> None:
                 print(line)
 
 
-def build(verbose: bool = False, extra_flags: list[str] | None = None, out: Path | None = None) -> Path:
-    """Compile every HIP source and link the shared library. Returns its path."""
-    cc = hipcc()
-    BUILD_DIR.mkdir(parents=True, exist_ok=True)
-    out = Path(out) if out is not None else LIB_PATH
-    out.parent.mkdir(parents=True, exist_ok=True)
-    flags = COMMON_FLAGS + [f"-I{INCLUDE}"] + list(extra_flags or [])
-
-    def compile_one(src: str) -> Path:
-        obj = BUILD_DIR / (Path(src).stem + ".o")
-        _run([cc, *flags, *SOURCE_FLAGS.get(src, []), "-c", str(CSRC / src), "-o", str(obj)], verbose)
-        return obj
-
-    jobs = min(len(SOURCES), max(1, (os.cpu_count() or 1)))
-    with ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(compile_one, SOURCES))
+def _link(cc: str, objs: list[Path], out: Path, verbose: bool) -> None:
     tmp = out.with_suffix(".so.tmp")
     _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)], verbose)
     os.replace(tmp, out)
+
+
+def build(verbose: bool = False, extra_flags: list[str] | None = None, out: Path | None = None,
+          probe: bool = True) -> Path:
+    """Compile every HIP source and link the shared library (and, with probe,
+    the probe library beside the default one). Returns the library's path.
+
+    extra_flags / out build a variant of the library under another name (its
+    objects go to a build directory of their own)."""
+    cc = hipcc()
+    out = Path(out) if out is not None else LIB_PATH
+    build_dir = BUILD_DIR if out == LIB_PATH else BUILD_DIR / out.stem
+    build_dir.mkdir(parents=True, exist_ok=True)
+    out.parent.mkdir(parents=True, exist_ok=True)
+    flags = COMMON_FLAGS + [f"-I{INCLUDE}"] + list(extra_flags or [])
+    sources = SOURCES + (PROBE_SOURCES if probe and out == LIB_PATH else ())
+
+    def compile_one(src: str) -> Path:
+        obj = build_dir / (Path(src).stem + ".o")
+        _run([cc, *flags, *SOURCE_FLAGS.get(src, []), "-c", str(CSRC / src), "-o", str(obj)], verbose)
+        return obj
+
+    jobs = min(len(sources), max(1, (os.cpu_count() or 1)))
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = dict(zip(sources, ex.map(compile_one, sources)))
+    _link(cc, [objs[s] for s in SOURCES], out, verbose)
+    if probe and out == LIB_PATH:
+        _link(cc, [objs[s] for s in PROBE_SOURCES], PROBE_LIB_PATH, verbose)
     return out
 
 

@@ -14,15 +14,21 @@ import pytest
 from flash_mhc import _abi
 
 ROOT = Path(__file__).resolve().parents[1]
-HEADERS = sorted((ROOT / "include").glob("*.h"))
+HEADERS = [ROOT / "include" / "flash_mhc_hip.h"]  # the product library's ABI
+PROBE_HEADER = ROOT / "include" / "flash_mhc_probe.h"  # bench.py's probe library
+PROBE_LIB = _abi.LIB_PATH.parent / "libflash_mhc_probe.so"
 
 
-def declared_functions() -> set[str]:
+def declared_functions(headers=HEADERS) -> set[str]:
     names = set()
-    for h in HEADERS:
+    for h in headers:
         text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
         names |= set(re.findall(r"\b(fmhc_\w+)\s*\(", text))
     return names
+
+
+def test_every_header_is_checked():
+    assert sorted((ROOT / "include").glob("*.h")) == sorted(HEADERS + [PROBE_HEADER])
 
 
 def test_header_declares_the_abi():
@@ -39,6 +45,29 @@ def test_library_exports_every_declared_symbol():
     exported = set(re.findall(r"\b(fmhc_\w+)\b", out))
     missing = declared_functions() - exported
     assert not missing, missing
+
+
+def test_probe_library_is_separate():
+    """The bandwidth probe lives in its own library (bench.py only): the
+    product library exports none of its symbols, and the probe library
+    exports every function its header declares."""
+    assert PROBE_LIB.exists(), f"build the extension first: {PROBE_LIB}"
+    probe = declared_functions([PROBE_HEADER])
+    assert probe == {"fmhc_stream_probe", "fmhc_probe_abi_version"}
+    out = subprocess.run(["nm", "-D", "--defined-only", str(PROBE_LIB)], capture_output=True, text=True,
+                         check=True).stdout
+    assert probe <= set(re.findall(r"\b(fmhc_\w+)\b", out))
+    main = subprocess.run(["nm", "-D", "--defined-only", str(_abi.lib_path())], capture_output=True, text=True,
+                          check=True).stdout
+    assert not probe & set(re.findall(r"\b(fmhc_\w+)\b", main))
+    lib = ctypes.CDLL(str(PROBE_LIB))
+    assert lib.fmhc_probe_abi_version() == 2
+    # Host-side argument checks (no launch): odd size, unknown kind, null source.
+    lib.fmhc_stream_probe.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                      ctypes.c_void_p]
+    assert lib.fmhc_stream_probe(0, _FAKE, _FAKE, 15, None) == 1
+    assert lib.fmhc_stream_probe(9, _FAKE, _FAKE, 16, None) == 1
+    assert lib.fmhc_stream_probe(3, None, _FAKE, 16, None) == 1
 
 
 def test_library_is_gfx950_code():
