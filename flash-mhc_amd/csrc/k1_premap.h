@@ -7,7 +7,7 @@
 
 namespace fmhc {
 
-constexpr float kRmsEps = 1e-6f;  // K1's RMSNorm epsilon (kernels.py:279 of the reference)
+constexpr float kRmsEps = 1e-6f;  // K1's RMSNorm epsilon (kernels.py:296 of the reference)
 
 // The first kernel of K1's column-split forward alone: when T tokens take that
 // path (few tokens, MFMA-eligible pointers) it writes the fp32 partial sums to

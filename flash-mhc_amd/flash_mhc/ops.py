@@ -26,16 +26,15 @@ Additions (not in the reference):
                               way, with the reference's bf16 rounding points.
                               MHCLiteBlock uses it unless FLASH_MHC_FUSED_K2=0.
   mhc_pre_map (+ _backward)   the pre-map region (K1, K2, K3 of block.py:157-177)
-                              as one op: x is read once forward; the backward
-                              runs K3's reduction, K2 and K1 (with grad_W) and
-                              returns one grad_x.  MHCLiteBlock uses it unless
+                              as one op: the forward runs the K1, K2 and K3
+                              kernels; the backward runs K3's reduction, K2 and
+                              K1 (with grad_W) and returns one grad_x.  MHCLiteBlock uses it unless
                               FLASH_MHC_FUSED_PREMAP=0 (or FLASH_MHC_FUSED_K2=0).
 """
 
 from __future__ import annotations
 
 import os
-import threading
 from contextlib import contextmanager
 
 import torch
@@ -109,26 +108,16 @@ _lib.define(
 
 
 # ---------------------------------------------------------------------------
-# Launch-configuration control.  The reference switches between Triton
-# autotuning and fixed launch parameters (ops.py:44-63); the HIP kernels have
-# one fixed gfx950 configuration per shape class, so the context manager only
-# tracks its nesting depth (MHCLiteBlock enters it in eval mode).
-
-_AUTOTUNE_CONTROL = threading.local()
-
-
-def _autotune_disable_depth() -> int:
-    return int(getattr(_AUTOTUNE_CONTROL, "disable_depth", 0))
+# Launch-configuration control.  The reference switches Triton autotuning off
+# inside this context manager (ops.py:44-63); the HIP kernels have one fixed
+# gfx950 configuration per shape class, so here it does nothing.  It stays
+# for callers that enter it (MHCLiteBlock does in eval mode).
 
 
 @contextmanager
 def disable_autotune_temporarily():
     """Kept for API compatibility; launch configurations are fixed."""
-    _AUTOTUNE_CONTROL.disable_depth = _autotune_disable_depth() + 1
-    try:
-        yield
-    finally:
-        _AUTOTUNE_CONTROL.disable_depth = max(0, _autotune_disable_depth() - 1)
+    yield
 
 
 # ---------------------------------------------------------------------------
