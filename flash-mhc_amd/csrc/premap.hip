@@ -24,6 +24,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+
 #include "flash_mhc_hip.h"
 #include "fmhc_common.h"
 #include "k1_premap.h"
@@ -142,12 +144,14 @@ extern "C" int64_t fmhc_premap_fwd_workspace_bytes(int64_t T, int64_t C) {
   return fmhc_k1_fwd_workspace_bytes(T, 4 * C);
 }
 
-extern "C" int fmhc_premap_fwd(const uint16_t* x, const uint16_t* W, const void* alpha_pre,
-                               const void* alpha_post, const void* alpha_res, const void* bias,
-                               const void* perm, int param_dtype, uint16_t* layer_input, uint16_t* proj,
-                               float* inv_rms, float* h_pre, float* h_post, float* H_merged,
-                               uint16_t* zero_word_a, uint16_t* zero_word_b, void* workspace,
-                               int64_t workspace_bytes, int64_t T, int64_t C, int64_t n, void* stream) {
+namespace {
+
+// The forward of fmhc_premap_fwd with its workspace already in hand.
+int premap_fwd_run(const uint16_t* x, const uint16_t* W, const void* alpha_pre, const void* alpha_post,
+                   const void* alpha_res, const void* bias, const void* perm, int param_dtype,
+                   uint16_t* layer_input, uint16_t* proj, float* inv_rms, float* h_pre, float* h_post,
+                   float* H_merged, uint16_t* zero_word_a, uint16_t* zero_word_b, void* workspace,
+                   int64_t workspace_bytes, int64_t T, int64_t C, int64_t n, void* stream) {
   if (T < 0 || C <= 0 || n != 4 || !param_dtype_ok(param_dtype)) return FMHC_ERR_INVALID_ARGUMENT;
   if (T == 0) return FMHC_OK;
   if (!x || !W || !alpha_pre || !alpha_post || !alpha_res || !bias || !perm || !proj || !inv_rms || !h_pre ||
@@ -185,6 +189,77 @@ extern "C" int fmhc_premap_fwd(const uint16_t* x, const uint16_t* W, const void*
   }
   if (st == FMHC_OK && layer_input) st = fmhc_k3_fwd(x, h_pre, layer_input, T, C, n, stream);
   return st;
+}
+
+// Scratch of fmhc_premap_fwd_noalloc: the column-split forward's partial sums
+// (T x 33 x S4 fp32 for T <= 2048 tokens; at most 2,145,792 bytes over every
+// (T, C), at T = 2032, C = 160).  Each device holds its own copy for the life
+// of the process.  In host code `scratch` names a host-side stand-in, so its
+// device address is looked up once per device (scratch_on_device) and only
+// that address is used.
+constexpr int64_t kNoAllocScratchBytes = int64_t{4} << 20;
+__device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mu;
+void* scratch_addr[kMaxDevices];  // per device; guarded by scratch_mu
+
+// Device address of `scratch` on the device that runs `stream` (which must be
+// the current device), looked up on the first call on that device.
+int scratch_on_device(void* stream, void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fmhc::hip_status(e);
+  if (stream) {
+    int sdev = 0;
+    e = hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev);
+    if (e != hipSuccess) return fmhc::hip_status(e);
+    if (sdev != dev) return FMHC_ERR_INVALID_ARGUMENT;
+  }
+  if (dev < 0 || dev >= kMaxDevices) return FMHC_ERR_INVALID_ARGUMENT;
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (!scratch_addr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return fmhc::hip_status(e);
+    if (!p) return FMHC_ERR_HIP_BASE + static_cast<int>(hipErrorInvalidSymbol);
+    scratch_addr[dev] = p;
+  }
+  *out = scratch_addr[dev];
+  return FMHC_OK;
+}
+
+}  // namespace
+
+extern "C" int fmhc_premap_fwd(const uint16_t* x, const uint16_t* W, const void* alpha_pre,
+                               const void* alpha_post, const void* alpha_res, const void* bias,
+                               const void* perm, int param_dtype, uint16_t* layer_input, uint16_t* proj,
+                               float* inv_rms, float* h_pre, float* h_post, float* H_merged,
+                               uint16_t* zero_word_a, uint16_t* zero_word_b, void* workspace,
+                               int64_t workspace_bytes, int64_t T, int64_t C, int64_t n, void* stream) {
+  return premap_fwd_run(x, W, alpha_pre, alpha_post, alpha_res, bias, perm, param_dtype, layer_input, proj,
+                        inv_rms, h_pre, h_post, H_merged, zero_word_a, zero_word_b, workspace, workspace_bytes,
+                        T, C, n, stream);
+}
+
+extern "C" int fmhc_premap_fwd_noalloc(const uint16_t* x, const uint16_t* W, const void* alpha_pre,
+                                       const void* alpha_post, const void* alpha_res, const void* bias,
+                                       const void* perm, int param_dtype, uint16_t* layer_input,
+                                       uint16_t* proj, float* inv_rms, float* h_pre, float* h_post,
+                                       float* H_merged, uint16_t* zero_word_a, uint16_t* zero_word_b,
+                                       int64_t T, int64_t C, int64_t n, void* stream) {
+  if (T < 0 || C <= 0 || n != 4) return FMHC_ERR_INVALID_ARGUMENT;
+  if (T == 0) return FMHC_OK;
+  const int64_t need = fmhc_premap_fwd_workspace_bytes(T, C);
+  if (need > kNoAllocScratchBytes) return FMHC_ERR_SCRATCH_LIMIT;
+  void* ws = nullptr;
+  if (need > 0) {
+    const int st = scratch_on_device(stream, &ws);
+    if (st != FMHC_OK) return st;
+  }
+  return premap_fwd_run(x, W, alpha_pre, alpha_post, alpha_res, bias, perm, param_dtype, layer_input, proj,
+                        inv_rms, h_pre, h_post, H_merged, zero_word_a, zero_word_b, ws,
+                        need > 0 ? kNoAllocScratchBytes : 0, T, C, n, stream);
 }
 
 extern "C" int64_t fmhc_premap_bwd_workspace_bytes(int64_t T, int64_t C) {

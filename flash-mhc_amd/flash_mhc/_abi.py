@@ -37,6 +37,7 @@ SIGNATURES: dict[str, list] = {
     "fmhc_k2_bwd_workspace_bytes": [_I64],
     "fmhc_premap_fwd": [_P] * 7 + [_INT] + [_P] * 9 + [_I64, _I64, _I64, _I64, _P],
     "fmhc_premap_fwd_workspace_bytes": [_I64, _I64],
+    "fmhc_premap_fwd_noalloc": [_P] * 7 + [_INT] + [_P] * 8 + [_I64, _I64, _I64, _P],
     "fmhc_premap_bwd": [_P] * 7 + [_INT] + [_P] * 14 + [_I64, _I64, _I64, _I64, _P],
     "fmhc_premap_bwd_workspace_bytes": [_I64, _I64],
     "fmhc_k3_fwd": [_P, _P, _P, _I64, _I64, _I64, _P],
@@ -55,7 +56,7 @@ RESTYPES = {
     "fmhc_premap_bwd_workspace_bytes": ctypes.c_int64,
 }
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -12,7 +12,8 @@
  *   - Sizes are int64_t.  T == 0 is valid and launches nothing.
  *   - `stream` is a hipStream_t (NULL = the legacy default stream).  Work is
  *     enqueued asynchronously; nothing blocks the host.
- *   - The library allocates no memory and keeps no state between calls.
+ *   - The library allocates no memory.  It keeps no state between calls,
+ *     except fmhc_premap_fwd_noalloc's static scratch array (below).
  *     Every element of every output is written.
  *   - n (streams per token) must be 4 and D_out (K1 projection width) must be
  *     32, matching the reference's n = 4 specialisation.
@@ -33,9 +34,10 @@ extern "C" {
 
 #define FMHC_OK 0
 #define FMHC_ERR_INVALID_ARGUMENT 1 /* negative size, n != 4, D_out != 32, null pointer */
+#define FMHC_ERR_SCRATCH_LIMIT 2    /* fmhc_premap_fwd_noalloc: shape needs more than its scratch */
 #define FMHC_ERR_HIP_BASE 1000      /* + hipError_t from the launch */
 
-#define FMHC_ABI_VERSION 6
+#define FMHC_ABI_VERSION 7
 
 /* Storage dtype of the block parameters K2 reads (alpha_pre, alpha_post,
  * alpha_res, bias, perm: all five the same) and of their gradients. */
@@ -50,7 +52,7 @@ extern "C" {
  *           src/flash_mhc/kernels.py:250-303 (_fused_rmsnorm_project_fwd_kernel). */
 int fmhc_k1_fwd(const uint16_t* x_flat, const uint16_t* W, uint16_t* out, float* inv_rms,
                 int64_t T, int64_t nC, int64_t D_out, void* stream);
-/* fmhc_k1_fwd with a workspace: for few tokens (T < 8192) the nC axis is split
+/* fmhc_k1_fwd with a workspace: for few tokens (T <= 2048) the nC axis is split
  * over up to 64 workgroups per 16-token block, whose fp32 partial sums (in
  * `workspace`) a second kernel adds in a fixed order.  `workspace`: at least
  * fmhc_k1_fwd_workspace_bytes(T, nC) bytes, 16-byte aligned (may be NULL when
@@ -145,6 +147,27 @@ int fmhc_premap_fwd(const uint16_t* x, const uint16_t* W, const void* alpha_pre,
 /* Workspace bytes fmhc_premap_fwd needs (fmhc_k1_fwd_workspace_bytes(T, 4 C);
  * 0: workspace may be NULL).  No counterpart in the reference. */
 int64_t fmhc_premap_fwd_workspace_bytes(int64_t T, int64_t C);
+/* fmhc_premap_fwd without a workspace argument, allocating nothing: no
+ * hipMalloc / hipFree or allocating library call on any path.  No counterpart
+ * in the reference; it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation).  The few-token forward's partial sums go to a static 4 MiB
+ * device array of the library (one per device, held until the process ends),
+ * which covers every shape (at most 2,145,792 bytes are needed, at T = 2032,
+ * C = 160); a shape needing more returns FMHC_ERR_SCRATCH_LIMIT.  The array's
+ * device address is looked up on the first call on each device.  `stream`
+ * must belong to the current device (else FMHC_ERR_INVALID_ARGUMENT).  Every
+ * call on a device shares that device's array and overwrites what the last
+ * call left there (every partial it reads was written by the same call, so
+ * nothing needs clearing): calls that overlap on one device (on different
+ * streams, or from several host threads without ordering) race.  Outputs
+ * are bit-identical to fmhc_premap_fwd's. */
+int fmhc_premap_fwd_noalloc(const uint16_t* x, const uint16_t* W, const void* alpha_pre,
+                            const void* alpha_post, const void* alpha_res, const void* bias,
+                            const void* perm, int param_dtype, uint16_t* layer_input, uint16_t* proj,
+                            float* inv_rms, float* h_pre, float* h_post, float* H_merged,
+                            uint16_t* zero_word_a, uint16_t* zero_word_b, int64_t T, int64_t C,
+                            int64_t n, void* stream);
 /* Pre-map backward: the gradients of fmhc_premap_fwd's inputs from those of
  * layer_input (T, C) bf16, h_post (T, 4) and H_merged (T, 4, 4) fp32 (the
  * latter two may be NULL: zero):

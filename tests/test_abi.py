@@ -82,6 +82,7 @@ def test_loads_and_reports_version():
     assert lib.fmhc_error_string(0) == b"ok"
     assert b"invalid argument" in lib.fmhc_error_string(1)
     assert lib.fmhc_error_string(123) == b"unknown flash_mhc status"
+    assert b"no-allocation" in lib.fmhc_error_string(2)
 
 
 _FAKE = 4096  # a non-null address that the host-side checks never dereference
@@ -105,6 +106,8 @@ _FAKE = 4096  # a non-null address that the host-side checks never dereference
         lambda L: L.fmhc_k2_fwd(*[_FAKE] * 6, 2, *[_FAKE] * 3, 8, 4, None),
         lambda L: L.fmhc_k2_fwd(*[None] * 6, 0, *[None] * 3, 8, 4, None),  # null parameters
         lambda L: L.fmhc_premap_fwd(*[_FAKE] * 7, -1, *[_FAKE] * 6, None, None, None, 0, 8, 16, 4, None),
+        lambda L: L.fmhc_premap_fwd_noalloc(*[_FAKE] * 7, 0, *[_FAKE] * 6, None, None, 8, 16, 5, None),  # n != 4
+        lambda L: L.fmhc_premap_fwd_noalloc(*[_FAKE] * 7, 0, *[_FAKE] * 6, None, None, -3, 16, 4, None),
     ],
 )
 def test_invalid_arguments_rejected_before_launch(call):
