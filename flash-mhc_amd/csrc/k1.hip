@@ -35,6 +35,15 @@ namespace {
 constexpr int kDout = 32;
 constexpr float kEps = kRmsEps;
 
+// Evidence build (build.py, variant "k1_valu"): the two K1 contractions run as
+// fp32 FMAs on the VALU instead of on the matrix cores, with the same tiles,
+// loads, LDS transposes and pipeline, so that the two can be timed against
+// each other.  The product library is built with the matrix cores.
+#ifndef FMHC_K1_VALU
+#define FMHC_K1_VALU 0
+#endif
+constexpr bool kValu = FMHC_K1_VALU != 0;
+
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 
@@ -71,18 +80,17 @@ struct FwdFrag {
 // workgroup writes its fp32 partial sums (32 projections + sum of squares per
 // token) to part[t][33][S4] (S4 = gridDim.y rounded up to 4) instead of the
 // outputs; k1_fwd_finish adds the gridDim.y partials in order.
-// Workgroups whose tokens all lie before nt_end load x with the nontemporal
-// hint (see the chunk loop).
 template <int R, int SPLIT, bool SPLITK>
 __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __restrict__ x,
                                                              const uint16_t* __restrict__ W,
                                                              uint16_t* __restrict__ out,
                                                              float* __restrict__ inv_rms,
                                                              float* __restrict__ part,
-                                                             int64_t T, int nC, int cps, int64_t nt_end) {
+                                                             int64_t T, int nC, int cps) {
   __shared__ float red_acc[SPLIT][R][8][kWave];
   __shared__ float red_ss[SPLIT][R][16];
   __shared__ u32x4 xs[SPLIT][16 * R * 8];  // per wave: 16R tokens x 8 swizzled 16-byte slots
+  __shared__ u32x4 wts[kValu ? SPLIT : 1][kValu ? 32 * 8 : 1];  // VALU build: the W chunk, 32 rows x 8 slots
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
@@ -126,25 +134,21 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
   // concurrent reads of all workgroups over the DRAM channels instead of every
   // workgroup hitting the same column of its 8 KiB-strided rows), and
   // double-buffers: the next chunk's fragments are loaded while the MFMAs of
-  // the current one run.  The nontemporal hint makes this kernel 10% faster
-  // alone, but the next kernel that reads x (K3's forward, K1's backward)
-  // then loses as much, because it no longer finds the tail of x in the
-  // memory-side cache.  So only the head of x, which that cache could not
-  // keep anyway, takes the hint: workgroups before nt_end (the host leaves
-  // the last kFwdCachedTail bytes of x to ordinary loads).  The flag is
-  // uniform per workgroup, and the loop is instantiated once per value: a
-  // select between the two loads would be folded into one ordinary load.
-  // With SPLITK the workgroup's chunks are cbeg .. cbeg + nfull - 1 (no
-  // rotation: the workgroups of one token block already cover different
-  // columns), and only the last split takes the ragged chunk.
+  // the current one run.  x is read once per launch, so its loads carry the
+  // nontemporal hint (8-10% faster than ordinary loads).  With SPLITK (few
+  // tokens) they do not: the pre-map's few-token kernel reads the same x
+  // again right after, from the caches.  With SPLITK the workgroup's chunks
+  // are cbeg .. cbeg + nfull - 1 (no rotation: the workgroups of one token
+  // block already cover different columns), and only the last split takes the
+  // ragged chunk.
   const int nall = nC >> 6;
   const int cbeg = SPLITK ? static_cast<int>(blockIdx.y) * cps : 0;
   const int nfull = SPLITK ? (cps < nall - cbeg ? cps : nall - cbeg) : nall;
   const bool last_split = !SPLITK || blockIdx.y + 1 == gridDim.y;
   const int rot = !SPLITK && nfull > 0 ? static_cast<int>(blockIdx.x % static_cast<unsigned>(nfull)) : 0;
   FwdFrag<R> f0, f1;
-  auto chunk_at = [&](int p) { return cbeg + (p + rot < nfull ? p + rot : p + rot - nfull); };
-  auto load = [&](FwdFrag<R>& f, int p, auto nt) {
+  auto chunk_at = [&](int p) __attribute__((always_inline)) { return cbeg + (p + rot < nfull ? p + rot : p + rot - nfull); };
+  auto load = [&](FwdFrag<R>& f, int p) __attribute__((always_inline)) {
     const int k = chunk_at(p) * 64;
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
@@ -153,7 +157,7 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const u32x4* px = reinterpret_cast<const u32x4*>(xw + xoff[s * R + r] + k);
-        if constexpr (decltype(nt)::value)
+        if constexpr (!SPLITK)
           f.xv[s][r] = __builtin_nontemporal_load(px);
         else
           f.xv[s][r] = *px;
@@ -163,7 +167,7 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
   // Token rows -> MFMA layout (lane: token row, 8 consecutive k) through the
   // wave's LDS tile.  Same-wave LDS operations complete in order, so the
   // next chunk's writes cannot overtake these reads.
-  auto transpose = [&](FwdFrag<R>& f) {
+  auto transpose = [&](FwdFrag<R>& f) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < 2 * R; ++j) xl[64 * j + ((j & 1) ? wr1 : wr0)] = f.xv[j / R][j % R];
 #pragma unroll
@@ -171,7 +175,7 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
 #pragma unroll
       for (int r = 0; r < R; ++r) f.xv[s][r] = xl[128 * r + (s ? rd1 : rd0)];
   };
-  auto compute = [&](const FwdFrag<R>& f) {
+  auto compute_mfma = [&](const FwdFrag<R>& f) __attribute__((always_inline)) {
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
 #pragma unroll
@@ -183,21 +187,66 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
       }
     }
   };
+  // VALU build: lane (grp, row) accumulates, for token `row` of each block,
+  // the outputs d = 4 grp + q and 16 + 4 grp + q (the matrix-core D layout)
+  // over the chunk's 64 k, reading x from the wave's transpose tile and W
+  // from a wave-private copy of the chunk; the sum of squares goes into the
+  // diagonal slot of `gram` that the epilogue reads.
+  float ssq[kValu ? R : 1];
+#pragma unroll
+  for (int r = 0; r < (kValu ? R : 1); ++r) ssq[r] = 0.f;
+  auto compute_valu = [&](const FwdFrag<R>& f, bool mfma_layout) __attribute__((always_inline)) {
+    u32x4* wl = wts[kValu ? wave : 0];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      wl[row * 8 + 4 * s + grp] = f.wa[s];
+      wl[(16 + row) * 8 + 4 * s + grp] = f.wb[s];
+      if (mfma_layout) {  // x is in registers in the matrix-core layout: put it where the tile would hold it
+#pragma unroll
+        for (int r = 0; r < R; ++r) xl[128 * r + (s ? rd1 : rd0)] = f.xv[s][r];
+      }
+    }
+    const int key = (row >> 1) & 7;
+#pragma unroll 1
+    for (int p = 0; p < 8; ++p) {
+      float xv[R][8];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        unpack8(xl[128 * r + row * 8 + (p ^ key)], xv[r]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ssq[r] = __builtin_fmaf(xv[r][e], xv[r][e], ssq[r]);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float w[8];
+        unpack8(wl[(i < 4 ? 4 * grp + i : 12 + 4 * grp + i) * 8 + p], w);
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[i >> 2][r][i & 3] = __builtin_fmaf(w[e], xv[r][e], acc[i >> 2][r][i & 3]);
+      }
+    }
+  };
+  auto compute = [&](const FwdFrag<R>& f, bool mfma_layout = false) __attribute__((always_inline)) {
+    if constexpr (kValu)
+      compute_valu(f, mfma_layout);
+    else
+      compute_mfma(f);
+  };
   // n chunks for this wave, two per trip.  Both prefetches are issued on every
   // path (a clamped index re-reads a cached chunk that is never computed), so
   // the compiler keeps them ahead of the MFMAs; an odd count ends with f0.
   const int n = nfull > wave ? (nfull - wave + SPLIT - 1) / SPLIT : 0;
-  auto pos = [&](int i) { return wave + SPLIT * (i < n ? i : n - 1); };
-  auto chunks = [&](auto nt) {
-    if (n <= 0) return;
-    load(f0, pos(0), nt);
+  auto pos = [&](int i) __attribute__((always_inline)) { return wave + SPLIT * (i < n ? i : n - 1); };
+  if (n > 0) {
+    load(f0, pos(0));
     int i = 0;
     for (; i + 1 < n; i += 2) {
-      load(f1, pos(i + 1), nt);
+      load(f1, pos(i + 1));
       __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the MFMAs
       transpose(f0);
       compute(f0);
-      load(f0, pos(i + 2), nt);
+      load(f0, pos(i + 2));
       __builtin_amdgcn_sched_barrier(0);
       transpose(f1);
       compute(f1);
@@ -206,11 +255,7 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
       transpose(f0);
       compute(f0);
     }
-  };
-  if (t0 + 16 * R <= nt_end)
-    chunks(std::true_type{});
-  else
-    chunks(std::false_type{});
+  }
   // Ragged last chunk (nC % 64 != 0): 16-byte pieces past nC contribute zero.
   if ((nC & 63) != 0 && last_split && wave == nfull % SPLIT) {
     const int k = nall * 64;
@@ -231,9 +276,16 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
         }
       }
     }
-    compute(f0);
+    compute(f0, true);
   }
 
+  if constexpr (kValu) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int qd = row & 3;
+      gram[r] = f32x4{qd == 0 ? ssq[r] : 0.f, qd == 1 ? ssq[r] : 0.f, qd == 2 ? ssq[r] : 0.f, qd == 3 ? ssq[r] : 0.f};
+    }
+  }
   // Diagonal G[row][row] sits in lane row + 16 * (row >> 2), register row & 3.
   const int q_diag = row & 3;
   const bool holds_diag = grp == (row >> 2);
@@ -363,7 +415,7 @@ struct BwdFrag {
 // operand takes the kernel to one wave per SIMD; it is still bound by HBM
 // (measured: +80 us at T=65536, C=1024 for the 512 MiB it reads, against
 // 260 us for the separate accumulation pass it replaces).
-template <bool DW, bool FULLK, bool EPI, bool GI>
+template <bool DW, bool FULLK, bool EPI, bool GI, int NBUF>
 __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ x,
                                                    const uint16_t* __restrict__ W,
                                                    const uint16_t* __restrict__ go,
@@ -408,6 +460,9 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
 
   __shared__ uint32_t gtile[DW ? 4 : 1][16 * 16];  // wave-private 16 tokens x 32 d bf16
   __shared__ u32x4 btile[EPI ? 4 : 1][EPI ? 8 : 1][EPI ? kWave : 1];  // EPI: wave-private B tiles
+  // VALU build: W[d][kl .. kl + 8) for d = 0..31 and the lane columns, and the token block's go rows.
+  __shared__ u32x4 wvl[kValu ? 4 : 1][kValu ? 32 * 16 : 1];
+  __shared__ u32x4 gvl[kValu ? 4 : 1][kValu ? 16 * 4 : 1];
   // EPI: the lane's stream j and position c (C % 8 == 0: k .. k + 7 stay in one stream).
   const int sj = EPI ? kl / C : 0;
   const uint32_t c3bytes = EPI ? 2u * static_cast<uint32_t>(kl - sj * C) : 0u;
@@ -435,6 +490,10 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
       const u32x4 v = {h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
       bfr[m] = as_bf16x8(v);
       if constexpr (EPI) btile[wave][m][lane] = v;
+    }
+    if constexpr (kValu) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) wvl[wave][(8 * grp + e) * 16 + col] = rows[e];
     }
   }
   // Same-wave LDS writes and reads are ordered: the tiles need no barrier.
@@ -508,9 +567,32 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
       scale[q] = d * (f.inv[q] * f.inv[q]) / static_cast<float>(nC);
     }
     f32x4 acc[8];
-    const bf16x8 a = as_bf16x8(f.gv);
+    if constexpr (kValu) {
+      // VALU build: acc[m][q] = sum_d go[token 4 grp + q][d] * W[d][kl + m] as
+      // fp32 FMAs, go rows and W columns read from the wave's LDS copies.
+      gvl[wave][col * 4 + grp] = f.gv;
 #pragma unroll
-    for (int m = 0; m < 8; ++m) acc[m] = mfma16(a, btile_at(m), f32x4{0.f, 0.f, 0.f, 0.f});
+      for (int m = 0; m < 8; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+      for (int j = 0; j < 4; ++j) {
+        float g[4][8];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) unpack8(gvl[wave][(4 * grp + q) * 4 + j], g[q]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float w[8];
+          unpack8(wvl[wave][(8 * j + e) * 16 + col], w);
+#pragma unroll
+          for (int m = 0; m < 8; ++m)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) acc[m][q] = __builtin_fmaf(g[q][e], w[m], acc[m][q]);
+        }
+      }
+    } else {
+      const bf16x8 a = as_bf16x8(f.gv);
+#pragma unroll
+      for (int m = 0; m < 8; ++m) acc[m] = mfma16(a, btile_at(m), f32x4{0.f, 0.f, 0.f, 0.f});
+    }
     if (kok) {
       char* gxb = reinterpret_cast<char*>(gx + tbase * nC);
 #pragma unroll
@@ -583,18 +665,40 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
       }
     }
   };
+  // NBUF = 3: two blocks in flight while one computes (three rotating
+  // fragments, three blocks per trip); NBUF = 2: one.
   BwdFrag<EPI, GI> f0, f1;
-  load(f0, 0);
-  int i = 0;
-  for (; i + 1 < nb; i += 2) {
-    load(f1, pos(i + 1));
-    __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the compute
-    compute(f0, i);
-    load(f0, pos(i + 2));
-    __builtin_amdgcn_sched_barrier(0);
-    compute(f1, i + 1);
+  if constexpr (NBUF == 3) {
+    BwdFrag<EPI, GI> f2;
+    load(f0, 0);
+    load(f1, pos(1));
+    int i = 0;
+    for (; i + 2 < nb; i += 3) {
+      load(f2, pos(i + 2));
+      __builtin_amdgcn_sched_barrier(0);  // keep the prefetches ahead of the compute
+      compute(f0, i);
+      load(f0, pos(i + 3));
+      __builtin_amdgcn_sched_barrier(0);
+      compute(f1, i + 1);
+      load(f1, pos(i + 4));
+      __builtin_amdgcn_sched_barrier(0);
+      compute(f2, i + 2);
+    }
+    if (i < nb) compute(f0, i);
+    if (i + 1 < nb) compute(f1, i + 1);
+  } else {
+    load(f0, 0);
+    int i = 0;
+    for (; i + 1 < nb; i += 2) {
+      load(f1, pos(i + 1));
+      __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the compute
+      compute(f0, i);
+      load(f0, pos(i + 2));
+      __builtin_amdgcn_sched_barrier(0);
+      compute(f1, i + 1);
+    }
+    if (i < nb) compute(f0, i);
   }
-  if (i < nb) compute(f0, i);
 
   if constexpr (DW) {
     // Partial layout [run][slice][m][h][r][lane]: one 256-byte row per store.
@@ -757,16 +861,6 @@ constexpr int kFwdSplit = 4;  // waves per workgroup (split of the nC axis)
 constexpr int kFwdR = 4;
 constexpr int kFwdRSmall = 2;
 constexpr int64_t kFwdLargeT = 16384;
-// Bytes at the end of x that the one-pass forward reads with ordinary loads,
-// so that the next kernel over x finds them in the 256 MB memory-side cache;
-// the tokens before them take the nontemporal hint.  In the six-kernel step
-// (K1 forward, then K1's backward over the same x) against ordinary loads
-// throughout: K1 forward 99 -> 92.5 us, the step 0.8% faster at T = 65536,
-// C = 1024; the step 1.0% faster at T = 16384, C = 4096 with 384 MiB (0.5%
-// with 256).  A tail of 128 MiB or none costs K1's backward more (up to
-// 29 us) than the forward saves.
-constexpr int64_t kFwdCachedTail = int64_t{320} << 20;
-int64_t k1_fwd_nt_end(int64_t T, int64_t nC) { return T - kFwdCachedTail / (2 * nC); }
 // Split forward for few tokens: one 16-token block per workgroup and up to
 // kSplitMax column ranges per block, aiming at kSplitTarget workgroups; taken
 // when the plan has at least kSplitMinS ranges (T <= 2048): from there on the
@@ -779,8 +873,13 @@ constexpr int64_t kSplitMinS = 4;
 // alone, kBwdDwNTB with grad_W (fewer runs, fewer grad_W partials); with few
 // tokens, runs as short as kBwdDwMinNTB blocks with grad_W (its partials then
 // stay below x's bytes) or one block without.
-constexpr int kBwdNTB = 16;
+constexpr int kBwdNTB = 8;
 constexpr int kBwdDwNTB = 64;
+// Fragments in flight in k1_bwd_mfma's block loop (two blocks load while one
+// computes): the K1 op kernels, and the pre-map variants (EPI), whose extra
+// operands leave no registers for a third buffer at two waves per SIMD.
+constexpr int kBwdBufs = 3;
+constexpr int kBwdEpiBufs = 2;
 constexpr int kBwdDwMinNTB = 4;
 constexpr int64_t kBwdFillWaves = 1024;  // one wave per SIMD of 256 CUs
 
@@ -834,18 +933,18 @@ int k1_fwd_run(const uint16_t* x_flat, const uint16_t* W, uint16_t* out, float* 
       float* part = static_cast<float*>(ws);
       const dim3 grid(blocks_for(T, 16 * kSplitR), p.S);
       k1_fwd_mfma<kSplitR, kFwdSplit, true><<<grid, kWave * kFwdSplit, 0, s>>>(x_flat, W, out, inv_rms, part,
-                                                                              T, nc, p.cps, 0);
+                                                                              T, nc, p.cps);
       const int st = launch_status();
       if (st != FMHC_OK) return st;
       k1_fwd_finish<<<dim3(blocks_for(T, 4)), 256, 0, s>>>(part, out, inv_rms, T, nc, p.S);
     } else if (T >= kFwdLargeT) {
       const dim3 grid(blocks_for(T, 16 * kFwdR));
       k1_fwd_mfma<kFwdR, kFwdSplit, false><<<grid, kWave * kFwdSplit, 0, s>>>(x_flat, W, out, inv_rms, nullptr,
-                                                                             T, nc, 0, k1_fwd_nt_end(T, nC));
+                                                                             T, nc, 0);
     } else {
       const dim3 grid(blocks_for(T, 16 * kFwdRSmall));
       k1_fwd_mfma<kFwdRSmall, kFwdSplit, false><<<grid, kWave * kFwdSplit, 0, s>>>(
-          x_flat, W, out, inv_rms, nullptr, T, nc, 0, k1_fwd_nt_end(T, nC));
+          x_flat, W, out, inv_rms, nullptr, T, nc, 0);
     }
   } else {
     const dim3 grid(blocks_for(T, 4));
@@ -878,12 +977,13 @@ void launch_k1_bwd_mfma(hipStream_t s, const uint16_t* x, const uint16_t* W, con
                         int nslices, int64_t nruns, const uint16_t* go3 = nullptr, const float* h_pre = nullptr,
                         int C = 1, const uint16_t* gi = nullptr) {
   const dim3 grid(blocks_for(nruns * nslices, 4));
+  constexpr int nbuf = EPI ? kBwdEpiBufs : kBwdBufs;
   if (nC % 128 == 0)
-    k1_bwd_mfma<DW, true, EPI, GI><<<grid, 256, 0, s>>>(x, W, go, proj, inv_rms, gx, partial, go3, h_pre, gi, T,
-                                                        nC, nslices, nruns, C);
+    k1_bwd_mfma<DW, true, EPI, GI, nbuf><<<grid, 256, 0, s>>>(x, W, go, proj, inv_rms, gx, partial, go3, h_pre, gi,
+                                                              T, nC, nslices, nruns, C);
   else
-    k1_bwd_mfma<DW, false, EPI, GI><<<grid, 256, 0, s>>>(x, W, go, proj, inv_rms, gx, partial, go3, h_pre, gi, T,
-                                                         nC, nslices, nruns, C);
+    k1_bwd_mfma<DW, false, EPI, GI, nbuf><<<grid, 256, 0, s>>>(x, W, go, proj, inv_rms, gx, partial, go3, h_pre,
+                                                               gi, T, nC, nslices, nruns, C);
 }
 
 }  // namespace
@@ -992,7 +1092,7 @@ int k1_fwd_partials(const uint16_t* x_flat, const uint16_t* W, void* ws, int64_t
   if (!ws || ws_bytes < p.bytes || !aligned16(ws)) return -FMHC_ERR_INVALID_ARGUMENT;
   const dim3 grid(blocks_for(T, 16 * kSplitR), p.S);
   k1_fwd_mfma<kSplitR, kFwdSplit, true><<<grid, kWave * kFwdSplit, 0, s>>>(
-      x_flat, W, nullptr, nullptr, static_cast<float*>(ws), T, static_cast<int>(nC), p.cps, 0);
+      x_flat, W, nullptr, nullptr, static_cast<float*>(ws), T, static_cast<int>(nC), p.cps);
   const int st = launch_status();
   return st == FMHC_OK ? p.S : -st;
 }

@@ -1,6 +1,8 @@
 """Build the gfx950 HIP extension ``_lib/libflash_mhc_hip.so`` in-tree, and
 beside it ``_lib/libflash_mhc_probe.so``, the bandwidth probe and cache flush
-that only bench.py loads (include/flash_mhc_probe.h; not part of the path).
+that only bench.py loads (include/flash_mhc_probe.h; not part of the path),
+and the evidence variants of VARIANTS (``_lib/libflash_mhc_hip_<name>.so``,
+same ABI; nothing loads them unless FLASH_MHC_HIP_LIB names one).
 
 Usage: ``python -m flash_mhc.build`` (run from ``flash-mhc_amd/``) or
 ``flash_mhc.build.build()``.  hipcc cross-compiles for gfx950 without a GPU.
@@ -53,6 +55,15 @@ COMMON_FLAGS = [
 # loop-carried weight-gradient accumulators in VGPRs and copies them to and
 # from AGPRs around every MFMA, which doubles the kernel's register footprint.
 SOURCE_FLAGS = {"k1.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+# Evidence builds of the same library, selected at compile time.  k1_valu: the
+# K1 forward and backward-dx contractions as fp32 FMAs on the VALU instead of
+# the matrix cores (same tiles, loads and pipeline), to time the two.
+VARIANTS = {"k1_valu": ["-DFMHC_K1_VALU=1"]}
+
+
+def variant_path(name: str) -> Path:
+    return LIB_DIR / f"libflash_mhc_hip_{name}.so"
 
 
 def hipcc() -> str:
@@ -113,6 +124,14 @@ def build(verbose: bool = False, extra_flags: list[str] | None = None, out: Path
     return out
 
 
+def build_all(verbose: bool = False) -> Path:
+    """The product library, the probe library and every evidence variant."""
+    path = build(verbose=verbose)
+    for name, flags in VARIANTS.items():
+        build(verbose=verbose, extra_flags=flags, out=variant_path(name), probe=False)
+    return path
+
+
 if __name__ == "__main__":
-    path = build(verbose="-v" in sys.argv)
+    path = build_all(verbose="-v" in sys.argv)
     print(path)

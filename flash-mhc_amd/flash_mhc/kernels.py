@@ -34,6 +34,13 @@ _F32 = torch.float32
 
 
 def _require(t: torch.Tensor, name: str, dtype: torch.dtype, shape: tuple[int, ...], device) -> None:
+    # One compound test on the common path; the messages come from _reject.
+    if (not isinstance(t, torch.Tensor) or t.dtype is not dtype or t.shape != shape or t.device != device
+            or not t.is_contiguous()):
+        _reject(t, name, dtype, shape, device)
+
+
+def _reject(t, name: str, dtype: torch.dtype, shape: tuple[int, ...], device) -> None:
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"{name} must be a torch.Tensor")
     if t.device != device:
@@ -42,8 +49,7 @@ def _require(t: torch.Tensor, name: str, dtype: torch.dtype, shape: tuple[int, .
         raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
     if t.shape != shape:  # torch.Size compares equal to a tuple of the same ints
         raise ValueError(f"{name} must have shape {tuple(shape)}, got {tuple(t.shape)}")
-    if not t.is_contiguous():
-        raise ValueError(f"{name} must be contiguous")
+    raise ValueError(f"{name} must be contiguous")
 
 
 def _device_of(x: torch.Tensor) -> torch.device:
@@ -60,7 +66,8 @@ class _OnDevice:
     __slots__ = ("idx", "prev")
 
     def __init__(self, device: torch.device):
-        self.idx = device.index if device.index is not None else torch.cuda.current_device()
+        idx = device.index
+        self.idx = torch.cuda.current_device() if idx is None else idx
         self.prev = None
 
     def __enter__(self):
@@ -273,6 +280,52 @@ def premap_fwd(x_streams: torch.Tensor, W: torch.Tensor, alpha_pre: torch.Tensor
     return li, H, h_post, h_pre, proj, inv
 
 
+_PREMAP_WS_BYTES: dict[tuple[int, int], int] = {}
+
+
+def _premap_ws_bytes(lib, T: int, C: int) -> int:
+    key = (T, C)
+    n = _PREMAP_WS_BYTES.get(key)
+    if n is None:
+        if len(_PREMAP_WS_BYTES) > 4096:
+            _PREMAP_WS_BYTES.clear()
+        n = _PREMAP_WS_BYTES[key] = int(lib.fmhc_premap_fwd_workspace_bytes(T, C))
+    return n
+
+
+def premap_fwd_eval(x_streams: torch.Tensor, W: torch.Tensor, alpha_pre: torch.Tensor,
+                    alpha_post: torch.Tensor, alpha_res: torch.Tensor, bias: torch.Tensor,
+                    perm: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """premap_fwd for a forward that keeps only (layer_input, H_merged, h_post):
+    the same launch, with h_pre, proj, inv_rms and the workspace carved out of
+    one scratch allocation that is released after the call (stream-ordered,
+    as every temporary of the caching allocator)."""
+    T, n, C = _streams_shape(x_streams)
+    dev = _device_of(x_streams)
+    _require(x_streams, "x_streams", _BF16, (T, n, C), dev)
+    _require(W, "W", _BF16, (D_OUT, n * C), dev)
+    pdt = _k2_params(alpha_pre, alpha_post, alpha_res, bias, perm, dev)
+    lib = _abi.load()
+    ws_bytes = _premap_ws_bytes(lib, T, C)
+    li = torch.empty((T, C), device=dev, dtype=_BF16)
+    H = torch.empty((T, n, n), device=dev, dtype=_F32)
+    h_post = torch.empty((T, n), device=dev, dtype=_F32)
+    # scratch: h_pre (T, 4) fp32 | inv_rms (T,) fp32 | proj (T, 32) bf16 | workspace, 16-byte aligned pieces
+    o_inv = 16 * T
+    o_proj = (o_inv + 4 * T + 15) // 16 * 16
+    o_ws = (o_proj + 2 * D_OUT * T + 255) // 256 * 256
+    scratch = torch.empty((o_ws + ws_bytes,), device=dev, dtype=torch.uint8)
+    base = scratch.data_ptr()
+    with _OnDevice(dev):
+        st = lib.fmhc_premap_fwd(x_streams.data_ptr(), W.data_ptr(), alpha_pre.data_ptr(),
+                                 alpha_post.data_ptr(), alpha_res.data_ptr(), bias.data_ptr(),
+                                 perm.data_ptr(), pdt, li.data_ptr(), base + o_proj, base + o_inv, base,
+                                 h_post.data_ptr(), H.data_ptr(), None, None,
+                                 base + o_ws if ws_bytes else None, ws_bytes, T, C, n, _abi.stream_of(x_streams))
+    _abi.check(st, "premap_fwd")
+    return li, H, h_post
+
+
 def premap_bwd(x_streams: torch.Tensor, W: torch.Tensor, alpha_pre: torch.Tensor,
                alpha_post: torch.Tensor, alpha_res: torch.Tensor, bias: torch.Tensor,
                perm: torch.Tensor, h_pre: torch.Tensor, proj: torch.Tensor, inv_rms: torch.Tensor,
@@ -387,6 +440,26 @@ def k4_fwd(x_streams: torch.Tensor, layer_output: torch.Tensor, H_merged: torch.
     if out is None:
         out = torch.empty_like(x_streams)
     _require(out, "out", _BF16, (T, n, C), dev)
+    lib = _abi.load()
+    with _OnDevice(dev):
+        st = lib.fmhc_k4_fwd(x_streams.data_ptr(), layer_output.data_ptr(), H_merged.data_ptr(),
+                             h_post.data_ptr(), out.data_ptr(), T, C, n, _abi.stream_of(x_streams))
+    _abi.check(st, "k4_fwd")
+    return out
+
+
+def k4_fwd_eval(x_streams: torch.Tensor, layer_output: torch.Tensor, H_merged: torch.Tensor,
+                h_post: torch.Tensor) -> torch.Tensor:
+    """k4_fwd for the no-autograd forward, whose H_merged and h_post come from
+    premap_fwd_eval of the same x_streams (fresh fp32 (T, 4, 4) / (T, 4)
+    buffers): those two are checked for shape only."""
+    dev = _device_of(x_streams)
+    T, n, C = _streams_shape(x_streams)
+    _require(x_streams, "x_streams", _BF16, (T, n, C), dev)
+    _require(layer_output, "layer_output", _BF16, (T, C), dev)
+    if H_merged.shape != (T, n, n) or h_post.shape != (T, n):
+        raise ValueError("H_merged / h_post do not match x_streams")
+    out = torch.empty_like(x_streams)
     lib = _abi.load()
     with _OnDevice(dev):
         st = lib.fmhc_k4_fwd(x_streams.data_ptr(), layer_output.data_ptr(), H_merged.data_ptr(),

@@ -314,6 +314,24 @@ def _mhc_pre_map_cuda(x_streams, W, alpha_pre, alpha_post, alpha_res, bias, perm
     return (*outs, x_sink)
 
 
+def pre_map_nograd(x_streams, W, alpha_pre, alpha_post, alpha_res, bias, perm_mat):
+    """(layer_input, H_merged, h_post) of mhc_pre_map without the op's
+    dispatch, for forwards that record no autograd graph: the same kernels and
+    conversions as the op's device implementation, so the same values, with
+    the outputs nobody reads (h_pre, proj, inv_rms) kept in scratch memory."""
+    _check_n4(x_streams, "flash_mhc::mhc_pre_map supports n=4 only")
+    _check_k2_shapes((0, W.shape[0]), perm_mat)
+    return _k.premap_fwd_eval(x_streams.contiguous(), W.to(x_streams.dtype).contiguous(),
+                              *_params(alpha_pre, alpha_post, alpha_res, bias, perm_mat))
+
+
+def post_res_nograd(x_streams, layer_output, H_merged, h_post):
+    """fused_post_res's device implementation without the op's dispatch, for
+    H_merged and h_post from pre_map_nograd of the same x_streams."""
+    _check_n4(x_streams, "flash_mhc::fused_post_res currently supports n=4 only")
+    return _k.k4_fwd_eval(x_streams.contiguous(), layer_output.contiguous(), H_merged, h_post)
+
+
 @torch.library.impl(_lib, "mhc_pre_map_coeffs", "CUDA")
 def _mhc_pre_map_coeffs_cuda(x_streams, W, alpha_pre, alpha_post, alpha_res, bias, perm_mat):
     _check_n4(x_streams, "flash_mhc::mhc_pre_map_coeffs supports n=4 only")
@@ -413,8 +431,12 @@ def _setup_k1(ctx, inputs, output):
     ctx.save_for_backward(x_flat, W, out, inv_rms)
 
 
+_OFF = frozenset({"0", "false", "off", "no"})
+
+
 def _env_flag(name: str) -> bool:
-    return os.getenv(name, "1").strip().lower() not in {"0", "false", "off", "no"}
+    v = os.environ.get(name)
+    return v is None or v.strip().lower() not in _OFF
 
 
 def _fused_dw_enabled() -> bool:

@@ -342,3 +342,21 @@ def test_empty_batch_forward_backward(ckpt):
         assert p.grad is None or float(p.grad.float().abs().sum()) == 0.0, name
     with torch.no_grad():
         assert blk.eval()(x.detach()).shape == (0, 4, C)
+
+
+@pytest.mark.parametrize("T,C", [(1, 4096), (64, 4096), (257, 1024), (5000, 1024), (333, 100)])
+def test_nograd_forward_equals_op_path(T, C):
+    """Without autograd the block launches the pre-map and post-res kernels
+    directly (no custom-op dispatch): the same bits as the op path that a
+    forward recording a graph takes, in eval and in training mode."""
+    torch.manual_seed(7)
+    blk = flash_mhc.MHCLiteBlock(4, C, torch.nn.Linear(C, C, bias=False)).to(DEV, BF16)
+    x = randn((T, 4, C), 70 + T, dtype=BF16).to(DEV)
+    for training in (False, True):
+        blk.train(training)
+        with torch.no_grad():
+            fast = blk(x)
+        with torch.enable_grad():
+            ops_path = blk(x.clone().requires_grad_(True)).detach()
+        torch.cuda.synchronize()
+        assert torch.equal(fast, ops_path), (T, C, training)
