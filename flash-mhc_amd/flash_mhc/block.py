@@ -253,11 +253,11 @@ class MHCLiteBlock(nn.Module):
         each call (tens of microseconds per call at few tokens).  Same
         kernels, same values."""
         p = self._parameters
-        layer_input, H_merged, h_post = _ops.pre_map_nograd(
+        layer_input, coeffs = _ops.pre_map_nograd(
             x_streams, self._projection_weight(x_streams.dtype), p["alpha_pre"], p["alpha_post"], p["alpha_res"],
             self.W_all.bias, self._buffers["perm_mat"])
         layer_output = self.layer(layer_input, **kwargs)
-        return _ops.post_res_nograd(x_streams, layer_output, H_merged, h_post)
+        return _ops.post_res_nograd(x_streams, layer_output, coeffs)
 
     # -- common driver ------------------------------------------------------
 

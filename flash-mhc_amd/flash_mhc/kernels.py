@@ -295,11 +295,13 @@ def _premap_ws_bytes(lib, T: int, C: int) -> int:
 
 def premap_fwd_eval(x_streams: torch.Tensor, W: torch.Tensor, alpha_pre: torch.Tensor,
                     alpha_post: torch.Tensor, alpha_res: torch.Tensor, bias: torch.Tensor,
-                    perm: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """premap_fwd for a forward that keeps only (layer_input, H_merged, h_post):
-    the same launch, with h_pre, proj, inv_rms and the workspace carved out of
-    one scratch allocation that is released after the call (stream-ordered,
-    as every temporary of the caching allocator)."""
+                    perm: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """premap_fwd for a forward that records no autograd graph: the same
+    launch, returning (layer_input, coeffs).  coeffs is one uint8 scratch
+    buffer that holds H_merged (T, 4, 4) fp32 at byte 0 and h_post (T, 4)
+    fp32 at byte 64 T, the inputs k4_fwd_eval reads, followed by h_pre, proj,
+    inv_rms and the workspace, which nothing reads after the call: one
+    allocation instead of six."""
     T, n, C = _streams_shape(x_streams)
     dev = _device_of(x_streams)
     _require(x_streams, "x_streams", _BF16, (T, n, C), dev)
@@ -308,22 +310,20 @@ def premap_fwd_eval(x_streams: torch.Tensor, W: torch.Tensor, alpha_pre: torch.T
     lib = _abi.load()
     ws_bytes = _premap_ws_bytes(lib, T, C)
     li = torch.empty((T, C), device=dev, dtype=_BF16)
-    H = torch.empty((T, n, n), device=dev, dtype=_F32)
-    h_post = torch.empty((T, n), device=dev, dtype=_F32)
-    # scratch: h_pre (T, 4) fp32 | inv_rms (T,) fp32 | proj (T, 32) bf16 | workspace, 16-byte aligned pieces
-    o_inv = 16 * T
+    # H_merged | h_post | h_pre | inv_rms | proj | workspace, 16-byte aligned pieces
+    o_hq, o_hp, o_inv = 64 * T, 80 * T, 96 * T
     o_proj = (o_inv + 4 * T + 15) // 16 * 16
     o_ws = (o_proj + 2 * D_OUT * T + 255) // 256 * 256
-    scratch = torch.empty((o_ws + ws_bytes,), device=dev, dtype=torch.uint8)
-    base = scratch.data_ptr()
+    coeffs = torch.empty((o_ws + ws_bytes,), device=dev, dtype=torch.uint8)
+    base = coeffs.data_ptr()
     with _OnDevice(dev):
         st = lib.fmhc_premap_fwd(x_streams.data_ptr(), W.data_ptr(), alpha_pre.data_ptr(),
                                  alpha_post.data_ptr(), alpha_res.data_ptr(), bias.data_ptr(),
-                                 perm.data_ptr(), pdt, li.data_ptr(), base + o_proj, base + o_inv, base,
-                                 h_post.data_ptr(), H.data_ptr(), None, None,
+                                 perm.data_ptr(), pdt, li.data_ptr(), base + o_proj, base + o_inv, base + o_hp,
+                                 base + o_hq, base, None, None,
                                  base + o_ws if ws_bytes else None, ws_bytes, T, C, n, _abi.stream_of(x_streams))
     _abi.check(st, "premap_fwd")
-    return li, H, h_post
+    return li, coeffs
 
 
 def premap_bwd(x_streams: torch.Tensor, W: torch.Tensor, alpha_pre: torch.Tensor,
@@ -448,22 +448,21 @@ def k4_fwd(x_streams: torch.Tensor, layer_output: torch.Tensor, H_merged: torch.
     return out
 
 
-def k4_fwd_eval(x_streams: torch.Tensor, layer_output: torch.Tensor, H_merged: torch.Tensor,
-                h_post: torch.Tensor) -> torch.Tensor:
-    """k4_fwd for the no-autograd forward, whose H_merged and h_post come from
-    premap_fwd_eval of the same x_streams (fresh fp32 (T, 4, 4) / (T, 4)
-    buffers): those two are checked for shape only."""
+def k4_fwd_eval(x_streams: torch.Tensor, layer_output: torch.Tensor, coeffs: torch.Tensor) -> torch.Tensor:
+    """k4_fwd with H_merged and h_post read from premap_fwd_eval's coeffs
+    buffer for the same x_streams."""
     dev = _device_of(x_streams)
     T, n, C = _streams_shape(x_streams)
     _require(x_streams, "x_streams", _BF16, (T, n, C), dev)
     _require(layer_output, "layer_output", _BF16, (T, C), dev)
-    if H_merged.shape != (T, n, n) or h_post.shape != (T, n):
-        raise ValueError("H_merged / h_post do not match x_streams")
+    if coeffs.dtype is not torch.uint8 or coeffs.numel() < 80 * T or coeffs.device != dev:
+        raise ValueError("coeffs is not premap_fwd_eval's buffer for these tokens")
     out = torch.empty_like(x_streams)
     lib = _abi.load()
+    base = coeffs.data_ptr()
     with _OnDevice(dev):
-        st = lib.fmhc_k4_fwd(x_streams.data_ptr(), layer_output.data_ptr(), H_merged.data_ptr(),
-                             h_post.data_ptr(), out.data_ptr(), T, C, n, _abi.stream_of(x_streams))
+        st = lib.fmhc_k4_fwd(x_streams.data_ptr(), layer_output.data_ptr(), base, base + 64 * T,
+                             out.data_ptr(), T, C, n, _abi.stream_of(x_streams))
     _abi.check(st, "k4_fwd")
     return out
 

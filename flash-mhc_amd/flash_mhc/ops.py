@@ -247,12 +247,15 @@ def _coeff(t: torch.Tensor) -> torch.Tensor:
     return t.to(torch.float32).contiguous()
 
 
-def _params(*ts: torch.Tensor) -> list[torch.Tensor]:
+def _params(*ts: torch.Tensor):
     """K2's parameters (alphas, bias, perm) as the kernels take them: in their
     own dtype when all are fp32 or all bf16 (no conversion launches), else fp32."""
     dt = ts[0].dtype
-    if dt in (torch.float32, torch.bfloat16) and all(t.dtype == dt for t in ts):
-        return [t.contiguous() for t in ts]
+    if dt is torch.float32 or dt is torch.bfloat16:
+        if all(t.dtype is dt and t.is_contiguous() for t in ts):
+            return ts
+        if all(t.dtype is dt for t in ts):
+            return [t.contiguous() for t in ts]
     return [_coeff(t) for t in ts]
 
 
@@ -315,21 +318,21 @@ def _mhc_pre_map_cuda(x_streams, W, alpha_pre, alpha_post, alpha_res, bias, perm
 
 
 def pre_map_nograd(x_streams, W, alpha_pre, alpha_post, alpha_res, bias, perm_mat):
-    """(layer_input, H_merged, h_post) of mhc_pre_map without the op's
-    dispatch, for forwards that record no autograd graph: the same kernels and
-    conversions as the op's device implementation, so the same values, with
-    the outputs nobody reads (h_pre, proj, inv_rms) kept in scratch memory."""
+    """(layer_input, coeffs) of mhc_pre_map without the op's dispatch, for
+    forwards that record no autograd graph: the same kernels and conversions
+    as the op's device implementation, so the same values; coeffs holds
+    H_merged and h_post for post_res_nograd (kernels.premap_fwd_eval)."""
     _check_n4(x_streams, "flash_mhc::mhc_pre_map supports n=4 only")
     _check_k2_shapes((0, W.shape[0]), perm_mat)
     return _k.premap_fwd_eval(x_streams.contiguous(), W.to(x_streams.dtype).contiguous(),
                               *_params(alpha_pre, alpha_post, alpha_res, bias, perm_mat))
 
 
-def post_res_nograd(x_streams, layer_output, H_merged, h_post):
+def post_res_nograd(x_streams, layer_output, coeffs):
     """fused_post_res's device implementation without the op's dispatch, for
-    H_merged and h_post from pre_map_nograd of the same x_streams."""
+    the coeffs of pre_map_nograd of the same x_streams."""
     _check_n4(x_streams, "flash_mhc::fused_post_res currently supports n=4 only")
-    return _k.k4_fwd_eval(x_streams.contiguous(), layer_output.contiguous(), H_merged, h_post)
+    return _k.k4_fwd_eval(x_streams.contiguous(), layer_output.contiguous(), coeffs)
 
 
 @torch.library.impl(_lib, "mhc_pre_map_coeffs", "CUDA")
