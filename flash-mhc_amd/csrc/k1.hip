@@ -27,6 +27,7 @@
 
 #include "fmhc_common.h"
 #include "k1_premap.h"
+#include "k2_chain.h"
 
 namespace fmhc {
 
@@ -70,6 +71,14 @@ __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
 // directly from HBM is 3% slower than loading whole lines (8 tokens x 128
 // bytes per instruction) and moving them into the MFMA layout through a
 // wave-private LDS tile (16R tokens x 128 bytes).
+// The pre-map tile epilogue's shared memory (TILE below).
+template <int R>
+struct TileSmem {
+  K2Smem k2;
+  float proj[16 * R][kDk];
+  f32x4 hpre[16 * R];
+};
+
 template <int R>
 struct FwdFrag {
   u32x4 wa[2], wb[2];  // W rows 0-15 / 16-31, two 32-wide k steps
@@ -80,17 +89,31 @@ struct FwdFrag {
 // workgroup writes its fp32 partial sums (32 projections + sum of squares per
 // token) to part[t][33][S4] (S4 = gridDim.y rounded up to 4) instead of the
 // outputs; k1_fwd_finish adds the gridDim.y partials in order.
-template <int R, int SPLIT, bool SPLITK>
+// TILE (the pre-map region for many tokens, premap.hip): after a tile's
+// projections, the same workgroup runs K2 on the tile's tokens (one lane per
+// token, the K2 kernel's per-token chain) and then K3, mixing the tile's
+// streams into the layer input while L2 and the memory-side cache may still
+// hold the rows it just read (its x loads are ordinary loads, which allocate
+// there).  Same values as K1 -> K2 -> K3 launched separately.
+template <int R, int SPLIT, bool SPLITK, bool TILE = false>
 __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __restrict__ x,
                                                              const uint16_t* __restrict__ W,
                                                              uint16_t* __restrict__ out,
                                                              float* __restrict__ inv_rms,
                                                              float* __restrict__ part,
-                                                             int64_t T, int nC, int cps) {
+                                                             int64_t T, int nC, int cps,
+                                                             const PremapTile pt = PremapTile{}) {
+  static_assert(!TILE || (R == SPLIT && !SPLITK), "the tile epilogue gives each wave one 16-token block");
   __shared__ float red_acc[SPLIT][R][8][kWave];
   __shared__ float red_ss[SPLIT][R][16];
   __shared__ u32x4 xs[SPLIT][16 * R * 8];  // per wave: 16R tokens x 8 swizzled 16-byte slots
   __shared__ u32x4 wts[kValu ? SPLIT : 1][kValu ? 32 * 8 : 1];  // VALU build: the W chunk, 32 rows x 8 slots
+  // TILE: K2's parameters, the tile's stored projections and its h_pre.
+  __shared__ std::conditional_t<TILE, TileSmem<R>, char> tile_sm;
+  if constexpr (TILE) {
+    zero_words(pt.z);
+    stage_params<kWave * SPLIT>(pt.P, tile_sm.k2);
+  }
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
@@ -157,7 +180,7 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const u32x4* px = reinterpret_cast<const u32x4*>(xw + xoff[s * R + r] + k);
-        if constexpr (!SPLITK)
+        if constexpr (!SPLITK && !TILE)
           f.xv[s][r] = __builtin_nontemporal_load(px);
         else
           f.xv[s][r] = *px;
@@ -334,6 +357,49 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
         st_stream(reinterpret_cast<u32x2*>(orow), lo2);
         st_stream(reinterpret_cast<u32x2*>(orow + 16), hi2);
         if (grp == 0) inv_rms[t] = inv;
+      }
+      if constexpr (TILE) {
+        // The stored (bf16) projections of token row, for the K2 lanes below.
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          tile_sm.proj[16 * r + row][4 * grp + q] = bf16_to_f32(f32_to_bf16(a[q] * inv));
+          tile_sm.proj[16 * r + row][16 + 4 * grp + q] = bf16_to_f32(f32_to_bf16(a[4 + q] * inv));
+        }
+      }
+    }
+  }
+  if constexpr (TILE) {
+    // Wave w owns block r = w.  Same-wave LDS operations are ordered, so the
+    // projections written above and the h_pre written below need no barrier.
+    const int r = wave;
+    if (lane < 16) {
+#pragma clang fp contract(off)
+      const int64_t t = t0 + 16 * r + lane;
+      float p[kDk];
+#pragma unroll
+      for (int k = 0; k < kDk; ++k) p[k] = tile_sm.proj[16 * r + lane][k];
+      float ap, apo, ar, b[kDk];
+      load_params(tile_sm.k2, ap, apo, ar, b);
+      K2Fwd f;
+      k2_chain(p, ap, apo, ar, b, f);
+      f32x4 Hm[kN];
+      k2_h_merged(f, tile_sm.k2.perm, Hm);
+      const f32x4 hp = {f.hp[0], f.hp[1], f.hp[2], f.hp[3]};
+      if (t < T) {
+        reinterpret_cast<f32x4*>(pt.h_pre)[t] = hp;
+        reinterpret_cast<f32x4*>(pt.h_post)[t] = f32x4{f.hq[0], f.hq[1], f.hq[2], f.hq[3]};
+#pragma unroll
+        for (int i = 0; i < kN; ++i) reinterpret_cast<f32x4*>(pt.H)[t * kN + i] = Hm[i];
+      }
+      tile_sm.hpre[16 * r + lane] = hp;
+    }
+    if (pt.layer_input) {
+      for (int tt = 0; tt < 16; ++tt) {
+        const int64_t t = t0 + 16 * r + tt;
+        if (t >= T) break;
+        const f32x4 hv = tile_sm.hpre[16 * r + tt];
+        const float h[4] = {hv[0], hv[1], hv[2], hv[3]};
+        k3_token<8>(x + t * 4 * pt.C, h, pt.layer_input + t * pt.C, lane, kWave, pt.C);
       }
     }
   }
@@ -1083,6 +1149,19 @@ extern "C" int fmhc_k1_bwd(const uint16_t* x_flat, const uint16_t* W, const uint
 }
 
 namespace fmhc {
+
+bool k1_premap_tile(const uint16_t* x, const uint16_t* W, uint16_t* proj, float* inv_rms, const PremapTile& pt,
+                    int64_t T, int64_t C, hipStream_t s, int* status) {
+  const int64_t nC = 4 * C;
+  if (T < kFwdLargeT || C % 8 != 0 || nC > (int64_t{1} << 24) || !aligned16(x) || !aligned16(W) ||
+      !aligned16(proj) || (pt.layer_input && !aligned16(pt.layer_input)))
+    return false;
+  const dim3 grid(blocks_for(T, 16 * kFwdR));
+  k1_fwd_mfma<kFwdR, kFwdSplit, false, true><<<grid, kWave * kFwdSplit, 0, s>>>(
+      x, W, proj, inv_rms, nullptr, T, static_cast<int>(nC), 0, pt);
+  *status = launch_status();
+  return true;
+}
 
 int k1_fwd_partials(const uint16_t* x_flat, const uint16_t* W, void* ws, int64_t ws_bytes, int64_t T,
                     int64_t nC, hipStream_t s) {

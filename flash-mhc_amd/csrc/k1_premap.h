@@ -5,6 +5,8 @@
 
 #include <cstdint>
 
+#include "k2_chain.h"
+
 namespace fmhc {
 
 constexpr float kRmsEps = 1e-6f;  // K1's RMSNorm epsilon (kernels.py:296 of the reference)
@@ -15,6 +17,26 @@ constexpr float kRmsEps = 1e-6f;  // K1's RMSNorm epsilon (kernels.py:296 of the
 // rounded up to 4) and returns the number of splits S >= 2; it returns 0 when
 // the tokens do not take that path and -status on an error.  The second stage
 // (k1_fwd_finish in k1.hip) adds the S partials of each value in split order.
+// Outputs of the pre-map tile kernel beyond K1's (k1_fwd_mfma with TILE):
+// K2's parameters and outputs, and the layer input (null: K1 + K2 only).
+struct PremapTile {
+  K2Params P{};
+  float* h_pre = nullptr;
+  float* h_post = nullptr;
+  float* H = nullptr;
+  uint16_t* layer_input = nullptr;
+  int C = 0;
+  ZeroWords z{};
+};
+
+// The pre-map forward of many tokens as one kernel, when its shapes allow
+// (T >= the one-pass kernel's 64-token tiles, C % 8 == 0, 16-byte aligned
+// x / W / proj / layer_input): K1 on 64-token tiles, then K2 and K3 on each
+// tile by the same workgroup.  Returns false (nothing launched) when they do
+// not; otherwise launches and returns true with *status set.
+bool k1_premap_tile(const uint16_t* x, const uint16_t* W, uint16_t* proj, float* inv_rms, const PremapTile& pt,
+                    int64_t T, int64_t C, hipStream_t s, int* status);
+
 int k1_fwd_partials(const uint16_t* x_flat, const uint16_t* W, void* ws, int64_t ws_bytes, int64_t T,
                     int64_t nC, hipStream_t s);
 

@@ -11,16 +11,19 @@
 // (bf16(grad_x_in + pre-map gradient), autograd's sum), which replaces
 // autograd's separate accumulation pass (1.5 x T x nC x 2 bytes).
 //
-// Forward: K1 -> K2 -> K3, the three kernels of k1.hip, k2.hip, k3.hip.  For
-// few tokens K1 is split over the columns (partial sums in the caller's
-// workspace), and its second stage runs inside the K2 kernel (k1_finish_k2;
-// with K3 too when the layer input is wanted, k1_finish_k2_k3).  A
-// one-pass variant that kept each token tile of x in LDS between K1 and K3
-// (saving K3's read of x) was built and measured slower on gfx950 at
-// C <= 1024: with tiles of 8-16 tokens every tile re-reads the whole of W
-// (32 x nC) from L2, and holding a wave's share of W in registers instead
-// does not fit beside the tile pipeline (register spills), whereas K1
-// amortises W over 64 tokens per workgroup.
+// Forward, many tokens (T >= 16384): one kernel (k1_premap_tile, k1.hip).
+// Each workgroup runs K1 on its 64-token tile with ordinary loads of x, then
+// K2 on the tile's tokens (one lane per token) and K3 on the tile, whose
+// re-read of the tile's rows finds them in L2 or the memory-side cache: x
+// comes from HBM about once (T = 65536, C = 1024: 178 us against 209 us for
+// three kernels; with nontemporal K1 loads, which do not leave the rows in
+// the caches, the one kernel is no faster than three).  Keeping the tile in
+// LDS instead does not fit beside K1's pipeline: tiles of 8-16 tokens make
+// every tile re-read all of W (32 x nC) from L2.  Fewer tokens: K1 -> K2 ->
+// K3, the kernels of k1.hip, k2.hip, k3.hip; for few tokens K1 is split over
+// the columns (partial sums in the caller's workspace), and its second stage
+// runs inside the K2 kernel (k1_finish_k2; with K3 too when the layer input
+// is wanted, k1_finish_k2_k3).
 
 #include <hip/hip_runtime.h>
 
@@ -30,6 +33,13 @@
 #include "fmhc_common.h"
 #include "k1_premap.h"
 #include "k2_chain.h"
+
+// 1: the forward of many tokens runs as one kernel, K1 with K2 and K3 on
+// each 64-token tile (k1_premap_tile); 0 (an evidence build): K1, K2 and K3
+// as three kernels, each reading x from HBM.
+#ifndef FMHC_PREMAP_TILE
+#define FMHC_PREMAP_TILE 1
+#endif
 
 namespace {
 
@@ -163,6 +173,18 @@ int premap_fwd_run(const uint16_t* x, const uint16_t* W, const void* alpha_pre, 
     return FMHC_ERR_INVALID_ARGUMENT;
   const fmhc::ZeroWords z{zero_word_a, zero_word_b};
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (FMHC_PREMAP_TILE) {
+    fmhc::PremapTile pt;
+    pt.P = P;
+    pt.h_pre = h_pre;
+    pt.h_post = h_post;
+    pt.H = H_merged;
+    pt.layer_input = layer_input;
+    pt.C = static_cast<int>(C);
+    pt.z = z;
+    int st = FMHC_OK;
+    if (fmhc::k1_premap_tile(x, W, proj, inv_rms, pt, T, C, s, &st)) return st;
+  }
   const int S = fmhc::k1_fwd_partials(x, W, workspace, workspace_bytes, T, n * C, s);
   if (S < 0) return -S;
   int st = FMHC_OK;

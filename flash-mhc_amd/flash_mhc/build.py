@@ -59,7 +59,10 @@ SOURCE_FLAGS = {"k1.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 # Evidence builds of the same library, selected at compile time.  k1_valu: the
 # K1 forward and backward-dx contractions as fp32 FMAs on the VALU instead of
 # the matrix cores (same tiles, loads and pipeline), to time the two.
-VARIANTS = {"k1_valu": ["-DFMHC_K1_VALU=1"]}
+# premap_three_kernels: the pre-map forward of many tokens as K1, K2, K3 in
+# three kernels, against the product's one kernel (K1 on a 64-token tile, then
+# K2 and K3 on it by the same workgroup).
+VARIANTS = {"k1_valu": ["-DFMHC_K1_VALU=1"], "premap_three_kernels": ["-DFMHC_PREMAP_TILE=0"]}
 
 
 def variant_path(name: str) -> Path:

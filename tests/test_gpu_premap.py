@@ -66,10 +66,11 @@ def test_premap_fwd_stages(T, C):
     check_bf16("premap layer_input", li, R, S, 4)
 
 
-@pytest.mark.parametrize("T,C", [(8192, 1024), (300, 1024), (1, 4096)])
+@pytest.mark.parametrize("T,C", [(8192, 1024), (300, 1024), (1, 4096), (16400, 1024), (20000, 512)])
 def test_premap_matches_three_kernels(T, C):
     """Same outputs as K1 + K2 + K3 launched separately (few tokens: both
-    take K1's column-split kernel)."""
+    take K1's column-split kernel; from T = 16384 on the pre-map runs its
+    one-kernel tile path, K2 and K3 inside K1's workgroups)."""
     x = randn((T, 4, C), 3).to(DEV)
     W = randn((32, 4 * C), 4, 0.02).to(DEV)
     p = [t.to(DEV) for t in (*_params(5), PERM)]
