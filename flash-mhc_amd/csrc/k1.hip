@@ -587,11 +587,18 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
     f.pv = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(proj + tbase * kDout) + goff);
     const char* ib = reinterpret_cast<const char*>(inv_rms + tbase);
     const char* xb = reinterpret_cast<const char*>(x + tbase * nC);
+    // The lane's four tokens are consecutive: a full block reads their
+    // inv_rms with one 16-byte load (the block-uniform branch below).
+    if (last == 15) {
+      const f32x4 iv = *reinterpret_cast<const f32x4*>(ib + 16u * static_cast<uint32_t>(grp));
+#pragma unroll
+      for (int q = 0; q < 4; ++q) f.inv[q] = iv[q];
+    }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int r0 = 4 * grp + q;
       const uint32_t r = static_cast<uint32_t>(r0 < last ? r0 : last);
-      f.inv[q] = *reinterpret_cast<const float*>(ib + 4u * r);
+      if (last != 15) f.inv[q] = *reinterpret_cast<const float*>(ib + 4u * r);
       f.xv[q] = u32x4{0u, 0u, 0u, 0u};
       if (kok) f.xv[q] = ld_stream(reinterpret_cast<const u32x4*>(xb + (r * row_bytes + kbytes)));
       if constexpr (EPI) {
@@ -953,11 +960,12 @@ bool bad_sizes(int64_t T, int64_t nC, int64_t D_out) {
   return T < 0 || nC <= 0 || nC > (int64_t{1} << 30) || D_out != kDout;
 }
 
-// The backward MFMA kernel addresses 16 rows of x with 32-bit byte offsets.
-bool k1_bwd_mfma_path(const void* x, const void* W, const void* go, const void* proj, const void* gx,
-                      int64_t nC) {
+// The backward MFMA kernel addresses 16 rows of x with 32-bit byte offsets
+// and reads inv_rms four tokens at a time.
+bool k1_bwd_mfma_path(const void* x, const void* W, const void* go, const void* proj, const void* inv_rms,
+                      const void* gx, int64_t nC) {
   return nC % 8 == 0 && nC <= (int64_t{1} << 26) && aligned16(x) && aligned16(W) && aligned16(go) &&
-         aligned16(proj) && aligned16(gx);
+         aligned16(proj) && aligned16(inv_rms) && aligned16(gx);
 }
 
 // Column split of the forward for T tokens (S = 1: the one-pass kernel).
@@ -1089,7 +1097,7 @@ extern "C" int fmhc_k1_bwd_dx(const uint16_t* x_flat, const uint16_t* W, const u
     return FMHC_ERR_INVALID_ARGUMENT;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int nc = static_cast<int>(nC);
-  if (k1_bwd_mfma_path(x_flat, W, grad_out, proj_out, grad_x, nC)) {
+  if (k1_bwd_mfma_path(x_flat, W, grad_out, proj_out, inv_rms, grad_x, nC)) {
     const int nslices = static_cast<int>((nC + 127) / 128);
     const int64_t nruns = k1_bwd_nruns(T, nC, kBwdNTB, 1);
     launch_k1_bwd_mfma<false>(s, x_flat, W, grad_out, proj_out, inv_rms, grad_x, nullptr, T, nc, nslices, nruns);
@@ -1128,7 +1136,7 @@ extern "C" int fmhc_k1_bwd(const uint16_t* x_flat, const uint16_t* W, const uint
     return launch_status();
   }
   if (!x_flat || !W || !grad_out || !proj_out || !inv_rms || !grad_x) return FMHC_ERR_INVALID_ARGUMENT;
-  if (k1_bwd_mfma_path(x_flat, W, grad_out, proj_out, grad_x, nC)) {
+  if (k1_bwd_mfma_path(x_flat, W, grad_out, proj_out, inv_rms, grad_x, nC)) {
     const int64_t need = fmhc_k1_bwd_workspace_bytes(T, nC);
     if (!workspace || workspace_bytes < need || !aligned16(workspace)) return FMHC_ERR_INVALID_ARGUMENT;
     const int nslices = static_cast<int>((nC + 127) / 128);
@@ -1180,9 +1188,9 @@ int k1_fwd_partials(const uint16_t* x_flat, const uint16_t* W, void* ws, int64_t
 // grad_x = bf16(bf16(h_pre[t, j] go3[t, c]) + bf16(dx)).  On the MFMA path the
 // K3 term is computed in the store; otherwise grad_x must already hold it
 // (fmhc_k3_bwd's grad_x) and the element-wise kernel adds dx to it.
-bool k1_bwd_premap_fused(const void* x, const void* W, const void* go, const void* proj, const void* gx,
-                         const void* go3, const void* gi, int64_t C) {
-  return C % 8 == 0 && k1_bwd_mfma_path(x, W, go, proj, gx, 4 * C) && aligned16(go3) && aligned16(gi);
+bool k1_bwd_premap_fused(const void* x, const void* W, const void* go, const void* proj, const void* inv_rms,
+                         const void* gx, const void* go3, const void* gi, int64_t C) {
+  return C % 8 == 0 && k1_bwd_mfma_path(x, W, go, proj, inv_rms, gx, 4 * C) && aligned16(go3) && aligned16(gi);
 }
 
 int k1_bwd_premap(const uint16_t* x_flat, const uint16_t* W, const uint16_t* grad_proj,
@@ -1195,7 +1203,7 @@ int k1_bwd_premap(const uint16_t* x_flat, const uint16_t* W, const uint16_t* gra
     k1_dw_zero<<<dim3(blocks_for(static_cast<int64_t>(kDout) * nC, 256)), 256, 0, s>>>(grad_W, nc);
     return launch_status();
   }
-  if (k1_bwd_premap_fused(x_flat, W, grad_proj, proj, grad_x, go3, grad_x_in, C)) {
+  if (k1_bwd_premap_fused(x_flat, W, grad_proj, proj, inv_rms, grad_x, go3, grad_x_in, C)) {
     if (!workspace || workspace_bytes < fmhc_k1_bwd_workspace_bytes(T, nC) || !aligned16(workspace))
       return FMHC_ERR_INVALID_ARGUMENT;
     const int nslices = static_cast<int>((nC + 127) / 128);

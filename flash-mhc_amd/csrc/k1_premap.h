@@ -42,8 +42,8 @@ int k1_fwd_partials(const uint16_t* x_flat, const uint16_t* W, void* ws, int64_t
 
 // True when k1_bwd_premap computes the K3 term of grad_x itself (MFMA path);
 // otherwise grad_x must hold it on entry.  gi: the incoming gradient or null.
-bool k1_bwd_premap_fused(const void* x, const void* W, const void* go, const void* proj, const void* gx,
-                         const void* go3, const void* gi, int64_t C);
+bool k1_bwd_premap_fused(const void* x, const void* W, const void* go, const void* proj, const void* inv_rms,
+                         const void* gx, const void* go3, const void* gi, int64_t C);
 
 // grad_W (32, 4C) and grad_x = bf16(bf16(h_pre[t, j] go3[t, c]) + bf16(dx)) of
 // K1 for x (T, 4, C); with grad_x_in (may be null, must not overlap grad_x)

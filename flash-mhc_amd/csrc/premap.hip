@@ -317,7 +317,7 @@ extern "C" int fmhc_premap_bwd(const uint16_t* x, const uint16_t* W, const void*
   float* gh = T > 0 ? reinterpret_cast<float*>(ws + w.gh) : nullptr;
   uint16_t* gp = T > 0 ? reinterpret_cast<uint16_t*>(ws + w.gp) : nullptr;
   int st = FMHC_OK;
-  const bool fused = T > 0 && k1_bwd_premap_fused(x, W, gp, proj, grad_x, grad_layer_input, grad_x_in, C);
+  const bool fused = T > 0 && k1_bwd_premap_fused(x, W, gp, proj, inv_rms, grad_x, grad_layer_input, grad_x_in, C);
   if (T > 0) st = fmhc_k3_bwd(x, h_pre, grad_layer_input, fused ? nullptr : grad_x, gh, T, C, n, stream);
   if (st == FMHC_OK)
     st = fmhc_k2_bwd(proj, alpha_pre, alpha_post, alpha_res, bias, perm, param_dtype, gh, grad_h_post,

@@ -159,6 +159,26 @@ def test_k1_bwd_dx_misaligned():
     check_bf16("k1 grad_x (misaligned)", gx, R, S, 64)
 
 
+def test_k1_bwd_inv_rms_off_16_bytes():
+    """Every operand aligned but inv_rms (4 mod 16 bytes): the matrix-core
+    backward reads inv_rms 16 bytes at a time, so this input takes the
+    element-wise kernels, which must give the oracle's values too."""
+    T, C = 320, 256
+    x, W = _k1_inputs(T, C, seed=33)
+    go = randn((T, 32), seed=34)
+    xd, Wd, god = x.to(DEV), W.to(DEV), go.to(DEV)
+    proj, inv = K.k1_fwd(xd, Wd)
+    inv_off = misaligned(inv.cpu())
+    assert inv_off.data_ptr() % 16 == 4
+    gx = K.k1_bwd_dx(god, xd, Wd, proj, inv_off)
+    gx2, gW = K.k1_bwd(god, xd, Wd, proj, inv_off)
+    R, S = O.k1_bwd_dx(go, x, W, proj.cpu(), inv.cpu())
+    check_bf16("k1 grad_x (inv_rms off 16)", gx, R, S, 64)
+    check_bf16("k1 fused grad_x (inv_rms off 16)", gx2, R, S, 64)
+    R, S = O.k1_grad_W(go, x, inv.cpu())
+    check_bf16("k1 fused grad_W (inv_rms off 16)", gW, R, S, T)
+
+
 @pytest.mark.parametrize(
     "T,C", [(2048, 256), (257, 1024), (1, 4096), (1500, 1024), (20000, 256), (333, 100), (31, 24), (17, 25)]
 )
