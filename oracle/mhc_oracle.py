@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE ONLY.  The ``flash_mhc`` package never imports this
 module.  Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline``
-leg of ``bench.py`` may use it, as the checker or as the timed CPU baseline,
+leg of ``bench.py`` may use it, to check results or as the timed CPU baseline,
 never as an implementation of the product path.
 
 Contents

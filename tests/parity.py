@@ -4,8 +4,8 @@ Every check compares a device result ``o`` with the oracle value ``R``
 computed in float64 from the *same* bf16/fp32 inputs, and with
 ``S = sum |terms|`` of the same formula.
 
-bf16 outputs (the north-star rule: equal to the fp32 value rounded to bf16
-within 1 bf16 ulp):
+bf16 outputs (the path's tolerance: equal to the fp32 value rounded to
+bf16 within 1 bf16 ulp):
     |o - R| <= ulp_bf16(R) + 4 * sqrt(n) * 2^-24 * S
 The second term is the probabilistic bound of an n-term fp32 sum in any
 order (Higham's sqrt(n) rule with a 4-sigma margin).  It only matters where

@@ -1,4 +1,4 @@
-"""The reference's own correctness suite, restated for this build: the same
+"""The reference's own correctness suite, restated for the HIP kernels: the same
 shapes, comparisons and tolerances as tests/test_correctness.py of
 alint77/flash-mHC (K1 / K3 / K4 forward and backward against PyTorch
 formulations of the paper's precision rules, and MHCLiteBlock's fused path

@@ -5,7 +5,8 @@ C = 4096, bf16, activation checkpointing on, under torch.compile (inductor).
 Checks that the fused path runs at this size (x alone is 8.6 GB per block
 input), that every parameter receives a finite gradient, that the compiled
 stack's forward equals the eager one on the same weights, and reports the
-forward + backward time per step and the peak HBM allocated.
+forward + backward time per step and the peak HBM allocated, beside the
+same stack under the reference's rules, eager and compiled.
 """
 
 from __future__ import annotations
@@ -74,29 +75,41 @@ def test_training_scale_stack():
           f"first (compiling) step {compile_s:.1f} s", flush=True)
 
     # The same stack with the reference's rules (K2 as PyTorch ops, K1's
-    # grad_W as a matmul, separate pre-map ops; eager), for comparison.
+    # grad_W as a matmul, separate pre-map ops), for comparison: eager, then
+    # under torch.compile like the fused stack above (the switches are read
+    # while tracing, so the compiled stack is traced again after a reset).
     flags = ("FLASH_MHC_FUSED_K2", "FLASH_MHC_FUSED_DW", "FLASH_MHC_FUSED_PREMAP")
     saved = {f: os.environ.get(f) for f in flags}
     try:
         for f in flags:
             os.environ[f] = "0"
+        del compiled
+        torch._dynamo.reset()
 
-        def ref_step():
-            for p in blocks.parameters():
-                p.grad = None
-            x.grad = None
-            blocks(x).backward(up)
+        def timed(run, label):
+            def one():
+                for p in blocks.parameters():
+                    p.grad = None
+                x.grad = None
+                run(x).backward(up)
 
-        ref_step()
-        torch.cuda.synchronize()
-        torch.cuda.reset_peak_memory_stats()
-        e0.record()
-        for _ in range(n):
-            ref_step()
-        e1.record()
-        torch.cuda.synchronize()
-        print(f"[train-scale] same stack, reference rules, eager: fwd+bwd {e0.elapsed_time(e1) / n:.1f} ms/step, "
-              f"peak HBM allocated {torch.cuda.max_memory_allocated() / 1e9:.1f} GB", flush=True)
+            t0 = time.perf_counter()
+            one()
+            torch.cuda.synchronize()
+            first_s = time.perf_counter() - t0
+            torch.cuda.reset_peak_memory_stats()
+            e0.record()
+            for _ in range(n):
+                one()
+            e1.record()
+            torch.cuda.synchronize()
+            print(f"[train-scale] same stack, reference rules, {label}: fwd+bwd {e0.elapsed_time(e1) / n:.1f} "
+                  f"ms/step, peak HBM allocated {torch.cuda.max_memory_allocated() / 1e9:.1f} GB, first step "
+                  f"{first_s:.1f} s", flush=True)
+
+        timed(blocks, "eager")
+        timed(torch.compile(blocks), "torch.compile")
+        torch._dynamo.reset()
     finally:
         for f, v in saved.items():
             if v is None:
