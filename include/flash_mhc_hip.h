@@ -18,8 +18,9 @@
  *   - n (streams per token) must be 4 and D_out (K1 projection width) must be
  *     32, matching the reference's n = 4 specialisation.
  *   - Fast paths move 16 bytes per lane and are taken when C % 8 == 0 and
- *     the bf16 pointers are 16-byte aligned; any other C or alignment takes an
- *     element-wise path with identical results.
+ *     the bf16 pointers (for K1's backward also inv_rms) are 16-byte aligned;
+ *     any other C or alignment takes an element-wise path, which gives the
+ *     same values up to the order of fp32 sums.
  *   - Return value: FMHC_OK (0), or an FMHC_ERR_* code; for HIP runtime
  *     failures FMHC_ERR_HIP_BASE + hipError_t.  fmhc_error_string() names it.
  */
