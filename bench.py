@@ -518,6 +518,8 @@ def main() -> None:
                     help="tokens of the CPU baseline's sample (default: the whole metric workload)")
     ap.add_argument("--cpu-iters", type=int, default=10, help="timed passes of the CPU baseline (median)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--columns", action="store_true",
+                    help="with --no-extras: still time each kernel alone and cold")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the K1-backward and block-step fields (profiler runs: only the six kernels)")
     ap.add_argument("--traffic", type=str, default=str(ROOT / "profiles" / "traffic_k4_bwd_T65536_C1024.json"),
@@ -619,9 +621,10 @@ def main() -> None:
     # The latency-bound eval shapes first: after the block steps' seconds of
     # full-bandwidth work the same graph replays measure up to 25% slower.
     lat = None if args.no_extras else eval_latency(tokens=eval_tokens)
-    alone = None if args.no_extras else isolated_kernels(launch, bm)
+    columns = args.columns or not args.no_extras
+    alone = isolated_kernels(launch, bm) if columns else None
     probe = Probe()
-    cold = None if args.no_extras else cold_kernels(launch, bm, CacheFlush(probe))
+    cold = cold_kernels(launch, bm, CacheFlush(probe)) if columns else None
     k1_full_bwd = None if args.no_extras else k1_backward_paths(inp, T, C)
     blk = None if args.no_extras else block_step(T, C)
     # The block configuration at C = 2048 (same T), with its own layer width.
