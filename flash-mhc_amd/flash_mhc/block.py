@@ -180,7 +180,8 @@ class MHCLiteBlock(nn.Module):
     def _projection_weight(self, dt: torch.dtype) -> torch.Tensor:
         """K1's W in dtype dt, with the optional RMSNorm weight folded in."""
         if self.rms_weight is None:
-            return self.W_all.weight.to(dt)
+            w = self.W_all.weight
+            return w if w.dtype is dt else w.to(dt)
         return (self.W_all.weight.float() * self.rms_weight.float()).to(dt)
 
     def _project_triton(self, x_streams: torch.Tensor) -> torch.Tensor:

@@ -172,16 +172,26 @@ N_PERM = 24  # n! at n = 4
 PARAM_DTYPES = {_F32: 0, _BF16: 1}  # FMHC_PARAM_F32, FMHC_PARAM_BF16
 
 
+_K2_NAMES = ("alpha_pre", "alpha_post", "alpha_res", "bias", "perm")
+_K2_SHAPES = ((1,), (1,), (1,), (D_OUT,), (N_PERM, N_STREAMS * N_STREAMS))
+
+
 def _k2_params(alpha_pre, alpha_post, alpha_res, bias, perm, dev) -> int:
     """Check K2's parameters (all fp32 or all bf16) and return the ABI's dtype code."""
     dt = alpha_pre.dtype if isinstance(alpha_pre, torch.Tensor) else None
-    if dt not in PARAM_DTYPES:
+    code = PARAM_DTYPES.get(dt)
+    if code is None:
         raise TypeError(f"K2 parameters must be float32 or bfloat16, got {dt}")
-    for t, name, shape in ((alpha_pre, "alpha_pre", (1,)), (alpha_post, "alpha_post", (1,)),
-                           (alpha_res, "alpha_res", (1,)), (bias, "bias", (D_OUT,)),
-                           (perm, "perm", (N_PERM, N_STREAMS * N_STREAMS))):
+    ps = (alpha_pre, alpha_post, alpha_res, bias, perm)
+    for t, shape in zip(ps, _K2_SHAPES):
+        if (not isinstance(t, torch.Tensor) or t.dtype is not dt or t.shape != shape or t.device != dev
+                or not t.is_contiguous()):
+            break
+    else:
+        return code
+    for t, name, shape in zip(ps, _K2_NAMES, _K2_SHAPES):
         _require(t, name, dt, shape, dev)
-    return PARAM_DTYPES[dt]
+    return code
 
 
 def k2_fwd(proj: torch.Tensor, alpha_pre: torch.Tensor, alpha_post: torch.Tensor,
@@ -302,10 +312,16 @@ def premap_fwd_eval(x_streams: torch.Tensor, W: torch.Tensor, alpha_pre: torch.T
     fp32 at byte 64 T, the inputs k4_fwd_eval reads, followed by h_pre, proj,
     inv_rms and the workspace, which nothing reads after the call: one
     allocation instead of six."""
-    T, n, C = _streams_shape(x_streams)
-    dev = _device_of(x_streams)
-    _require(x_streams, "x_streams", _BF16, (T, n, C), dev)
-    _require(W, "W", _BF16, (D_OUT, n * C), dev)
+    dev = x_streams.device
+    shape = x_streams.shape
+    if (len(shape) != 3 or shape[1] != N_STREAMS or dev.type != "cuda" or x_streams.dtype is not _BF16
+            or not x_streams.is_contiguous() or W.dtype is not _BF16 or W.device != dev
+            or W.shape != (D_OUT, N_STREAMS * shape[2]) or not W.is_contiguous()):
+        T, n, C = _streams_shape(x_streams)
+        dev = _device_of(x_streams)
+        _require(x_streams, "x_streams", _BF16, (T, n, C), dev)
+        _require(W, "W", _BF16, (D_OUT, n * C), dev)
+    T, n, C = shape
     pdt = _k2_params(alpha_pre, alpha_post, alpha_res, bias, perm, dev)
     lib = _abi.load()
     ws_bytes = _premap_ws_bytes(lib, T, C)
@@ -451,10 +467,16 @@ def k4_fwd(x_streams: torch.Tensor, layer_output: torch.Tensor, H_merged: torch.
 def k4_fwd_eval(x_streams: torch.Tensor, layer_output: torch.Tensor, coeffs: torch.Tensor) -> torch.Tensor:
     """k4_fwd with H_merged and h_post read from premap_fwd_eval's coeffs
     buffer for the same x_streams."""
-    dev = _device_of(x_streams)
-    T, n, C = _streams_shape(x_streams)
-    _require(x_streams, "x_streams", _BF16, (T, n, C), dev)
-    _require(layer_output, "layer_output", _BF16, (T, C), dev)
+    dev = x_streams.device
+    shape = x_streams.shape
+    if (len(shape) != 3 or shape[1] != N_STREAMS or dev.type != "cuda" or x_streams.dtype is not _BF16
+            or not x_streams.is_contiguous() or layer_output.dtype is not _BF16 or layer_output.device != dev
+            or layer_output.shape != (shape[0], shape[2]) or not layer_output.is_contiguous()):
+        T, n, C = _streams_shape(x_streams)
+        dev = _device_of(x_streams)
+        _require(x_streams, "x_streams", _BF16, (T, n, C), dev)
+        _require(layer_output, "layer_output", _BF16, (T, C), dev)
+    T, n, C = shape
     if coeffs.dtype is not torch.uint8 or coeffs.numel() < 80 * T or coeffs.device != dev:
         raise ValueError("coeffs is not premap_fwd_eval's buffer for these tokens")
     out = torch.empty_like(x_streams)

@@ -322,17 +322,30 @@ def pre_map_nograd(x_streams, W, alpha_pre, alpha_post, alpha_res, bias, perm_ma
     forwards that record no autograd graph: the same kernels and conversions
     as the op's device implementation, so the same values; coeffs holds
     H_merged and h_post for post_res_nograd (kernels.premap_fwd_eval)."""
-    _check_n4(x_streams, "flash_mhc::mhc_pre_map supports n=4 only")
-    _check_k2_shapes((0, W.shape[0]), perm_mat)
-    return _k.premap_fwd_eval(x_streams.contiguous(), W.to(x_streams.dtype).contiguous(),
-                              *_params(alpha_pre, alpha_post, alpha_res, bias, perm_mat))
+    if x_streams.dim() != 3 or x_streams.shape[1] != 4:
+        _check_n4(x_streams, "flash_mhc::mhc_pre_map supports n=4 only")
+    if W.dim() != 2 or W.shape[0] != 32 or perm_mat.shape != (24, 16):
+        _check_k2_shapes((0, W.shape[0]), perm_mat)
+    # The op's conversions, skipped where they would return the tensor itself.
+    if not x_streams.is_contiguous():
+        x_streams = x_streams.contiguous()
+    if W.dtype is not x_streams.dtype:
+        W = W.to(x_streams.dtype)
+    if not W.is_contiguous():
+        W = W.contiguous()
+    return _k.premap_fwd_eval(x_streams, W, *_params(alpha_pre, alpha_post, alpha_res, bias, perm_mat))
 
 
 def post_res_nograd(x_streams, layer_output, coeffs):
     """fused_post_res's device implementation without the op's dispatch, for
     the coeffs of pre_map_nograd of the same x_streams."""
-    _check_n4(x_streams, "flash_mhc::fused_post_res currently supports n=4 only")
-    return _k.k4_fwd_eval(x_streams.contiguous(), layer_output.contiguous(), coeffs)
+    if x_streams.dim() != 3 or x_streams.shape[1] != 4:
+        _check_n4(x_streams, "flash_mhc::fused_post_res currently supports n=4 only")
+    if not x_streams.is_contiguous():
+        x_streams = x_streams.contiguous()
+    if not layer_output.is_contiguous():
+        layer_output = layer_output.contiguous()
+    return _k.k4_fwd_eval(x_streams, layer_output, coeffs)
 
 
 @torch.library.impl(_lib, "mhc_pre_map_coeffs", "CUDA")
