@@ -235,6 +235,44 @@ def block_step(T: int, C: int, iters: int = 10, variants=("fused", "reference_ru
     return out
 
 
+def premap_alone(T: int, C: int, iters: int = 10) -> dict:
+    """The block's pre-map forward (K1 + K2 + K3, the launch of
+    flash_mhc::mhc_pre_map) alone at (T, C), each launch after a cache flush,
+    for profiler runs that compare builds.  Beside it, two references for the
+    latency of reads past L2: an ordinary 128 MiB read repeated (served by
+    the 256 MB memory-side cache after its first pass) and an ordinary 1 GiB
+    read (HBM)."""
+    from flash_mhc import build_permutation_matrices
+    from flash_mhc import kernels as K
+
+    g = torch.Generator(device="cuda").manual_seed(0)
+    x = torch.randn(T, 4, C, device="cuda", generator=g).to(torch.bfloat16)
+    W = (torch.randn(32, 4 * C, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    p = [torch.tensor([0.8], device="cuda"), torch.tensor([1.2], device="cuda"), torch.tensor([1.7], device="cuda"),
+         torch.randn(32, device="cuda", generator=g) * 0.5, build_permutation_matrices(4)[0].cuda()]
+    probe = Probe()
+    flush = CacheFlush(probe)
+    times = []
+    for _ in range(iters):
+        flush()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        K.premap_fwd(x, W, *p)
+        e1.record()
+        times.append((e0, e1))
+    torch.cuda.synchronize()
+    small = torch.ones(128 << 20, dtype=torch.uint8, device="cuda")
+    big = torch.ones(1 << 30, dtype=torch.uint8, device="cuda")
+    sink = torch.empty(4096, dtype=torch.uint8, device="cuda")
+    for _ in range(4):
+        probe.run(PROBE_READ_CACHED, small, sink, small.numel())
+    probe.run(PROBE_READ_CACHED, big, sink, big.numel())
+    torch.cuda.synchronize()
+    ts = [a.elapsed_time(b) * 1e3 for a, b in times]
+    return {"premap_fwd_cold_us": round(statistics.median(ts), 1), "min_us": round(min(ts), 1),
+            "workload": f"pre-map forward, T={T}, n=4, C={C}, bf16, each launch after a cache flush"}
+
+
 def eval_latency(C: int = 4096, tokens=(1, 64, 257, 65537), variants=("fused", "reference_rules")) -> dict:
     """Eval-mode forward latency of MHCLiteBlock(4, C, Linear(C, C)) (bf16,
     random weights), the inference / ragged-tail shapes: eager and replayed from
@@ -524,7 +562,7 @@ def main() -> None:
                     help="skip the K1-backward and block-step fields (profiler runs: only the six kernels)")
     ap.add_argument("--traffic", type=str, default=str(ROOT / "profiles" / "traffic_k4_bwd_T65536_C1024.json"),
                     help="measured HBM traffic summary (rocprofv3 --pmc) for the dominant kernel")
-    ap.add_argument("--only", choices=("block", "eval"), default=None,
+    ap.add_argument("--only", choices=("block", "eval", "premap"), default=None,
                     help="run one extra alone, fused path only, and print its JSON (profiler runs of the "
                          "block step at --T/--C for --steps iterations, or of the eval latency at --eval-T)")
     ap.add_argument("--eval-T", type=str, default="1,64,257,65537", help="token counts of the eval latency")
@@ -547,6 +585,9 @@ def main() -> None:
     if args.only == "block":
         print(json.dumps({"block_step": block_step(args.T, args.C, iters=args.steps, variants=("fused",))}),
               flush=True)
+        return
+    if args.only == "premap":
+        print(json.dumps({"premap_alone": premap_alone(args.T, args.C, iters=args.steps)}), flush=True)
         return
     if args.only == "eval":
         print(json.dumps({"eval_latency": eval_latency(tokens=eval_tokens, variants=("fused",))}), flush=True)

@@ -44,6 +44,14 @@ constexpr float kEps = kRmsEps;
 #define FMHC_K1_VALU 0
 #endif
 constexpr bool kValu = FMHC_K1_VALU != 0;
+// Evidence build switch: the pre-map's one-kernel forward (TILE) loads x with
+// the nontemporal hint like the plain forward, so that K3's re-read of the
+// tile cannot find it in the memory-side cache.  The product loads it with
+// ordinary loads.
+#ifndef FMHC_PREMAP_TILE_NT
+#define FMHC_PREMAP_TILE_NT 0
+#endif
+constexpr bool kTileNt = FMHC_PREMAP_TILE_NT != 0;
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
@@ -180,7 +188,7 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const u32x4* px = reinterpret_cast<const u32x4*>(xw + xoff[s * R + r] + k);
-        if constexpr (!SPLITK && !TILE)
+        if constexpr (!SPLITK && (!TILE || kTileNt))
           f.xv[s][r] = __builtin_nontemporal_load(px);
         else
           f.xv[s][r] = *px;

@@ -1,9 +1,10 @@
 """The product's pre-map forward of many tokens is one kernel (K1 on a
 64-token tile, then K2 and K3 on it by the same workgroup).  The evidence
-build "premap_three_kernels" (build.py) runs K1, K2, K3 as three kernels.
-Loaded beside the product library through the same C ABI, the two
-fmhc_premap_fwd must give the same outputs bit for bit: the same per-token
-arithmetic in the same order."""
+builds of build.py time it against K1, K2, K3 as three kernels
+("premap_three_kernels") and against the one kernel with nontemporal loads of
+x ("premap_tile_nt").  Loaded beside the product library through the same C
+ABI, each fmhc_premap_fwd must give the product's outputs bit for bit: the
+same per-token arithmetic in the same order."""
 
 from __future__ import annotations
 
@@ -19,10 +20,10 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-@pytest.fixture(scope="module")
-def three_lib():
+@pytest.fixture(scope="module", params=["premap_three_kernels", "premap_tile_nt"])
+def three_lib(request):
     _abi.load()
-    path = build.variant_path("premap_three_kernels")
+    path = build.variant_path(request.param)
     assert path.exists(), f"build the evidence variant first: {path}"
     lib = ctypes.CDLL(str(path), mode=ctypes.RTLD_LOCAL)
     for name, argtypes in _abi.SIGNATURES.items():
