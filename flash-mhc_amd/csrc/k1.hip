@@ -163,9 +163,9 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
   // Full 64-wide chunks.  Wave w takes the chunks at positions w, w + SPLIT,
   // ... of a per-workgroup rotation of the chunk order (rotating spreads the
   // concurrent reads of all workgroups over the DRAM channels instead of every
-  // workgroup hitting the same column of its 8 KiB-strided rows), and
-  // double-buffers: the next chunk's fragments are loaded while the MFMAs of
-  // the current one run.  x is read once per launch, so its loads carry the
+  // workgroup hitting the same column of its 8 KiB-strided rows), and keeps
+  // three chunks in flight: the next two chunks' fragments are loaded while
+  // the MFMAs of the current one run.  x is read once per launch, so its loads carry the
   // nontemporal hint (8-10% faster than ordinary loads).  With SPLITK (few
   // tokens) they do not: the pre-map's few-token kernel reads the same x
   // again right after, from the caches.  With SPLITK the workgroup's chunks
@@ -264,25 +264,46 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
     else
       compute_mfma(f);
   };
-  // n chunks for this wave, two per trip.  Both prefetches are issued on every
-  // path (a clamped index re-reads a cached chunk that is never computed), so
-  // the compiler keeps them ahead of the MFMAs; an odd count ends with f0.
+  // n chunks for this wave (positions wave, wave + SPLIT, ...), three in
+  // flight: f0, f1, f2 in rotation, each trip loading two chunks ahead of the
+  // one it computes.  Every load of the steady loop is below n, so its wait
+  // counts stay exact and no chunk is read twice (a clamped re-read of the
+  // last chunk cost 3.5% more traffic under the nontemporal hint); the tail
+  // finishes the last one to four chunks.
   const int n = nfull > wave ? (nfull - wave + SPLIT - 1) / SPLIT : 0;
-  auto pos = [&](int i) __attribute__((always_inline)) { return wave + SPLIT * (i < n ? i : n - 1); };
   if (n > 0) {
-    load(f0, pos(0));
+    FwdFrag<R> f2;
+    load(f0, wave);
+    if (n > 1) load(f1, wave + SPLIT);
     int i = 0;
-    for (; i + 1 < n; i += 2) {
-      load(f1, pos(i + 1));
-      __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the MFMAs
+    for (; i + 4 < n; i += 3) {
+      load(f2, wave + SPLIT * (i + 2));
+      __builtin_amdgcn_sched_barrier(0);
       transpose(f0);
       compute(f0);
-      load(f0, pos(i + 2));
+      load(f0, wave + SPLIT * (i + 3));
       __builtin_amdgcn_sched_barrier(0);
       transpose(f1);
       compute(f1);
+      load(f1, wave + SPLIT * (i + 4));
+      __builtin_amdgcn_sched_barrier(0);
+      transpose(f2);
+      compute(f2);
     }
-    if (i < n) {
+    const int left = n - i;  // 1 .. 4: chunk i in f0, chunk i + 1 in f1
+    if (left >= 3) load(f2, wave + SPLIT * (i + 2));
+    transpose(f0);
+    compute(f0);
+    if (left >= 4) load(f0, wave + SPLIT * (i + 3));
+    if (left >= 2) {
+      transpose(f1);
+      compute(f1);
+    }
+    if (left >= 3) {
+      transpose(f2);
+      compute(f2);
+    }
+    if (left >= 4) {
       transpose(f0);
       compute(f0);
     }
