@@ -18,7 +18,8 @@ kernels' streaming loads and stores carry (ordinary-access probes beside them
 are labelled ``*_ordinary``).
 Extra fields report K1's full backward (fused grad_W vs the reference's matmul), a whole
 MHCLiteBlock forward + backward with the fused path vs the reference's rules
-(at C and at 2C, i.e. the C=2048 block configuration),
+(at C and at 2C, i.e. the C=2048 block configuration), the same step at
+T=4096 eager and replayed from a HIP graph,
 and the eval-mode forward latency of the inference shapes (C=4096,
 T = 1, 64, 257, 65537; eager and HIP-graph replay).
 ``cpu_baseline`` times the reference's PyTorch formulation of the same six ops
@@ -231,6 +232,51 @@ def block_step(T: int, C: int, iters: int = 10, variants=("fused", "reference_ru
                 os.environ.pop(f, None)
             else:
                 os.environ[f] = v
+    out["workload"] = f"MHCLiteBlock(4, {C}, Linear({C}, {C})) forward + backward, T={T}, bf16"
+    return out
+
+
+def block_step_graphed(T: int = 4096, C: int = 1024, iters: int = 20) -> dict:
+    """MHCLiteBlock(4, C, Linear(C, C)) forward + backward at few tokens, where
+    the host's launches bound an eager step: eager, and the whole step (forward
+    and backward) captured once in a HIP graph and replayed."""
+    import flash_mhc
+
+    torch.manual_seed(0)
+    blk = flash_mhc.MHCLiteBlock(4, C, torch.nn.Linear(C, C, bias=False)).cuda().bfloat16()
+    x = torch.randn(T, 4, C, device="cuda", dtype=torch.bfloat16).requires_grad_(True)
+    up = torch.randn(T, 4, C, device="cuda", dtype=torch.bfloat16)
+
+    def step():
+        blk.zero_grad(set_to_none=True)
+        x.grad = None
+        blk(x).backward(up)
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(iters):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return round(e0.elapsed_time(e1) / iters, 4)
+
+    out = {"eager_ms": timed(step)}
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            step()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    blk.zero_grad(set_to_none=True)
+    x.grad = None
+    with torch.cuda.graph(g):
+        blk(x).backward(up)
+    out["graph_ms"] = timed(g.replay)
     out["workload"] = f"MHCLiteBlock(4, {C}, Linear({C}, {C})) forward + backward, T={T}, bf16"
     return out
 
@@ -670,6 +716,7 @@ def main() -> None:
     blk = None if args.no_extras else block_step(T, C)
     # The block configuration at C = 2048 (same T), with its own layer width.
     blk2 = None if args.no_extras else block_step(T, 2 * C)
+    blk_small = None if args.no_extras else block_step_graphed()
     ceil = stream_ceilings(probe)
     split = read_write_split(T, n, C, D)
     for name in KERNELS:
@@ -702,6 +749,7 @@ def main() -> None:
         "k1_backward_with_grad_W": k1_full_bwd,
         "block_step": blk,
         "block_step_2C": blk2,
+        "block_step_T4096": blk_small,
         "eval_latency": lat,
         "kernels": per,
         "kernels_isolated": alone,

@@ -55,11 +55,13 @@ def build_permutation_matrices(n: int) -> tuple[torch.Tensor, int]:
 
 
 def _plain_eager(x: torch.Tensor) -> bool:
-    """x is an ordinary GPU tensor in eager mode: not traced or compiled, and
-    no Python dispatch mode (fake tensors, functionalization) is active, so the
-    ops' device implementations can be called without going through the ops."""
+    """x is an ordinary GPU tensor in eager mode: not traced or compiled, no
+    Python dispatch mode (fake tensors, functionalization) and no functorch
+    transform is active, so the ops' device implementations can be called
+    without going through the ops."""
     return (type(x) is torch.Tensor and x.is_cuda and not torch.compiler.is_compiling()
-            and not torch.jit.is_tracing() and _get_current_dispatch_mode() is None)
+            and not torch.jit.is_tracing() and _get_current_dispatch_mode() is None
+            and not torch._C._are_functorch_transforms_active())
 
 
 class MHCLiteBlock(nn.Module):
@@ -238,14 +240,30 @@ class MHCLiteBlock(nn.Module):
 
     def _forward_triton(self, x_streams: torch.Tensor, **kwargs) -> torch.Tensor:
         """Fused path: K1/K2/K3/K4 on the HIP kernels."""
-        if not torch.is_grad_enabled() and _ops.fused_premap_enabled() and _plain_eager(x_streams):
-            return self._forward_nograd(x_streams, **kwargs)
+        if _ops.fused_premap_enabled() and _plain_eager(x_streams):
+            if not torch.is_grad_enabled():
+                return self._forward_nograd(x_streams, **kwargs)
+            if not self._use_activation_checkpointing(x_streams) and _ops.fused_xgrad_flag():
+                return self._forward_eager(x_streams, **kwargs)
         ctx = nullcontext() if self.training else _ops.disable_autotune_temporarily()
         # Only the pre-map region is checkpointed: post-res's backward needs
         # exactly the inputs a checkpoint would keep (x, layer_output,
         # H_merged, h_post), so recomputing its forward would only cost time.
         return self._run(x_streams, self._mhc_pre_map_triton, self._mhc_post_res_triton, ctx, kwargs,
                          checkpoint_post_res=False)
+
+    def _forward_eager(self, x_streams: torch.Tensor, **kwargs) -> torch.Tensor:
+        """The fused forward in eager mode with autograd (training at few
+        tokens is bound by the host): mhc_pre_map and mhc_post_res with their
+        registered autograd, applied as autograd Functions around the ops'
+        device implementations instead of through the dispatcher.  Same
+        kernels, same values, same x-gradient sink."""
+        p = self._parameters
+        layer_input, H_merged, h_post, x_sink = _ops.pre_map_eager(
+            x_streams, self._projection_weight(x_streams.dtype), p["alpha_pre"], p["alpha_post"], p["alpha_res"],
+            self.W_all.bias, self._buffers["perm_mat"])
+        layer_output = self.layer(layer_input, **kwargs)
+        return _ops.post_res_eager(x_streams, x_sink, layer_output, H_merged, h_post)
 
     def _forward_nograd(self, x_streams: torch.Tensor, **kwargs) -> torch.Tensor:
         """The fused forward when no autograd graph is recorded (inference):

@@ -566,6 +566,59 @@ torch.library.register_autograd(
 )
 
 
+class _PreMapEager(torch.autograd.Function):
+    """mhc_pre_map with its registered autograd, without the op's dispatch,
+    for eager forwards that record an autograd graph: forward and backward
+    call the op's device implementations (_mhc_pre_map_cuda,
+    _mhc_pre_map_backward_cuda), so the values, the saved tensors and the
+    x_sink contract are the op's.  Returns (layer_input, H_merged, h_post,
+    x_sink); h_pre, proj and inv_rms stay internal (the block does not
+    differentiate them)."""
+
+    @staticmethod
+    def forward(ctx, x_streams, W, alpha_pre, alpha_post, alpha_res, bias, perm_mat):
+        li, H, hq, h_pre, proj, inv_rms, x_sink = _mhc_pre_map_cuda(x_streams, W, alpha_pre, alpha_post,
+                                                                     alpha_res, bias, perm_mat)
+        ctx.save_for_backward(x_streams, W, alpha_pre, alpha_post, alpha_res, bias, perm_mat, h_pre, proj, inv_rms)
+        ctx.set_materialize_grads(False)
+        return li, H, hq, x_sink
+
+    @staticmethod
+    def backward(ctx, g_li, g_H, g_hp, g_sink):
+        x, W, ap, apo, ar, b, perm, h_pre, proj, inv_rms = ctx.saved_tensors
+        grads = _mhc_pre_map_backward_cuda(g_li, g_H, g_hp, None, None, g_sink, x, W, ap, apo, ar, b, perm,
+                                           h_pre, proj, inv_rms)
+        return (*grads, None)
+
+
+class _PostResEager(torch.autograd.Function):
+    """mhc_post_res with its registered autograd, without the op's dispatch
+    (see _PreMapEager): x's gradient goes to x_sink."""
+
+    @staticmethod
+    def forward(ctx, x_streams, x_sink, layer_output, H_merged, h_post):
+        out = _mhc_post_res_cuda(x_streams, x_sink, layer_output, H_merged, h_post)
+        ctx.save_for_backward(x_streams, layer_output, H_merged, h_post)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        x_streams, layer_output, H_merged, h_post = ctx.saved_tensors
+        g_x, g_lo, g_H, g_hp = _fused_post_res_backward_cuda(grad_out, x_streams, layer_output, H_merged, h_post)
+        return None, g_x, g_lo, g_H, g_hp
+
+
+def pre_map_eager(x_streams, W, alpha_pre, alpha_post, alpha_res, bias, perm_mat):
+    """(layer_input, H_merged, h_post, x_sink) of mhc_pre_map, recorded for
+    autograd without the op's dispatch (eager training forwards)."""
+    return _PreMapEager.apply(x_streams, W, alpha_pre, alpha_post, alpha_res, bias, perm_mat)
+
+
+def post_res_eager(x_streams, x_sink, layer_output, H_merged, h_post):
+    """mhc_post_res, recorded for autograd without the op's dispatch."""
+    return _PostResEager.apply(x_streams, x_sink, layer_output, H_merged, h_post)
+
+
 def _setup_pre_map_coeffs(ctx, inputs, output):
     _H, _hp, h_pre, proj, inv_rms, _xs, _ls = output
     ctx.save_for_backward(*inputs, h_pre, proj, inv_rms)

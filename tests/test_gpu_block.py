@@ -326,6 +326,93 @@ def test_graph_capture_eval_forward(T):
             assert torch.equal(eager, ref)
 
 
+@pytest.mark.parametrize("T,rms", [(256, False), (4096, True), (20000, False)])
+def test_eager_autograd_path_equals_op_path(T, rms):
+    """In eager training the block applies mhc_pre_map and mhc_post_res as
+    autograd Functions around the ops' device implementations.  Its output,
+    x's gradient and every parameter gradient equal, bit for bit, those of
+    the same block driven through the torch.library ops (T = 20000: the
+    one-kernel pre-map forward)."""
+    from contextlib import nullcontext
+
+    C = 1024
+    torch.manual_seed(5)
+    blk = flash_mhc.MHCLiteBlock(4, C, torch.nn.Linear(C, C, bias=False), rmsnorm_weight=rms).to(DEV, BF16)
+    if rms:
+        with torch.no_grad():
+            blk.rms_weight.add_(randn((4 * C,), 96, 0.02).to(DEV, blk.rms_weight.dtype))
+    x = randn((T, 4, C), 97 + T, dtype=BF16).to(DEV)
+    up = randn((T, 4, C), 98 + T, dtype=BF16).to(DEV)
+
+    def run(fast):
+        blk.zero_grad(set_to_none=True)
+        xs = x.clone().requires_grad_(True)
+        if fast:
+            out = blk(xs)
+        else:
+            out = blk._run(xs, blk._mhc_pre_map_triton, blk._mhc_post_res_triton, nullcontext(), {},
+                           checkpoint_post_res=False)
+        out.backward(up)
+        return [out.detach(), xs.grad] + [p.grad.clone() for p in blk.parameters()]
+
+    fast, ops = run(True), run(False)
+    names = ["out", "grad_x"] + [n for n, _ in blk.named_parameters()]
+    for name, a, b in zip(names, fast, ops):
+        assert torch.equal(a, b), f"{name} differs"
+
+
+@pytest.mark.parametrize("T,ckpt", [(256, False), (4096, False), (256, True)])
+def test_graph_capture_training_step(T, ckpt):
+    """A whole training step of the fused block (forward, then backward of
+    out * up) captured in one HIP graph: for new inputs copied into the
+    captured buffers, every replay gives the eager step's output and
+    gradients bit for bit, with eager steps between the replays."""
+    C = 1024
+    torch.manual_seed(4)
+    blk = flash_mhc.MHCLiteBlock(4, C, torch.nn.Linear(C, C, bias=False), activation_checkpointing=ckpt).to(DEV, BF16)
+    sx = randn((T, 4, C), 80 + T, dtype=BF16).to(DEV).requires_grad_(True)
+    sup = randn((T, 4, C), 81 + T, dtype=BF16).to(DEV)
+
+    def step(x, up):
+        blk.zero_grad(set_to_none=True)
+        x.grad = None
+        out = blk(x)
+        out.backward(up)
+        return out
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            step(sx, sup)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    blk.zero_grad(set_to_none=True)
+    sx.grad = None
+    with torch.cuda.graph(g):
+        sout = blk(sx)
+        sout.backward(sup)
+    # The gradients the captured backward writes (the eager steps below
+    # attach new ones to the parameters).
+    names = [n for n, _ in blk.named_parameters()]
+    sgrads = [sx.grad] + [p.grad for p in blk.parameters()]
+    for i in range(3):
+        x = randn((T, 4, C), 90 + 7 * i + T, dtype=BF16).to(DEV)
+        up = randn((T, 4, C), 91 + 7 * i + T, dtype=BF16).to(DEV)
+        with torch.no_grad():
+            sx.copy_(x)
+            sup.copy_(up)
+        g.replay()
+        torch.cuda.synchronize()
+        got = [sout.detach().clone()] + [t.clone() for t in sgrads]
+        xe = x.clone().requires_grad_(True)
+        oute = step(xe, up)  # eager step between replays, on other buffers
+        torch.cuda.synchronize()
+        want = [oute.detach(), xe.grad] + [p.grad for p in blk.parameters()]
+        for name, a, b in zip(["out", "grad_x"] + names, got, want):
+            assert torch.equal(a, b), f"replay {i}: {name} differs"
+
+
 @pytest.mark.parametrize("ckpt", [False, True])
 def test_empty_batch_forward_backward(ckpt):
     """T = 0 through the fused block, training and eval: empty outputs, an empty
