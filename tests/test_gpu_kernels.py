@@ -327,11 +327,11 @@ def test_metric_size_sampled():
     nC = 4 * C
     g = torch.Generator().manual_seed(1234)
     idx = torch.randperm(T, generator=g)[:512]
-    # K1 forward reads the tokens before T - 320 MiB / (2 nC) with the
-    # nontemporal hint and the rest with ordinary loads: sample both sides of
-    # that boundary (token 24576 here) and the last tile as well.
-    nt_end = T - (320 << 20) // (2 * nC)
-    idx = torch.cat([idx, torch.arange(nt_end - 80, nt_end + 80), torch.arange(T - 64, T)]).unique()
+    # Besides the random tokens: a contiguous band (whole 64-token tiles of K1
+    # forward and both halves of a 16-token block of K1 backward) and the
+    # last tile.
+    band = T - 40960
+    idx = torch.cat([idx, torch.arange(band - 80, band + 80), torch.arange(T - 64, T)]).unique()
     x = randn((T, 4, C), 1)
     W = randn((32, nC), 2, scale=0.02)
     lo = randn((T, C), 3)
