@@ -110,8 +110,10 @@ __global__ __launch_bounds__(kFinishThreads) void k1_finish_k2(
 // The same with K3 fused, one token per workgroup (blockIdx.x): its first 32
 // lanes finish K1 and run K2 and leave h_pre in LDS; after the barrier all
 // 256 lanes mix the token's streams into layer_input with those values
-// (k3_token, so the results are those of the separate K3 kernel reading the
-// stored h_pre).  Saves K3's launch for few tokens.
+// (k3_token's arithmetic, so the results are those of the separate K3 kernel
+// reading the stored h_pre).  Saves K3's launch for few tokens.  Up to
+// C = 4096 (two 16-byte groups per lane) every lane loads its x vectors
+// before K1's partial sums and K2's chain run, so their latency overlaps.
 template <int VEC>
 __global__ __launch_bounds__(kFinishThreads) void k1_finish_k2_k3(
     const float* __restrict__ part, int S, int nC, const K2Params P, uint16_t* __restrict__ proj,
@@ -119,18 +121,57 @@ __global__ __launch_bounds__(kFinishThreads) void k1_finish_k2_k3(
     const ZeroWords z, const uint16_t* __restrict__ x, uint16_t* __restrict__ layer_input, int C) {
   __shared__ K2Smem sm;
   __shared__ float hsh[kN];  // the token's h_pre, handed from the K2 lanes to all
+  constexpr int kPre = 2;    // 16-byte groups per lane and stream loaded ahead
+  const int64_t t = blockIdx.x;
+  const int lane = static_cast<int>(threadIdx.x);
+  const uint16_t* x0 = x + t * 4 * C;
+  const int ng = C / 8;
+  const bool pre = VEC == 8 && ng <= kPre * kFinishThreads;
+  u32x4 xv[kPre][4];
+  if (pre) {
+#pragma unroll
+    for (int it = 0; it < kPre; ++it) {
+      const int g = lane + it * kFinishThreads;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        xv[it][j] = u32x4{0u, 0u, 0u, 0u};
+        if (g < ng) xv[it][j] = ld_stream(reinterpret_cast<const u32x4*>(x0 + j * C) + g);
+      }
+    }
+  }
   zero_words(z);
   stage_params<kFinishThreads>(P, sm);
-  const int64_t t = blockIdx.x;
   if (threadIdx.x < 32) {
-    const int q = static_cast<int>(threadIdx.x);
+    const int q = lane;
     const float p = finish_token32(part, S, nC, q, t, proj, inv_rms);
     const float y = k2_token32(sm, p, q, t, h_pre, h_post, H);
     if (q < kN) hsh[q] = y;
   }
   __syncthreads();
   const float h[4] = {hsh[0], hsh[1], hsh[2], hsh[3]};
-  k3_token<VEC>(x + t * 4 * C, h, layer_input + t * C, static_cast<int>(threadIdx.x), kFinishThreads, C);
+  if (!pre) {
+    k3_token<VEC>(x0, h, layer_input + t * C, lane, kFinishThreads, C);
+    return;
+  }
+#pragma unroll
+  for (int it = 0; it < kPre; ++it) {
+    const int g = lane + it * kFinishThreads;
+    if (g < ng) {
+      float a[8], b[8], c[8], d[8], o[8];
+      unpack8(xv[it][0], a);
+      unpack8(xv[it][1], b);
+      unpack8(xv[it][2], c);
+      unpack8(xv[it][3], d);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float acc = h[0] * a[e];
+        acc = __builtin_fmaf(h[1], b[e], acc);
+        acc = __builtin_fmaf(h[2], c[e], acc);
+        o[e] = __builtin_fmaf(h[3], d[e], acc);
+      }
+      Lanes<8>::store(layer_input + t * C, g, o);
+    }
+  }
 }
 
 struct PremapWs {

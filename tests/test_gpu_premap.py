@@ -66,7 +66,8 @@ def test_premap_fwd_stages(T, C):
     check_bf16("premap layer_input", li, R, S, 4)
 
 
-@pytest.mark.parametrize("T,C", [(8192, 1024), (300, 1024), (1, 4096), (16400, 1024), (20000, 512)])
+@pytest.mark.parametrize("T,C", [(8192, 1024), (300, 1024), (1, 4096), (64, 4096), (257, 4096), (5, 8192),
+                                 (3, 1000), (16400, 1024), (20000, 512)])
 def test_premap_matches_three_kernels(T, C):
     """Same outputs as K1 + K2 + K3 launched separately (few tokens: both
     take K1's column-split kernel; from T = 16384 on the pre-map runs its
