@@ -964,7 +964,9 @@ constexpr int kFwdR = 4;
 constexpr int kFwdRSmall = 2;
 constexpr int64_t kFwdLargeT = 16384;
 // Split forward for few tokens: one 16-token block per workgroup and up to
-// kSplitMax column ranges per block, aiming at kSplitTarget workgroups; taken
+// kSplitMax column ranges per block, aiming at kSplitTarget workgroups, each
+// range at least one 64-wide chunk per wave of the workgroup (narrower ranges
+// left waves idle: C = 1024, T = 1 ... 257 took 0.5-0.9 us longer); taken
 // when the plan has at least kSplitMinS ranges (T <= 2048): from there on the
 // one-pass kernel with 32-token tiles is faster (T = 3000 ... 6000: 20-40%).
 constexpr int kSplitR = 1;
@@ -1011,7 +1013,7 @@ K1FwdSplit k1_fwd_split(int64_t T, int64_t nC) {
   int64_t S = (kSplitTarget + nblk - 1) / nblk;
   if (S < kSplitMinS) return p;
   S = S < kSplitMax ? S : kSplitMax;
-  S = S < nall ? S : nall;
+  S = S < nall / kFwdSplit ? S : nall / kFwdSplit;
   if (S < 2) return p;
   const int64_t cps = (nall + S - 1) / S;
   S = (nall + cps - 1) / cps;  // every split non-empty

@@ -256,7 +256,7 @@ int premap_fwd_run(const uint16_t* x, const uint16_t* W, const void* alpha_pre, 
 
 // Scratch of fmhc_premap_fwd_noalloc: the column-split forward's partial sums
 // (T x 33 x S4 fp32 for T <= 2048 tokens; at most 2,145,792 bytes over every
-// (T, C), at T = 2032, C = 160).  Each device holds its own copy for the life
+// (T, C), at T = 2032, C = 320).  Each device holds its own copy for the life
 // of the process.  In host code `scratch` names a host-side stand-in, so its
 // device address is looked up once per device (scratch_on_device) and only
 // that address is used.

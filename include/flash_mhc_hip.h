@@ -155,7 +155,7 @@ int64_t fmhc_premap_fwd_workspace_bytes(int64_t T, int64_t C);
  * allocation).  The few-token forward's partial sums go to a static 4 MiB
  * device array of the library (one per device, held until the process ends),
  * which covers every shape (at most 2,145,792 bytes are needed, at T = 2032,
- * C = 160); a shape needing more returns FMHC_ERR_SCRATCH_LIMIT.  The array's
+ * C = 320); a shape needing more returns FMHC_ERR_SCRATCH_LIMIT.  The array's
  * device address is looked up on the first call on each device.  `stream`
  * must belong to the current device (else FMHC_ERR_INVALID_ARGUMENT).  Every
  * call on a device shares that device's array and overwrites what the last

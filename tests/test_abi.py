@@ -155,3 +155,19 @@ def test_ctypes_signatures_cover_argument_counts():
         params = [p for p in m.group(1).split(",") if p.strip() and p.strip() != "void"]
         assert len(params) == len(argtypes), (name, params)
         assert all(isinstance(a, type) and issubclass(a, ctypes._SimpleCData) for a in argtypes)
+
+
+def test_noalloc_scratch_covers_every_shape():
+    """fmhc_premap_fwd_noalloc's static scratch (4 MiB) holds the column-split
+    partial sums of every shape: the workspace sizing (a host computation) over
+    every T the split takes (T <= 2048) and C up to 4096 peaks at 2,145,792
+    bytes, reached at T = 2032, C = 320."""
+    lib = _abi.load()
+    f = lib.fmhc_premap_fwd_workspace_bytes
+    assert f(2032, 320) == 2145792
+    assert f(4096, 1024) == 0 and f(0, 1024) == 0
+    peak = 0
+    for C in range(8, 4097, 8):
+        for T in list(range(1, 129)) + list(range(1904, 2049)):
+            peak = max(peak, f(T, C))
+    assert peak == 2145792 <= 4 << 20

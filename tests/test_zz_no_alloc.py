@@ -65,10 +65,10 @@ def _same(a: torch.Tensor | None, b: torch.Tensor | None, what: str) -> None:
                        b.view(torch.int16) if b.dtype == torch.bfloat16 else b.view(torch.int32)), what
 
 
-# Shrinking shapes in a row.  (2032, 160) needs the largest scratch of any
+# Shrinking shapes in a row.  (2032, 320) needs the largest scratch of any
 # shape (2,145,792 bytes); (100, 1024) and (1, 4096) take fewer column splits
 # over the same array; (4096, 256) takes no scratch (one-pass forward).
-SEQUENCE = [(2032, 160, True), (100, 1024, True), (1, 4096, False), (4096, 256, True), (33, 1000, True)]
+SEQUENCE = [(2032, 320, True), (100, 1024, True), (1, 4096, False), (4096, 256, True), (33, 1000, True)]
 
 
 def _run_sequence(order):
