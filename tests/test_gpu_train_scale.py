@@ -6,7 +6,7 @@ Checks that the fused path runs at this size (x alone is 8.6 GB per block
 input), that every parameter receives a finite gradient, that the compiled
 stack's forward equals the eager one on the same weights, and reports the
 forward + backward time per step and the peak HBM allocated, beside the
-same stack under the reference's rules, eager and compiled.
+same stack eager and under the reference's rules, eager and compiled.
 """
 
 from __future__ import annotations
@@ -73,6 +73,24 @@ def test_training_scale_stack():
     print(f"\n[train-scale] 12 x MHCLiteBlock(4, 4096, Linear(4096, 4096)), T=262144, bf16, "
           f"checkpointing, torch.compile: fwd+bwd {ms:.1f} ms/step, peak HBM allocated {peak_gb:.1f} GB, "
           f"first (compiling) step {compile_s:.1f} s", flush=True)
+
+    # The fused stack eager, for comparison with the compiled one.
+    def eager_step():
+        for p in blocks.parameters():
+            p.grad = None
+        x.grad = None
+        blocks(x).backward(up)
+
+    eager_step()
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    e0.record()
+    for _ in range(n):
+        eager_step()
+    e1.record()
+    torch.cuda.synchronize()
+    print(f"[train-scale] same stack, fused, eager: fwd+bwd {e0.elapsed_time(e1) / n:.1f} ms/step, "
+          f"peak HBM allocated {torch.cuda.max_memory_allocated() / 1e9:.1f} GB", flush=True)
 
     # The same stack with the reference's rules (K2 as PyTorch ops, K1's
     # grad_W as a matmul, separate pre-map ops), for comparison: eager, then
