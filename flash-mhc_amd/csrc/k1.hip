@@ -599,9 +599,9 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
       return bfr[m];
   };
 
-  // Token blocks of this wave, two per trip with double-buffered fragments:
-  // the next block's go / proj_out / inv_rms / x are in flight while the
-  // current block computes (same structure as the forward kernel).
+  // Token blocks of this wave, NBUF fragments in rotation: the next blocks'
+  // go / proj_out / inv_rms / x (and the pre-map operands) are in flight
+  // while the current block computes.
   const int nb = static_cast<int>((nblocks - run + nruns - 1) / nruns);
   auto pos = [&](int i) { return i < nb ? i : nb - 1; };
   auto block_base = [&](int tb) { return (run + static_cast<int64_t>(tb) * nruns) * 16; };
