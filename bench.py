@@ -705,18 +705,29 @@ def main() -> None:
         except (OSError, ValueError):
             traffic = None
 
+    def extra(fn, *a, **kw):
+        # An extra that raises is reported in its field; the kernel step,
+        # which is the metric, is measured either way.
+        if args.no_extras:
+            return None
+        try:
+            return fn(*a, **kw)
+        except Exception as e:  # noqa: BLE001
+            torch.cuda.synchronize()
+            return {"error": f"{type(e).__name__}: {e}"[:300]}
+
     # The latency-bound eval shapes first: after the block steps' seconds of
     # full-bandwidth work the same graph replays measure up to 25% slower.
-    lat = None if args.no_extras else eval_latency(tokens=eval_tokens)
+    lat = extra(eval_latency, tokens=eval_tokens)
     columns = args.columns or not args.no_extras
     alone = isolated_kernels(launch, bm) if columns else None
     probe = Probe()
     cold = cold_kernels(launch, bm, CacheFlush(probe)) if columns else None
-    k1_full_bwd = None if args.no_extras else k1_backward_paths(inp, T, C)
-    blk = None if args.no_extras else block_step(T, C)
+    k1_full_bwd = extra(k1_backward_paths, inp, T, C)
+    blk = extra(block_step, T, C)
     # The block configuration at C = 2048 (same T), with its own layer width.
-    blk2 = None if args.no_extras else block_step(T, 2 * C)
-    blk_small = None if args.no_extras else block_step_graphed()
+    blk2 = extra(block_step, T, 2 * C)
+    blk_small = extra(block_step_graphed)
     ceil = stream_ceilings(probe)
     split = read_write_split(T, n, C, D)
     for name in KERNELS:
