@@ -12,7 +12,8 @@ durations come from a second pass of K steps with an event pair around each
 launch; ``roofline`` describes the dominant kernel (largest average duration),
 timed with those HIP events on the stream it runs on.  ``kernels_isolated``
 times each kernel alone (repeated launches of that kernel), ``kernels_cold``
-each kernel after a flush of L2 and the memory-side cache (CacheFlush).
+each kernel after a flush of L2 and the memory-side cache (CacheFlush), and
+``step_cold`` the whole step after such a flush.
 ``ceilings_GBps`` are 1 GiB streaming probes with the nontemporal hint, as the
 kernels' streaming loads and stores carry (ordinary-access probes beside them
 are labelled ``*_ordinary``).
@@ -447,6 +448,24 @@ class CacheFlush:
         self.probe.run(PROBE_READ_CACHED, self.r, self.w, self.r.numel())
 
 
+def cold_step(step, nbytes: int, flush: CacheFlush, reps: int = 10) -> dict:
+    """The six-kernel step with cold caches: before every step the caches are
+    flushed (CacheFlush), then the step's six launches between two events."""
+    step()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    torch.cuda.synchronize()
+    for e0, e1 in evs:
+        flush()
+        e0.record()
+        step()
+        e1.record()
+    torch.cuda.synchronize()
+    ts = [e0.elapsed_time(e1) for e0, e1 in evs]
+    med = statistics.median(ts)
+    return {"median_ms": round(med, 4), "min_ms": round(min(ts), 4),
+            "GBps": round(nbytes / (med * 1e-3) / 1e9, 1), "frac": round(nbytes / (med * 1e-3) / 1e9 / PEAK_GBPS, 4)}
+
+
 def cold_kernels(launch: dict, bm: dict, flush: CacheFlush, reps: int = 10) -> dict:
     """Each kernel with cold caches: before every launch the caches are flushed
     (CacheFlush), then one launch between two events (the flush is queued
@@ -722,7 +741,9 @@ def main() -> None:
     columns = args.columns or not args.no_extras
     alone = isolated_kernels(launch, bm) if columns else None
     probe = Probe()
-    cold = cold_kernels(launch, bm, CacheFlush(probe)) if columns else None
+    flush = CacheFlush(probe) if columns else None
+    cold = cold_kernels(launch, bm, flush) if columns else None
+    step_cold = cold_step(step, total_bytes, flush) if columns else None
     k1_full_bwd = extra(k1_backward_paths, inp, T, C)
     blk = extra(block_step, T, C)
     # The block configuration at C = 2048 (same T), with its own layer width.
@@ -765,6 +786,7 @@ def main() -> None:
         "kernels": per,
         "kernels_isolated": alone,
         "kernels_cold": cold,
+        "step_cold": step_cold,
         "roofline": {
             "kernel": dom,
             "bound": "hbm",
