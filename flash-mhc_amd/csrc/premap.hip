@@ -203,7 +203,8 @@ int premap_fwd_run(const uint16_t* x, const uint16_t* W, const void* alpha_pre, 
                    uint16_t* layer_input, uint16_t* proj, float* inv_rms, float* h_pre, float* h_post,
                    float* H_merged, uint16_t* zero_word_a, uint16_t* zero_word_b, void* workspace,
                    int64_t workspace_bytes, int64_t T, int64_t C, int64_t n, void* stream) {
-  if (T < 0 || C <= 0 || n != 4 || !param_dtype_ok(param_dtype)) return FMHC_ERR_INVALID_ARGUMENT;
+  if (T < 0 || C <= 0 || C > (int64_t{1} << 24) || n != 4 || !param_dtype_ok(param_dtype))
+    return FMHC_ERR_INVALID_ARGUMENT;
   if (T == 0) return FMHC_OK;
   if (!x || !W || !alpha_pre || !alpha_post || !alpha_res || !bias || !perm || !proj || !inv_rms || !h_pre ||
       !h_post || !H_merged)

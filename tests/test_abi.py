@@ -108,6 +108,10 @@ _FAKE = 4096  # a non-null address that the host-side checks never dereference
         lambda L: L.fmhc_premap_fwd(*[_FAKE] * 7, -1, *[_FAKE] * 6, None, None, None, 0, 8, 16, 4, None),
         lambda L: L.fmhc_premap_fwd_noalloc(*[_FAKE] * 7, 0, *[_FAKE] * 6, None, None, 8, 16, 5, None),  # n != 4
         lambda L: L.fmhc_premap_fwd_noalloc(*[_FAKE] * 7, 0, *[_FAKE] * 6, None, None, -3, 16, 4, None),
+        # C beyond the pre-map's 2^24 (its int offsets), forward and backward
+        lambda L: L.fmhc_premap_fwd(*[_FAKE] * 7, 0, *[_FAKE] * 6, None, None, _FAKE, 1 << 40, 8, (1 << 24) + 8,
+                                    4, None),
+        lambda L: L.fmhc_premap_bwd(*[_FAKE] * 7, 0, *[_FAKE] * 14, 1 << 40, 8, (1 << 24) + 8, 4, None),
     ],
 )
 def test_invalid_arguments_rejected_before_launch(call):
