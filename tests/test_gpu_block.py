@@ -431,19 +431,63 @@ def test_empty_batch_forward_backward(ckpt):
         assert blk.eval()(x.detach()).shape == (0, 4, C)
 
 
-@pytest.mark.parametrize("T,C", [(1, 4096), (64, 4096), (257, 1024), (5000, 1024), (333, 100)])
-def test_nograd_forward_equals_op_path(T, C):
+def _mixed_block(C, fp32_params: bool, rms: bool):
+    """A fused-path block: bf16 throughout, or with its own parameters (W_all,
+    alphas, the RMSNorm weight) in fp32 and only the layer in bf16."""
+    blk = flash_mhc.MHCLiteBlock(4, C, torch.nn.Linear(C, C, bias=False), rmsnorm_weight=rms).to(DEV)
+    if rms:
+        with torch.no_grad():
+            blk.rms_weight.add_(randn((4 * C,), 71, 0.02).to(DEV))
+    if fp32_params:
+        blk.layer.to(BF16)
+    else:
+        blk.to(BF16)
+    return blk
+
+
+@pytest.mark.parametrize("T,C,fp32_params,rms", [(1, 4096, False, False), (64, 4096, False, False),
+                                                  (257, 1024, False, False), (5000, 1024, False, False),
+                                                  (333, 100, False, False), (64, 4096, True, False),
+                                                  (20000, 1024, True, True), (257, 1024, False, True)])
+def test_nograd_forward_equals_op_path(T, C, fp32_params, rms):
     """Without autograd the block launches the pre-map and post-res kernels
-    directly (no custom-op dispatch): the same bits as the op path that a
-    forward recording a graph takes, in eval and in training mode."""
+    directly (no custom-op dispatch): the same bits as the block driven through
+    the torch.library ops, in eval and in training mode, with bf16 or fp32
+    block parameters and with the RMSNorm weight."""
+    from contextlib import nullcontext
+
     torch.manual_seed(7)
-    blk = flash_mhc.MHCLiteBlock(4, C, torch.nn.Linear(C, C, bias=False)).to(DEV, BF16)
+    blk = _mixed_block(C, fp32_params, rms)
     x = randn((T, 4, C), 70 + T, dtype=BF16).to(DEV)
     for training in (False, True):
         blk.train(training)
         with torch.no_grad():
             fast = blk(x)
-        with torch.enable_grad():
-            ops_path = blk(x.clone().requires_grad_(True)).detach()
+            ops_path = blk._run(x, blk._mhc_pre_map_triton, blk._mhc_post_res_triton, nullcontext(), {},
+                                checkpoint_post_res=False)
         torch.cuda.synchronize()
         assert torch.equal(fast, ops_path), (T, C, training)
+
+
+@pytest.mark.parametrize("T,C", [(64, 4096), (5000, 1024)])
+def test_eager_autograd_path_fp32_params_equals_op_path(T, C):
+    """The eager autograd path with fp32 block parameters (bf16 layer) and
+    the RMSNorm weight: output and every gradient equal the op path's."""
+    from contextlib import nullcontext
+
+    torch.manual_seed(8)
+    blk = _mixed_block(C, True, True)
+    x = randn((T, 4, C), 72 + T, dtype=BF16).to(DEV)
+    up = randn((T, 4, C), 73 + T, dtype=BF16).to(DEV)
+
+    def run(fast):
+        blk.zero_grad(set_to_none=True)
+        xs = x.clone().requires_grad_(True)
+        out = blk(xs) if fast else blk._run(xs, blk._mhc_pre_map_triton, blk._mhc_post_res_triton,
+                                            nullcontext(), {}, checkpoint_post_res=False)
+        out.backward(up)
+        return [out.detach(), xs.grad] + [p.grad.clone() for p in blk.parameters()]
+
+    names = ["out", "grad_x"] + [n for n, _ in blk.named_parameters()]
+    for name, a, b in zip(names, run(True), run(False)):
+        assert a.dtype == b.dtype and torch.equal(a, b), f"{name} differs"
