@@ -149,13 +149,53 @@ __device__ __forceinline__ void k3_token(const uint16_t* __restrict__ x0, const 
   }
 }
 
+// Sum over the wave's 64 lanes, every lane receiving the total, with the
+// pairs of group_sum<64>'s butterfly (lanes 32 apart first, then 16, 8, 4,
+// 2, 1), so the same bits, on the VALU's cross-lane moves instead of LDS
+// permutes.  Lanes 32 apart (v_permlane32_swap, which exchanges the two
+// halves of its operands) and 16 apart (v_permlane16_swap: odd rows of one
+// operand with even rows of the other); every 16-lane row then holds the same
+// values, so a rotation by 8 within the row pairs lane j with j ^ 8, and, the
+// values now repeating every 8 lanes, a rotation by 4 pairs j with a lane
+// holding j ^ 4's value; quad permutations pair j ^ 2 and j ^ 1.  Every lane
+// of the wave must be active.
+__device__ __forceinline__ float wave_sum(float v) {
+  const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(h[0]) + __uint_as_float(h[1]);
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  // DPP controls: row_ror:8, row_ror:4, quad_perm [2,3,0,1], quad_perm [1,0,3,2].
+  v += __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0x128, 0xf, 0xf, false));
+  v += __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0x124, 0xf, 0xf, false));
+  v += __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0x4e, 0xf, 0xf, false));
+  v += __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0xb1, 0xf, 0xf, false));
+  return v;
+}
+
+// Sum over the four lanes 16 apart (one per 16-lane row), in the order of the
+// two shuffle steps v += v[lane ^ 16]; v += v[lane ^ 32]: v_permlane16_swap
+// pairs each row with its neighbour, v_permlane32_swap the two halves.  Every
+// lane of the wave must be active.
+__device__ __forceinline__ float rows_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(h[0]) + __uint_as_float(h[1]);
+}
+
 // Sum over the LPT consecutive lanes that share one token (LPT a power of
-// two <= 64).  Every lane of the group receives the total.
+// two <= 64): a butterfly, lanes LPT / 2 apart first.  Every lane of the
+// group receives the total.  LPT = 64 runs wave_sum (same bits) and needs
+// every lane of the wave active.
 template <int LPT>
 __device__ __forceinline__ float group_sum(float v) {
+  if constexpr (LPT == kWave) {
+    return wave_sum(v);
+  } else {
 #pragma unroll
-  for (int m = LPT / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
-  return v;
+    for (int m = LPT / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+    return v;
+  }
 }
 
 // Status helpers shared by the C entry points.

@@ -660,8 +660,7 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
     float dot = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) dot = __builtin_fmaf(gf[e], pf[e], dot);
-    dot += __shfl_xor(dot, 16, kWave);
-    dot += __shfl_xor(dot, 32, kWave);
+    dot = rows_sum(dot);  // the wave is converged here
     float scale[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {

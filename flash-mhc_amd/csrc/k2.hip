@@ -166,15 +166,14 @@ __global__ __launch_bounds__(kK2Threads) void k2_bwd_kernel(
     }
   }
 
-  // Block partial sums: in-wave butterfly, then the four waves in order.
+  // Block partial sums: in-wave butterfly (every lane is here), then the
+  // four waves in order.
   __shared__ float red[kK2Threads / kWave][kNPar];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
 #pragma unroll
   for (int k = 0; k < kNPar; ++k) {
-    float v = par[k];
-#pragma unroll
-    for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    const float v = wave_sum(par[k]);
     if (lane == 0) red[wave][k] = v;
   }
   __syncthreads();
@@ -296,8 +295,7 @@ __global__ __launch_bounds__(kWave) void k2_param_reduce(const float* __restrict
   const int k = blockIdx.x;  // 0 .. kNPar - 1
   float v = 0.f;
   for (int64_t b = threadIdx.x; b < nblocks; b += kWave) v += partial[b * kNPar + k];
-#pragma unroll
-  for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  v = wave_sum(v);
   if (threadIdx.x == 0) {
     void* dst = k == 0 ? g_ap : (k == 1 ? g_apo : (k == 2 ? g_ar : g_bias));
     const int i = k < 3 ? 0 : k - 3;
