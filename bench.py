@@ -30,6 +30,7 @@ bytes model; ``cpu_block_config1`` the fp32 plain-path MHCLiteBlock forward +
 backward at T=4096, C=1024 on the same cores (the golden configuration).
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--T 65536] [--C 1024]
+The reference benchmark's command line (--T --C --n 4 --iters --seed --peak-gbps) is accepted.
 """
 
 from __future__ import annotations
@@ -611,12 +612,19 @@ def cpu_baseline(C: int, tokens: int, iters: int = 3) -> dict:
 
 
 def main() -> None:
+    global PEAK_GBPS  # --peak-gbps
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", "--iters", dest="steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--T", type=int, default=65536)
     ap.add_argument("--C", type=int, default=1024)
+    # The reference benchmark's flags (scripts/benchmark_kernels.py:145-151), so
+    # its documented command line runs here too; --iters is --steps.
+    ap.add_argument("--n", type=int, default=4, help="streams; the kernels are built for n = 4 only")
+    ap.add_argument("--seed", type=int, default=0, help="seed of the synthetic inputs")
+    ap.add_argument("--peak-gbps", type=float, default=PEAK_GBPS,
+                    help="HBM peak the fractions are quoted against (default: MI355X, 8000 GB/s)")
     ap.add_argument("--cpu-tokens", type=int, default=65536,
                     help="tokens of the CPU baseline's sample (default: the whole metric workload)")
     ap.add_argument("--cpu-iters", type=int, default=10, help="timed passes of the CPU baseline (median)")
@@ -632,6 +640,14 @@ def main() -> None:
                          "block step at --T/--C for --steps iterations, or of the eval latency at --eval-T)")
     ap.add_argument("--eval-T", type=str, default="1,64,257,65537", help="token counts of the eval latency")
     args = ap.parse_args()
+    if args.n != 4:
+        print("bench.py: the K1/K3/K4 kernels support n = 4 only (the reference's fused ops raise "
+              "ValueError for other n)", file=sys.stderr)
+        sys.exit(2)
+    if not args.peak_gbps > 0:
+        print("bench.py: --peak-gbps must be positive", file=sys.stderr)
+        sys.exit(2)
+    PEAK_GBPS = args.peak_gbps
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -658,7 +674,7 @@ def main() -> None:
         print(json.dumps({"eval_latency": eval_latency(tokens=eval_tokens, variants=("fused",))}), flush=True)
         return
     T, C, n, D = args.T, args.C, 4, 32
-    inp = make_inputs(T, C)
+    inp = make_inputs(T, C, seed=args.seed)
     launch = make_step(inp, T, C)
     bm = bytes_model(T, n, C, D)
 
