@@ -111,7 +111,7 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
                                                              float* __restrict__ part,
                                                              int64_t T, int nC, int cps,
                                                              const PremapTile pt = PremapTile{}) {
-  static_assert(!TILE || (R == SPLIT && !SPLITK), "the tile epilogue gives each wave one 16-token block");
+  static_assert(!TILE || !SPLITK, "the tile epilogue runs on the one-pass kernel");
   __shared__ float red_acc[SPLIT][R][8][kWave];
   __shared__ float red_ss[SPLIT][R][16];
   __shared__ u32x4 xs[SPLIT][16 * R * 8];  // per wave: 16R tokens x 8 swizzled 16-byte slots
@@ -398,9 +398,10 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
     }
   }
   if constexpr (TILE) {
-    // Wave w owns block r = w.  Same-wave LDS operations are ordered, so the
-    // projections written above and the h_pre written below need no barrier.
-    const int r = wave;
+    // Wave w owns blocks w, w + SPLIT, ... (the blocks whose projections it
+    // stored above).  Same-wave LDS operations are ordered, so those
+    // projections and the h_pre written below need no barrier.
+    for (int r = wave; r < R; r += SPLIT) {
     if (lane < 16) {
 #pragma clang fp contract(off)
       const int64_t t = t0 + 16 * r + lane;
@@ -430,6 +431,7 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
         const float h[4] = {hv[0], hv[1], hv[2], hv[3]};
         k3_token<8>(x + t * 4 * pt.C, h, pt.layer_input + t * pt.C, lane, kWave, pt.C);
       }
+    }
     }
   }
 }
@@ -954,14 +956,26 @@ __global__ __launch_bounds__(256) void k1_bwd_scalar(const uint16_t* __restrict_
 }
 
 constexpr int kFwdSplit = 4;  // waves per workgroup (split of the nC axis)
-// One-pass forward: 16-token blocks per workgroup, kFwdR from kFwdLargeT
-// tokens on, kFwdRSmall below.  Measured against 128-token tiles (one
-// workgroup per CU): equal at T = 65536, C = 1024; 2% faster at T = 262144,
-// C = 4096; 5-7% at T = 65537 (a smaller last tile); 25-50% where 128-token
-// tiles leave CUs idle (T = 8192 ... 32768).
+// One-pass forward: R blocks of 16 tokens per workgroup, the fewest that keep
+// a launch to one round of workgroups on the 256 CUs, up to 4 (k1_fwd_blocks:
+// R = 1 up to T = 4096, 2 up to 8192, 3 up to 12288, 4 beyond; from T = 8193
+// the pre-map forward is one kernel on the same tiles).  A workgroup too many
+// puts a second one on some CUs, and those set the kernel's time.  K1 forward
+// alone at C = 1024, against 32-token tiles below T = 16384 and 64 from there:
+// T = 4096 14.3 -> 12.1 us, 12000 27.9 -> 18.1 us, 16000 30.5 -> 21.9 us; the
+// pre-map forward at T = 9000 / 12000 / 16000 52.5 / 56.0 / 65.3 -> 35.8 /
+// 38.9 / 50.1 us.  More blocks per workgroup than needed cost time (16-token
+// blocks at T = 6000 15.3 -> 20.2 us: W is read from L2 once per 16 tokens).
+// 5-7 blocks would suit 16385-28672 tokens in the op alone (T = 20000
+// 37.6 -> 27.2 us), but with them the pre-map tile kernel exceeds 512
+// registers and spills (119 us at T = 20000 against 71) and with its K2 chain
+// in a separate function it is slower still (81 us); the op keeps the tile's
+// sizes so that the pre-map forward and K1 -> K2 -> K3 give the same bits.
+// 64-token tiles run two workgroups per CU; 128-token tiles (one) measured
+// equal at T = 65536 and 2% slower at T = 262144, C = 4096.
 constexpr int kFwdR = 4;
-constexpr int kFwdRSmall = 2;
-constexpr int64_t kFwdLargeT = 16384;
+constexpr int64_t kFwdCUs = 256;
+constexpr int64_t kFwdLargeT = 32 * kFwdCUs + 1;
 // Split forward for few tokens: one 16-token block per workgroup and up to
 // kSplitMax column ranges per block, aiming at kSplitTarget workgroups, each
 // range at least one 64-wide chunk per wave of the workgroup (narrower ranges
@@ -1023,6 +1037,39 @@ K1FwdSplit k1_fwd_split(int64_t T, int64_t nC) {
   return p;
 }
 
+// Blocks of 16 tokens per workgroup of the one-pass forward for T tokens.
+int k1_fwd_blocks(int64_t T) {
+  const int64_t r = ((T + 15) / 16 + kFwdCUs - 1) / kFwdCUs;
+  return r < 1 ? 1 : (r < kFwdR ? static_cast<int>(r) : kFwdR);
+}
+
+// The one-pass forward with R blocks per workgroup (k1_fwd_blocks); TILE (the
+// pre-map forward) with R = 3 or 4, returning false for fewer.
+template <bool TILE>
+bool launch_k1_fwd_onepass(int R, const uint16_t* x, const uint16_t* W, uint16_t* out, float* inv_rms,
+                           int64_t T, int nc, const PremapTile& pt, hipStream_t s) {
+  const dim3 block(kWave * kFwdSplit);
+  if constexpr (TILE) {
+    if (R < 3) return false;
+    if (R == 3) {
+      k1_fwd_mfma<3, kFwdSplit, false, true><<<dim3(blocks_for(T, 48)), block, 0, s>>>(x, W, out, inv_rms, nullptr,
+                                                                                     T, nc, 0, pt);
+    } else {
+      k1_fwd_mfma<kFwdR, kFwdSplit, false, true><<<dim3(blocks_for(T, 16 * kFwdR)), block, 0, s>>>(
+          x, W, out, inv_rms, nullptr, T, nc, 0, pt);
+    }
+  } else {
+    const dim3 grid(blocks_for(T, 16 * R));
+    switch (R) {
+      case 1: k1_fwd_mfma<1, kFwdSplit, false><<<grid, block, 0, s>>>(x, W, out, inv_rms, nullptr, T, nc, 0); break;
+      case 2: k1_fwd_mfma<2, kFwdSplit, false><<<grid, block, 0, s>>>(x, W, out, inv_rms, nullptr, T, nc, 0); break;
+      case 3: k1_fwd_mfma<3, kFwdSplit, false><<<grid, block, 0, s>>>(x, W, out, inv_rms, nullptr, T, nc, 0); break;
+      default: k1_fwd_mfma<4, kFwdSplit, false><<<grid, block, 0, s>>>(x, W, out, inv_rms, nullptr, T, nc, 0);
+    }
+  }
+  return true;
+}
+
 // K1 forward; with a workspace of k1_fwd_split(T, nC).bytes (allow_split) few
 // tokens take the column-split kernel.
 int k1_fwd_run(const uint16_t* x_flat, const uint16_t* W, uint16_t* out, float* inv_rms, void* ws,
@@ -1041,14 +1088,8 @@ int k1_fwd_run(const uint16_t* x_flat, const uint16_t* W, uint16_t* out, float* 
       const int st = launch_status();
       if (st != FMHC_OK) return st;
       k1_fwd_finish<<<dim3(blocks_for(T, 4)), 256, 0, s>>>(part, out, inv_rms, T, nc, p.S);
-    } else if (T >= kFwdLargeT) {
-      const dim3 grid(blocks_for(T, 16 * kFwdR));
-      k1_fwd_mfma<kFwdR, kFwdSplit, false><<<grid, kWave * kFwdSplit, 0, s>>>(x_flat, W, out, inv_rms, nullptr,
-                                                                             T, nc, 0);
     } else {
-      const dim3 grid(blocks_for(T, 16 * kFwdRSmall));
-      k1_fwd_mfma<kFwdRSmall, kFwdSplit, false><<<grid, kWave * kFwdSplit, 0, s>>>(
-          x_flat, W, out, inv_rms, nullptr, T, nc, 0);
+      launch_k1_fwd_onepass<false>(k1_fwd_blocks(T), x_flat, W, out, inv_rms, T, nc, PremapTile{}, s);
     }
   } else {
     const dim3 grid(blocks_for(T, 4));
@@ -1194,9 +1235,8 @@ bool k1_premap_tile(const uint16_t* x, const uint16_t* W, uint16_t* proj, float*
   if (T < kFwdLargeT || C % 8 != 0 || nC > (int64_t{1} << 24) || !aligned16(x) || !aligned16(W) ||
       !aligned16(proj) || (pt.layer_input && !aligned16(pt.layer_input)))
     return false;
-  const dim3 grid(blocks_for(T, 16 * kFwdR));
-  k1_fwd_mfma<kFwdR, kFwdSplit, false, true><<<grid, kWave * kFwdSplit, 0, s>>>(
-      x, W, proj, inv_rms, nullptr, T, static_cast<int>(nC), 0, pt);
+  if (!launch_k1_fwd_onepass<true>(k1_fwd_blocks(T), x, W, proj, inv_rms, T, static_cast<int>(nC), pt, s))
+    return false;
   *status = launch_status();
   return true;
 }

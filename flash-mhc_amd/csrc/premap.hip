@@ -11,8 +11,9 @@
 // (bf16(grad_x_in + pre-map gradient), autograd's sum), which replaces
 // autograd's separate accumulation pass (1.5 x T x nC x 2 bytes).
 //
-// Forward, many tokens (T >= 16384): one kernel (k1_premap_tile, k1.hip).
-// Each workgroup runs K1 on its 64-token tile with ordinary loads of x, then
+// Forward, many tokens (T > 8192): one kernel (k1_premap_tile, k1.hip).
+// Each workgroup runs K1 on its tile (48 tokens up to T = 12288, 64 beyond)
+// with ordinary loads of x, then
 // K2 on the tile's tokens (one lane per token) and K3 on the tile, whose
 // re-read of the tile's rows finds them in L2 or the memory-side cache: x
 // comes from HBM about once (T = 65536, C = 1024: 178 us against 209 us for

@@ -91,14 +91,15 @@ def test_k1_fwd_misaligned(T, C):
 
 
 @pytest.mark.parametrize("T,C", [(1, 1024), (100, 4096), (2048, 1024), (4095, 1024), (8191, 256), (8192, 1024),
-                                 (16417, 1024), (3, 16384)])
+                                 (8193, 1024), (16417, 1024), (3, 16384)])
 def test_k1_fwd_split_columns(T, C):
     """Few tokens: fmhc_k1_fwd_ws splits the nC axis over workgroups and adds
     the fp32 partials in a fixed order.  Both it and the one-pass fmhc_k1_fwd
     meet the oracle's bound; the split result is deterministic; where no split
     is planned (workspace size 0, always from T = 8192 on) the two entry
-    points run the same kernel: 32-token tiles below T = 16384 (T = 4095:
-    a ragged last tile), 64-token tiles from there (T = 16417: ragged)."""
+    points run the same kernel: 16-token workgroups up to T = 4096 (T = 4095:
+    a ragged last one), 32-token tiles up to 8192, 64-token tiles from 8193
+    (T = 8193, 16417: ragged)."""
     from flash_mhc import _abi
 
     nC = 4 * C
@@ -374,13 +375,15 @@ def test_metric_size_sampled():
     check_fp32("k4 grad_hp @metric", ghp4[i], *ref["grad_hp"], C)
 
 
-def test_k1_fwd_32_token_tiles_wide_rows():
-    """K1 forward below 16384 tokens (32-token workgroups) at wide rows:
-    T = 12300, C = 4096 (x 384 MiB, a ragged last tile).  Sampled tokens
-    (random, and the last tile) against the oracle; the first 4096 rows
-    computed alone give the same bits (a tile's result depends on its own
-    rows only)."""
-    T, C = 12300, 4096
+@pytest.mark.parametrize("T,sub,tile,C", [(4000, 3200, 16, 4096), (6150, 4352, 32, 4096), (12000, 8256, 48, 4096),
+                                          (16000, 12352, 64, 4096), (40000, 30016, 64, 1024)])
+def test_k1_fwd_tile_sizes(T, sub, tile, C):
+    """K1 forward on each one-pass tile size (blocks of 16 tokens, as many per
+    workgroup as keep the launch to one round of 256 workgroups, at most 4:
+    16, 32, 48 and 64 tokens), at wide rows and with a ragged last tile.  Sampled tokens (random, and the last tile) against the
+    oracle; the first `sub` rows computed alone (the same tile size) give the
+    same bits: a tile's result depends on its own rows and its workgroup's
+    place only (the chunk rotation starts at the workgroup id)."""
     nC = 4 * C
     g = torch.Generator().manual_seed(99)
     idx = torch.cat([torch.randperm(T, generator=g)[:192], torch.arange(T - 40, T)]).unique()
@@ -390,11 +393,12 @@ def test_k1_fwd_32_token_tiles_wide_rows():
     proj, inv = K.k1_fwd(xd, Wd)
     i = idx.to(DEV)
     R, S, invR = O.k1_fwd(x[idx], W)
-    check_bf16("k1 proj (R=2, wide rows)", proj[i], R, S, nC)
-    check_rel("k1 inv_rms (R=2, wide rows)", inv[i], invR, rtol=1e-5)
-    p2, i2 = K.k1_fwd(xd[:4096].contiguous(), Wd)
+    check_bf16(f"k1 proj ({tile}-token tiles, wide rows)", proj[i], R, S, nC)
+    check_rel(f"k1 inv_rms ({tile}-token tiles, wide rows)", inv[i], invR, rtol=1e-5)
+    assert sub % tile == 0
+    p2, i2 = K.k1_fwd(xd[:sub].contiguous(), Wd)
     torch.cuda.synchronize()
-    assert torch.equal(p2, proj[:4096]) and torch.equal(i2, inv[:4096])
+    assert torch.equal(p2, proj[:sub]) and torch.equal(i2, inv[:sub])
 
 
 # ---------------------------------------------------------------------------
