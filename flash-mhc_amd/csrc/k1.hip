@@ -967,10 +967,13 @@ constexpr int kFwdSplit = 4;  // waves per workgroup (split of the nC axis)
 // 38.9 / 50.1 us.  More blocks per workgroup than needed cost time (16-token
 // blocks at T = 6000 15.3 -> 20.2 us: W is read from L2 once per 16 tokens).
 // 5-7 blocks would suit 16385-28672 tokens in the op alone (T = 20000
-// 37.6 -> 27.2 us), but with them the pre-map tile kernel exceeds 512
-// registers and spills (119 us at T = 20000 against 71) and with its K2 chain
-// in a separate function it is slower still (81 us); the op keeps the tile's
-// sizes so that the pre-map forward and K1 -> K2 -> K3 give the same bits.
+// 37.6 -> 27.2 us), but not the pre-map tile kernel: it spills (119 us at
+// T = 20000 against 71), is slower with its K2 chain in a separate function
+// (81 us), and without spills (H_merged's LDS reads kept next to their use)
+// runs one workgroup per CU, whose K3 part then has half the waves in flight
+// (70 us at T = 20000, 80-86 against 71-76 us at T = 24576-28672).  The op
+// keeps the tile's sizes so that the pre-map forward and K1 -> K2 -> K3 give
+// the same bits.
 // 64-token tiles run two workgroups per CU; 128-token tiles (one) measured
 // equal at T = 65536 and 2% slower at T = 262144, C = 4096.
 constexpr int kFwdR = 4;
