@@ -28,7 +28,13 @@ namespace fmhc {
 namespace {
 
 constexpr int kK2Threads = 256;
-constexpr int64_t kK2SmallT = 4096;  // forward: 32 lanes per token up to this many tokens
+// 32 lanes per token (k2_fwd_small, k2_bwd_small) up to this many tokens, one
+// thread per token above.  The one-thread kernels take T / 256 workgroups,
+// too few to hide their chain's latency until about 12000 tokens: at
+// T = 4097 / 8192 / 12000 / 16384 the backward takes 13.2 / 13.4 / 13.2 /
+// 13.3 us against 6.9 / 9.7 / 12.7 / 15.3 us with 32 lanes, the forward
+// 7.7 / 7.9 / 8.0 / 8.1 against 4.7 / 6.3 / 7.6 / 9.0 us.
+constexpr int64_t kK2SmallT = 8192;
 
 template <bool VEC>
 __global__ __launch_bounds__(kK2Threads) void k2_fwd_kernel(

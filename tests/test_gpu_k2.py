@@ -57,7 +57,7 @@ PERM = O.permutation_matrices(4)[0]
 
 
 @pytest.mark.parametrize("T,seed,block_init", [(1, 0, False), (255, 1, False), (4096, 2, False),
-                                                (4096, 3, True), (65536, 4, False)])
+                                                (4096, 3, True), (8192, 5, False), (65536, 4, False)])
 def test_k2_fwd_matches_chain(T, seed, block_init):
     proj, alphas, bias, _ = _case(T, seed, block_init=block_init)
     hp, hq, H = K.k2_fwd(*_dev([proj, *alphas, bias, PERM]))
@@ -69,7 +69,7 @@ def test_k2_fwd_matches_chain(T, seed, block_init):
 
 
 @pytest.mark.parametrize("T,seed,block_init", [(1, 10, False), (255, 11, False), (4096, 12, False),
-                                                (4096, 13, True), (65536, 14, False)])
+                                                (4096, 13, True), (8192, 15, False), (65536, 14, False)])
 def test_k2_bwd_matches_chain(T, seed, block_init):
     proj, alphas, bias, grads = _case(T, seed, block_init=block_init)
     gp, ga1, ga2, ga3, gb = K.k2_bwd(*_dev([proj, *alphas, bias, PERM, *grads]))
@@ -225,25 +225,25 @@ def test_k2_bf16_parameters_equal_fp32():
 
 
 def test_k2_fwd_small_and_large_kernels_agree():
-    """Up to 4096 tokens the forward gives each token 32 lanes (one per logit),
+    """Up to 8192 tokens the forward gives each token 32 lanes (one per logit),
     beyond that one thread; both keep the same operation order, so the first
-    4096 tokens of a 4097-token call equal a 4096-token call bit for bit."""
-    proj, alphas, bias, _ = _case(4097, 90)
+    8192 tokens of an 8193-token call equal an 8192-token call bit for bit."""
+    proj, alphas, bias, _ = _case(8193, 90)
     prm = _dev([*alphas, bias, PERM])
     big = K.k2_fwd(proj.to(DEV), *prm)
-    small = K.k2_fwd(proj[:4096].to(DEV), *prm)
+    small = K.k2_fwd(proj[:8192].to(DEV), *prm)
     for u, v in zip(small, big):
-        assert torch.equal(u, v[:4096])
+        assert torch.equal(u, v[:8192])
 
 
 def test_k2_bwd_small_and_large_kernels_agree():
-    """The backward likewise: 32 lanes per token up to 4096 tokens, one thread
+    """The backward likewise: 32 lanes per token up to 8192 tokens, one thread
     beyond, with the same per-token operation order, so grad_proj of the first
-    4096 tokens of a 4097-token call equals a 4096-token call bit for bit (the
+    8192 tokens of an 8193-token call equals an 8192-token call bit for bit (the
     parameter gradients add the tokens in a different, fixed, order)."""
-    proj, alphas, bias, grads = _case(4097, 91)
+    proj, alphas, bias, grads = _case(8193, 91)
     prm = _dev([*alphas, bias, PERM])
     g = _dev(list(grads))
     big = K.k2_bwd(proj.to(DEV), *prm, *g)
-    small = K.k2_bwd(proj[:4096].to(DEV), *prm, *[t[:4096] for t in g])
-    assert torch.equal(small[0], big[0][:4096])
+    small = K.k2_bwd(proj[:8192].to(DEV), *prm, *[t[:8192] for t in g])
+    assert torch.equal(small[0], big[0][:8192])
