@@ -820,9 +820,17 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
 // i = (((slice * 8 + m) * 2 + h) * 4 + r) * 64 + lane stands for
 // d = 16 h + (lane & 15), k = 128 slice + 8 (4 (lane >> 4) + r) + m; each
 // thread sums four consecutive elements (16-byte loads, four parts per trip).
+// Workgroups from dw_blocks on sum K2's parameter gradients instead, one wave
+// per parameter (the pre-map backward; one launch fewer than K2's own reduce).
 __global__ __launch_bounds__(256) void k1_dw_reduce(const float* __restrict__ partial,
                                                     uint16_t* __restrict__ dW, int64_t nparts,
-                                                    int nslices, int nC) {
+                                                    int nslices, int nC, unsigned dw_blocks,
+                                                    const K2ParamSums k2) {
+  if (blockIdx.x >= dw_blocks) {
+    const int k = static_cast<int>(blockIdx.x - dw_blocks) * 4 + static_cast<int>(threadIdx.x >> 6);
+    if (k < kNPar) k2_param_sum(k2, k, static_cast<int>(threadIdx.x & (kWave - 1)));  // whole waves
+    return;
+  }
   const int64_t per_part = static_cast<int64_t>(nslices) * (8 * 2 * 4 * kWave);
   const int64_t i0 = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
   if (i0 >= per_part) return;
@@ -1220,7 +1228,8 @@ extern "C" int fmhc_k1_bwd(const uint16_t* x_flat, const uint16_t* W, const uint
     const int st = launch_status();
     if (st != FMHC_OK) return st;
     const int64_t per_part = static_cast<int64_t>(nslices) * (8 * 2 * 4 * kWave);
-    k1_dw_reduce<<<dim3(blocks_for(per_part / 4, 256)), 256, 0, s>>>(partial, grad_W, nruns, nslices, nc);
+    const unsigned nb = blocks_for(per_part / 4, 256);
+    k1_dw_reduce<<<dim3(nb), 256, 0, s>>>(partial, grad_W, nruns, nslices, nc, nb, K2ParamSums{});
     return launch_status();
   }
   const int st = fmhc_k1_bwd_dx(x_flat, W, grad_out, proj_out, inv_rms, grad_x, T, nC, D_out, stream);
@@ -1269,11 +1278,12 @@ bool k1_bwd_premap_fused(const void* x, const void* W, const void* go, const voi
 int k1_bwd_premap(const uint16_t* x_flat, const uint16_t* W, const uint16_t* grad_proj,
                   const uint16_t* proj, const float* inv_rms, const uint16_t* go3, const float* h_pre,
                   const uint16_t* grad_x_in, uint16_t* grad_x, uint16_t* grad_W, void* workspace,
-                  int64_t workspace_bytes, int64_t T, int64_t C, hipStream_t s) {
+                  int64_t workspace_bytes, int64_t T, int64_t C, const K2ParamSums& k2_sums, hipStream_t s) {
   const int64_t nC = 4 * C;
   const int nc = static_cast<int>(nC);
   if (T == 0) {
     k1_dw_zero<<<dim3(blocks_for(static_cast<int64_t>(kDout) * nC, 256)), 256, 0, s>>>(grad_W, nc);
+    launch_k2_param_reduce(k2_sums, s);
     return launch_status();
   }
   if (k1_bwd_premap_fused(x_flat, W, grad_proj, proj, inv_rms, grad_x, go3, grad_x_in, C)) {
@@ -1291,7 +1301,9 @@ int k1_bwd_premap(const uint16_t* x_flat, const uint16_t* W, const uint16_t* gra
     const int st = launch_status();
     if (st != FMHC_OK) return st;
     const int64_t per_part = static_cast<int64_t>(nslices) * (8 * 2 * 4 * kWave);
-    k1_dw_reduce<<<dim3(blocks_for(per_part / 4, 256)), 256, 0, s>>>(partial, grad_W, nruns, nslices, nc);
+    const unsigned nb = blocks_for(per_part / 4, 256);
+    constexpr unsigned k2_blocks = (kNPar + 3) / 4;  // one wave per K2 parameter
+    k1_dw_reduce<<<dim3(nb + k2_blocks), 256, 0, s>>>(partial, grad_W, nruns, nslices, nc, nb, k2_sums);
     return launch_status();
   }
   k1_bwd_scalar<true><<<dim3(blocks_for(T, 4)), 256, 0, s>>>(x_flat, W, grad_proj, proj, inv_rms, grad_x,
@@ -1300,6 +1312,7 @@ int k1_bwd_premap(const uint16_t* x_flat, const uint16_t* W, const uint16_t* gra
   if (st != FMHC_OK) return st;
   k1_dw_scalar<<<dim3(blocks_for(static_cast<int64_t>(kDout) * nC, 256)), 256, 0, s>>>(
       x_flat, grad_proj, inv_rms, grad_W, T, nc);
+  launch_k2_param_reduce(k2_sums, s);
   return launch_status();
 }
 

@@ -1,4 +1,4 @@
-// K1 pieces used by the pre-map region (premap.hip); defined in k1.hip.
+// K1 and K2 pieces used by the pre-map region (premap.hip); defined in k1.hip and k2.hip.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -48,10 +48,20 @@ bool k1_bwd_premap_fused(const void* x, const void* W, const void* go, const voi
 // grad_W (32, 4C) and grad_x = bf16(bf16(h_pre[t, j] go3[t, c]) + bf16(dx)) of
 // K1 for x (T, 4, C); with grad_x_in (may be null, must not overlap grad_x)
 // grad_x = bf16(grad_x_in + that).  `workspace` as fmhc_k1_bwd
-// (fmhc_k1_bwd_workspace_bytes(T, 4C)).
+// (fmhc_k1_bwd_workspace_bytes(T, 4C)).  K2's parameter gradients
+// (k2_bwd_partials) are summed by the same launch as grad_W's partials.
 int k1_bwd_premap(const uint16_t* x_flat, const uint16_t* W, const uint16_t* grad_proj,
                   const uint16_t* proj, const float* inv_rms, const uint16_t* go3, const float* h_pre,
                   const uint16_t* grad_x_in, uint16_t* grad_x, uint16_t* grad_W, void* workspace,
-                  int64_t workspace_bytes, int64_t T, int64_t C, hipStream_t s);
+                  int64_t workspace_bytes, int64_t T, int64_t C, const K2ParamSums& k2_sums, hipStream_t s);
+
+// fmhc_k2_bwd without its last launch: K2's backward writes grad_proj and the
+// per-workgroup parameter partials, and *sums describes what remains to sum
+// (k2_param_sum; launch_k2_param_reduce, or folded into another launch).
+int k2_bwd_partials(const uint16_t* proj, const K2Params& P, const float* grad_h_pre, const float* grad_h_post,
+                    const float* grad_H_merged, uint16_t* grad_proj, void* grad_alpha_pre, void* grad_alpha_post,
+                    void* grad_alpha_res, void* grad_bias, void* workspace, int64_t workspace_bytes, int64_t T,
+                    hipStream_t s, K2ParamSums* sums);
+void launch_k2_param_reduce(const K2ParamSums& sums, hipStream_t s);
 
 }  // namespace fmhc

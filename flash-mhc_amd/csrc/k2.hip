@@ -191,9 +191,6 @@ __global__ __launch_bounds__(kK2Threads) void k2_bwd_kernel(
   }
 }
 
-// One wave per parameter gradient: lanes take blocks lane, lane + 64, ...,
-// then a butterfly; the result is rounded to bf16 (the reference sums a bf16
-// tensor) and stored in the parameter's dtype (fp32 or bf16).
 // Backward for few tokens, 32 lanes per token (lane q: logit q) and 8 tokens
 // per workgroup.  Every per-token value is k2_bwd_kernel's: the forward is
 // k2_token32's (bit-identical to the chain), and each sum over a token's
@@ -295,21 +292,9 @@ __global__ __launch_bounds__(kK2Threads) void k2_bwd_small(
   }
 }
 
-__global__ __launch_bounds__(kWave) void k2_param_reduce(const float* __restrict__ partial,
-                                                         int64_t nblocks, void* g_ap, void* g_apo,
-                                                         void* g_ar, void* g_bias, bool bf16) {
-  const int k = blockIdx.x;  // 0 .. kNPar - 1
-  float v = 0.f;
-  for (int64_t b = threadIdx.x; b < nblocks; b += kWave) v += partial[b * kNPar + k];
-  v = wave_sum(v);
-  if (threadIdx.x == 0) {
-    void* dst = k == 0 ? g_ap : (k == 1 ? g_apo : (k == 2 ? g_ar : g_bias));
-    const int i = k < 3 ? 0 : k - 3;
-    if (bf16)
-      static_cast<uint16_t*>(dst)[i] = f32_to_bf16(v);
-    else
-      static_cast<float*>(dst)[i] = rb(v);
-  }
+// One wave per parameter gradient (k2_param_sum).
+__global__ __launch_bounds__(kWave) void k2_param_reduce(const K2ParamSums r) {
+  k2_param_sum(r, static_cast<int>(blockIdx.x), static_cast<int>(threadIdx.x));
 }
 
 bool k2_bad(int64_t T, int64_t n) { return T < 0 || n != kN; }
@@ -365,19 +350,13 @@ extern "C" int64_t fmhc_k2_bwd_workspace_bytes(int64_t T) {
   return k2_bwd_blocks(T) * kNPar * static_cast<int64_t>(sizeof(float));
 }
 
-extern "C" int fmhc_k2_bwd(const uint16_t* proj, const void* alpha_pre, const void* alpha_post,
-                           const void* alpha_res, const void* bias, const void* perm, int param_dtype,
-                           const float* grad_h_pre, const float* grad_h_post,
-                           const float* grad_H_merged, uint16_t* grad_proj, void* grad_alpha_pre,
-                           void* grad_alpha_post, void* grad_alpha_res, void* grad_bias,
-                           void* workspace, int64_t workspace_bytes, int64_t T, int64_t n,
-                           void* stream) {
-  using namespace fmhc;
-  if (k2_bad(T, n)) return FMHC_ERR_INVALID_ARGUMENT;
-  K2Params P;
-  if (!k2_params(alpha_pre, alpha_post, alpha_res, bias, perm, param_dtype, P)) return FMHC_ERR_INVALID_ARGUMENT;
+namespace fmhc {
+
+int k2_bwd_partials(const uint16_t* proj, const K2Params& P, const float* grad_h_pre, const float* grad_h_post,
+                    const float* grad_H_merged, uint16_t* grad_proj, void* grad_alpha_pre, void* grad_alpha_post,
+                    void* grad_alpha_res, void* grad_bias, void* workspace, int64_t workspace_bytes, int64_t T,
+                    hipStream_t s, K2ParamSums* sums) {
   if (!grad_alpha_pre || !grad_alpha_post || !grad_alpha_res || !grad_bias) return FMHC_ERR_INVALID_ARGUMENT;
-  hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t nblocks = k2_bwd_blocks(T);
   float* partial = static_cast<float*>(workspace);
   if (T > 0) {
@@ -396,8 +375,34 @@ extern "C" int fmhc_k2_bwd(const uint16_t* proj, const void* alpha_pre, const vo
     const int st = launch_status();
     if (st != FMHC_OK) return st;
   }
-  // T == 0: the reduce writes zero gradients (nblocks = 0 partials).
-  k2_param_reduce<<<dim3(kNPar), kWave, 0, s>>>(partial, T > 0 ? nblocks : 0, grad_alpha_pre,
-                                                grad_alpha_post, grad_alpha_res, grad_bias, P.bf16);
+  // T == 0: the sums write zero gradients (nblocks = 0 partials).
+  *sums = K2ParamSums{partial, T > 0 ? nblocks : 0, grad_alpha_pre, grad_alpha_post, grad_alpha_res, grad_bias,
+                      P.bf16};
+  return FMHC_OK;
+}
+
+void launch_k2_param_reduce(const K2ParamSums& sums, hipStream_t s) {
+  k2_param_reduce<<<dim3(kNPar), kWave, 0, s>>>(sums);
+}
+
+}  // namespace fmhc
+
+extern "C" int fmhc_k2_bwd(const uint16_t* proj, const void* alpha_pre, const void* alpha_post,
+                           const void* alpha_res, const void* bias, const void* perm, int param_dtype,
+                           const float* grad_h_pre, const float* grad_h_post,
+                           const float* grad_H_merged, uint16_t* grad_proj, void* grad_alpha_pre,
+                           void* grad_alpha_post, void* grad_alpha_res, void* grad_bias,
+                           void* workspace, int64_t workspace_bytes, int64_t T, int64_t n,
+                           void* stream) {
+  using namespace fmhc;
+  if (k2_bad(T, n)) return FMHC_ERR_INVALID_ARGUMENT;
+  K2Params P;
+  if (!k2_params(alpha_pre, alpha_post, alpha_res, bias, perm, param_dtype, P)) return FMHC_ERR_INVALID_ARGUMENT;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  K2ParamSums sums;
+  const int st = k2_bwd_partials(proj, P, grad_h_pre, grad_h_post, grad_H_merged, grad_proj, grad_alpha_pre,
+                                 grad_alpha_post, grad_alpha_res, grad_bias, workspace, workspace_bytes, T, s, &sums);
+  if (st != FMHC_OK) return st;
+  launch_k2_param_reduce(sums, s);
   return launch_status();
 }

@@ -90,6 +90,36 @@ __device__ __forceinline__ void load_proj(const uint16_t* __restrict__ row, floa
   }
 }
 
+// K2 backward's parameter gradients from its per-workgroup partials
+// (partial[b * kNPar + k] for workgroup b): parameter k (0-2: the alphas,
+// 3 + j: bias j) as one wave's sum, lane l adding workgroups l, l + 64, ...
+// in order, then wave_sum; rounded to bf16 (the reference sums a bf16
+// tensor) and stored in the parameters' dtype.  nblocks = 0 writes zeros.
+struct K2ParamSums {
+  const float* partial = nullptr;
+  int64_t nblocks = 0;
+  void* g_ap = nullptr;
+  void* g_apo = nullptr;
+  void* g_ar = nullptr;
+  void* g_bias = nullptr;
+  bool bf16 = false;
+};
+
+// Every lane of the wave must be active (wave_sum).
+__device__ __forceinline__ void k2_param_sum(const K2ParamSums& r, int k, int lane) {
+  float v = 0.f;
+  for (int64_t b = lane; b < r.nblocks; b += kWave) v += r.partial[b * kNPar + k];
+  v = wave_sum(v);
+  if (lane == 0) {
+    void* dst = k == 0 ? r.g_ap : (k == 1 ? r.g_apo : (k == 2 ? r.g_ar : r.g_bias));
+    const int i = k < 3 ? 0 : k - 3;
+    if (r.bf16)
+      static_cast<uint16_t*>(dst)[i] = f32_to_bf16(v);
+    else
+      static_cast<float*>(dst)[i] = rb(v);
+  }
+}
+
 // Forward chain of one token.  Fills the values the backward reuses.
 struct K2Fwd {
   float hp[kN], hq[kN], sq[kN];  // h_pre, h_post, sigmoid of the post logits

@@ -362,13 +362,17 @@ extern "C" int fmhc_premap_bwd(const uint16_t* x, const uint16_t* W, const void*
   int st = FMHC_OK;
   const bool fused = T > 0 && k1_bwd_premap_fused(x, W, gp, proj, inv_rms, grad_x, grad_layer_input, grad_x_in, C);
   if (T > 0) st = fmhc_k3_bwd(x, h_pre, grad_layer_input, fused ? nullptr : grad_x, gh, T, C, n, stream);
+  // K2's backward, whose parameter partials K1's grad_W reduce also sums.
+  K2Params P;
+  if (st == FMHC_OK && !k2_params(alpha_pre, alpha_post, alpha_res, bias, perm, param_dtype, P))
+    st = FMHC_ERR_INVALID_ARGUMENT;
+  K2ParamSums sums;
   if (st == FMHC_OK)
-    st = fmhc_k2_bwd(proj, alpha_pre, alpha_post, alpha_res, bias, perm, param_dtype, gh, grad_h_post,
-                     grad_H_merged, gp,
-                     grad_alpha_pre, grad_alpha_post, grad_alpha_res, grad_bias, T > 0 ? ws + w.k2 : nullptr,
-                     T > 0 ? w.k1 - w.k2 : 0, T, n, stream);
+    st = k2_bwd_partials(proj, P, gh, grad_h_post, grad_H_merged, gp, grad_alpha_pre, grad_alpha_post,
+                         grad_alpha_res, grad_bias, T > 0 ? ws + w.k2 : nullptr, T > 0 ? w.k1 - w.k2 : 0, T, s,
+                         &sums);
   if (st == FMHC_OK)
     st = k1_bwd_premap(x, W, gp, proj, inv_rms, grad_layer_input, h_pre, grad_x_in, grad_x, grad_W,
-                       T > 0 ? ws + w.k1 : nullptr, T > 0 ? w.total - w.k1 : 0, T, C, s);
+                       T > 0 ? ws + w.k1 : nullptr, T > 0 ? w.total - w.k1 : 0, T, C, sums, s);
   return st;
 }
