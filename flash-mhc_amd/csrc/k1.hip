@@ -1,7 +1,7 @@
 // K1: fused RMSNorm over the flattened n*C stream + the D_out = 32 wide
 // coefficient projection, and its backward.
 //
-// Kernels: k1_fwd_mfma (one pass over x per 32- or 64-token workgroup, or, for
+// Kernels: k1_fwd_mfma (one pass over x per workgroup of 16-64 tokens, or, for
 // few tokens, a column split whose partial sums k1_fwd_finish adds),
 // k1_bwd_mfma (dx; with DW also grad_W's per-run partials, which
 // k1_dw_reduce adds; with EPI / GI the pre-map backward's extra terms of

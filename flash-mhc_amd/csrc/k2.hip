@@ -14,9 +14,10 @@
 //   H_res  = rb(a @ perm),  H_merged = rb(H_res - rb(h_post (x) h_pre))
 // The outputs are the fp32 casts the fused path hands to K3 / K4
 // (block.py:176-177).  The backward follows PyTorch's GPU kernels, whose bf16
-// sigmoid and softmax backward round intermediate products as well.  The backward also produces per-block partial sums of
-// the alpha and bias gradients (sums over tokens), which k2_param_reduce adds
-// in a fixed order.
+// sigmoid and softmax backward round intermediate products as well.  The
+// backward also produces per-workgroup partial sums of the alpha and bias
+// gradients (sums over tokens), which k2_param_sum adds in a fixed order
+// (k2_param_reduce, or the pre-map backward's grad_W reduce).
 
 #include <hip/hip_runtime.h>
 

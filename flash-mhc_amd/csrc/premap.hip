@@ -36,7 +36,7 @@
 #include "k2_chain.h"
 
 // 1: the forward of many tokens runs as one kernel, K1 with K2 and K3 on
-// each 64-token tile (k1_premap_tile); 0 (an evidence build): K1, K2 and K3
+// each tile (k1_premap_tile); 0 (an evidence build): K1, K2 and K3
 // as three kernels, each reading x from HBM.
 #ifndef FMHC_PREMAP_TILE
 #define FMHC_PREMAP_TILE 1
