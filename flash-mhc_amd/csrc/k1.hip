@@ -97,9 +97,10 @@ struct FwdFrag {
 // workgroup writes its fp32 partial sums (32 projections + sum of squares per
 // token) to part[t][33][S4] (S4 = gridDim.y rounded up to 4) instead of the
 // outputs; k1_fwd_finish adds the gridDim.y partials in order.
-// TILE (the pre-map region for many tokens, premap.hip): after a tile's
-// projections, the same workgroup runs K2 on the tile's tokens (one lane per
-// token, the K2 kernel's per-token chain) and then K3, mixing the tile's
+// TILE (the pre-map region without the column split, premap.hip): after a
+// tile's projections, the same workgroup runs K2 on the tile's tokens (one
+// lane per token, the K2 kernel's per-token chain) and then K3 (each wave its
+// own blocks; with fewer blocks than waves, all waves over the tile), mixing the tile's
 // streams into the layer input while L2 and the memory-side cache may still
 // hold the rows it just read (its x loads are ordinary loads, which allocate
 // there).  Same values as K1 -> K2 -> K3 launched separately.
@@ -399,8 +400,11 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
   }
   if constexpr (TILE) {
     // Wave w owns blocks w, w + SPLIT, ... (the blocks whose projections it
-    // stored above).  Same-wave LDS operations are ordered, so those
-    // projections and the h_pre written below need no barrier.
+    // stored above) and runs K2 for their tokens on lanes 0-15.  With at least
+    // a block per wave it also runs K3 over its blocks: same-wave LDS
+    // operations are ordered, so those projections and the h_pre written below
+    // need no barrier.  With fewer blocks than waves, every wave takes a share
+    // of the tile's tokens in K3, after a barrier.
     for (int r = wave; r < R; r += SPLIT) {
     if (lane < 16) {
 #pragma clang fp contract(off)
@@ -423,7 +427,7 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
       }
       tile_sm.hpre[16 * r + lane] = hp;
     }
-    if (pt.layer_input) {
+    if (R >= SPLIT && pt.layer_input) {
       for (int tt = 0; tt < 16; ++tt) {
         const int64_t t = t0 + 16 * r + tt;
         if (t >= T) break;
@@ -432,6 +436,16 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
         k3_token<8>(x + t * 4 * pt.C, h, pt.layer_input + t * pt.C, lane, kWave, pt.C);
       }
     }
+    }
+    if (R < SPLIT && pt.layer_input) {  // the same branch in every thread
+      __syncthreads();
+      for (int tt = wave; tt < 16 * R; tt += SPLIT) {
+        const int64_t t = t0 + tt;
+        if (t >= T) break;
+        const f32x4 hv = tile_sm.hpre[tt];
+        const float h[4] = {hv[0], hv[1], hv[2], hv[3]};
+        k3_token<8>(x + t * 4 * pt.C, h, pt.layer_input + t * pt.C, lane, kWave, pt.C);
+      }
     }
   }
 }
@@ -966,8 +980,10 @@ __global__ __launch_bounds__(256) void k1_bwd_scalar(const uint16_t* __restrict_
 constexpr int kFwdSplit = 4;  // waves per workgroup (split of the nC axis)
 // One-pass forward: R blocks of 16 tokens per workgroup, the fewest that keep
 // a launch to one round of workgroups on the 256 CUs, up to 4 (k1_fwd_blocks:
-// R = 1 up to T = 4096, 2 up to 8192, 3 up to 12288, 4 beyond; from T = 8193
-// the pre-map forward is one kernel on the same tiles).  A workgroup too many
+// R = 1 up to T = 4096, 2 up to 8192, 3 up to 12288, 4 beyond; where the
+// column split below is not planned the pre-map forward is one kernel on the
+// same tiles: against K1 -> K2 -> K3 at C = 1024, T = 4096 / 6000 / 8192
+// 29.5 / 36.1 / 41.2 -> 27.1 / 34.5 / 37.2 us).  A workgroup too many
 // puts a second one on some CUs, and those set the kernel's time.  K1 forward
 // alone at C = 1024, against 32-token tiles below T = 16384 and 64 from there:
 // T = 4096 14.3 -> 12.1 us, 12000 27.9 -> 18.1 us, 16000 30.5 -> 21.9 us; the
@@ -986,13 +1002,12 @@ constexpr int kFwdSplit = 4;  // waves per workgroup (split of the nC axis)
 // equal at T = 65536 and 2% slower at T = 262144, C = 4096.
 constexpr int kFwdR = 4;
 constexpr int64_t kFwdCUs = 256;
-constexpr int64_t kFwdLargeT = 32 * kFwdCUs + 1;
 // Split forward for few tokens: one 16-token block per workgroup and up to
 // kSplitMax column ranges per block, aiming at kSplitTarget workgroups, each
 // range at least one 64-wide chunk per wave of the workgroup (narrower ranges
 // left waves idle: C = 1024, T = 1 ... 257 took 0.5-0.9 us longer); taken
-// when the plan has at least kSplitMinS ranges (T <= 2048): from there on the
-// one-pass kernel with 32-token tiles is faster (T = 3000 ... 6000: 20-40%).
+// when the plan has at least kSplitMinS ranges (T <= 2720 from C = 128 on):
+// from there on the one-pass kernel is faster (T = 3000 ... 6000: 20-40%).
 constexpr int kSplitR = 1;
 constexpr int64_t kSplitTarget = 512;
 constexpr int64_t kSplitMax = 64;
@@ -1054,23 +1069,28 @@ int k1_fwd_blocks(int64_t T) {
   return r < 1 ? 1 : (r < kFwdR ? static_cast<int>(r) : kFwdR);
 }
 
-// The one-pass forward with R blocks per workgroup (k1_fwd_blocks); TILE (the
-// pre-map forward) with R = 3 or 4, returning false for fewer.
+// The one-pass forward with R blocks per workgroup (k1_fwd_blocks); TILE: the
+// pre-map forward on the same tiles.
 template <bool TILE>
-bool launch_k1_fwd_onepass(int R, const uint16_t* x, const uint16_t* W, uint16_t* out, float* inv_rms,
+void launch_k1_fwd_onepass(int R, const uint16_t* x, const uint16_t* W, uint16_t* out, float* inv_rms,
                            int64_t T, int nc, const PremapTile& pt, hipStream_t s) {
   const dim3 block(kWave * kFwdSplit);
+  const dim3 grid(blocks_for(T, 16 * R));
   if constexpr (TILE) {
-    if (R < 3) return false;
-    if (R == 3) {
-      k1_fwd_mfma<3, kFwdSplit, false, true><<<dim3(blocks_for(T, 48)), block, 0, s>>>(x, W, out, inv_rms, nullptr,
-                                                                                     T, nc, 0, pt);
-    } else {
-      k1_fwd_mfma<kFwdR, kFwdSplit, false, true><<<dim3(blocks_for(T, 16 * kFwdR)), block, 0, s>>>(
-          x, W, out, inv_rms, nullptr, T, nc, 0, pt);
+    switch (R) {
+      case 1:
+        k1_fwd_mfma<1, kFwdSplit, false, true><<<grid, block, 0, s>>>(x, W, out, inv_rms, nullptr, T, nc, 0, pt);
+        break;
+      case 2:
+        k1_fwd_mfma<2, kFwdSplit, false, true><<<grid, block, 0, s>>>(x, W, out, inv_rms, nullptr, T, nc, 0, pt);
+        break;
+      case 3:
+        k1_fwd_mfma<3, kFwdSplit, false, true><<<grid, block, 0, s>>>(x, W, out, inv_rms, nullptr, T, nc, 0, pt);
+        break;
+      default:
+        k1_fwd_mfma<4, kFwdSplit, false, true><<<grid, block, 0, s>>>(x, W, out, inv_rms, nullptr, T, nc, 0, pt);
     }
   } else {
-    const dim3 grid(blocks_for(T, 16 * R));
     switch (R) {
       case 1: k1_fwd_mfma<1, kFwdSplit, false><<<grid, block, 0, s>>>(x, W, out, inv_rms, nullptr, T, nc, 0); break;
       case 2: k1_fwd_mfma<2, kFwdSplit, false><<<grid, block, 0, s>>>(x, W, out, inv_rms, nullptr, T, nc, 0); break;
@@ -1078,7 +1098,6 @@ bool launch_k1_fwd_onepass(int R, const uint16_t* x, const uint16_t* W, uint16_t
       default: k1_fwd_mfma<4, kFwdSplit, false><<<grid, block, 0, s>>>(x, W, out, inv_rms, nullptr, T, nc, 0);
     }
   }
-  return true;
 }
 
 // K1 forward; with a workspace of k1_fwd_split(T, nC).bytes (allow_split) few
@@ -1244,11 +1263,12 @@ namespace fmhc {
 bool k1_premap_tile(const uint16_t* x, const uint16_t* W, uint16_t* proj, float* inv_rms, const PremapTile& pt,
                     int64_t T, int64_t C, hipStream_t s, int* status) {
   const int64_t nC = 4 * C;
-  if (T < kFwdLargeT || C % 8 != 0 || nC > (int64_t{1} << 24) || !aligned16(x) || !aligned16(W) ||
+  // Where K1's column split is planned (few tokens) the pre-map forward takes
+  // it and its second stage fused with K2 and K3 (premap.hip) instead.
+  if (T <= 0 || k1_fwd_split(T, nC).S > 1 || C % 8 != 0 || nC > (int64_t{1} << 24) || !aligned16(x) || !aligned16(W) ||
       !aligned16(proj) || (pt.layer_input && !aligned16(pt.layer_input)))
     return false;
-  if (!launch_k1_fwd_onepass<true>(k1_fwd_blocks(T), x, W, proj, inv_rms, T, static_cast<int>(nC), pt, s))
-    return false;
+  launch_k1_fwd_onepass<true>(k1_fwd_blocks(T), x, W, proj, inv_rms, T, static_cast<int>(nC), pt, s);
   *status = launch_status();
   return true;
 }

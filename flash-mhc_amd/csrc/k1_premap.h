@@ -29,10 +29,11 @@ struct PremapTile {
   ZeroWords z{};
 };
 
-// The pre-map forward of many tokens as one kernel, when its shapes allow
-// (T > 8192, C % 8 == 0, 16-byte aligned x / W / proj / layer_input): K1 on
-// tiles of 48 or 64 tokens, then K2 and K3 on each tile by the same workgroup.  Returns false (nothing launched) when they do
-// not; otherwise launches and returns true with *status set.
+// The pre-map forward as one kernel, when T takes K1's one-pass forward (no
+// column split planned) and the shapes allow (C % 8 == 0, 16-byte aligned x /
+// W / proj / layer_input): K1 on tiles of 16 to 64 tokens, then K2 and K3 on
+// each tile by the same workgroup.  Returns false (nothing launched) when
+// they do not; otherwise launches and returns true with *status set.
 bool k1_premap_tile(const uint16_t* x, const uint16_t* W, uint16_t* proj, float* inv_rms, const PremapTile& pt,
                     int64_t T, int64_t C, hipStream_t s, int* status);
 

@@ -11,20 +11,22 @@
 // (bf16(grad_x_in + pre-map gradient), autograd's sum), which replaces
 // autograd's separate accumulation pass (1.5 x T x nC x 2 bytes).
 //
-// Forward, many tokens (T > 8192): one kernel (k1_premap_tile, k1.hip).
-// Each workgroup runs K1 on its tile (48 tokens up to T = 12288, 64 beyond)
-// with ordinary loads of x, then
+// Forward, from the token count where K1 runs one pass on (no column split;
+// T > 2720 at C >= 128): one kernel (k1_premap_tile, k1.hip).  Each workgroup
+// runs K1 on its tile (16, 32, 48 or 64 tokens, the fewest that keep the
+// launch to one round on the CUs) with ordinary loads of x, then
 // K2 on the tile's tokens (one lane per token) and K3 on the tile, whose
 // re-read of the tile's rows finds them in L2 or the memory-side cache: x
 // comes from HBM about once (T = 65536, C = 1024: 178 us against 209 us for
 // three kernels; with nontemporal K1 loads, which do not leave the rows in
 // the caches, the one kernel is no faster than three).  Keeping the tile in
 // LDS instead does not fit beside K1's pipeline: tiles of 8-16 tokens make
-// every tile re-read all of W (32 x nC) from L2.  Fewer tokens: K1 -> K2 ->
-// K3, the kernels of k1.hip, k2.hip, k3.hip; for few tokens K1 is split over
-// the columns (partial sums in the caller's workspace), and its second stage
-// runs inside the K2 kernel (k1_finish_k2; with K3 too when the layer input
-// is wanted, k1_finish_k2_k3).
+// every tile re-read all of W (32 x nC) from L2.  Fewer tokens, and shapes
+// off the matrix-core path: K1 -> K2 -> K3, the kernels of k1.hip, k2.hip,
+// k3.hip; for few tokens K1 is split over the columns (partial sums in the
+// caller's workspace), and its second stage runs inside the K2 kernel
+// (k1_finish_k2; with K3 too when the layer input is wanted,
+// k1_finish_k2_k3).
 
 #include <hip/hip_runtime.h>
 
@@ -35,8 +37,8 @@
 #include "k1_premap.h"
 #include "k2_chain.h"
 
-// 1: the forward of many tokens runs as one kernel, K1 with K2 and K3 on
-// each tile (k1_premap_tile); 0 (an evidence build): K1, K2 and K3
+// 1: the forward without K1's column split runs as one kernel, K1 with K2
+// and K3 on each tile (k1_premap_tile); 0 (an evidence build): K1, K2 and K3
 // as three kernels, each reading x from HBM.
 #ifndef FMHC_PREMAP_TILE
 #define FMHC_PREMAP_TILE 1

@@ -60,8 +60,8 @@ SOURCE_FLAGS = {"k1.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 # K1 forward and backward-dx contractions as fp32 FMAs on the VALU instead of
 # the matrix cores (same tiles, loads and pipeline), to time the two.
 # premap_three_kernels: the pre-map forward of many tokens as K1, K2, K3 in
-# three kernels, against the product's one kernel (K1 on a 64-token tile, then
-# K2 and K3 on it by the same workgroup).  premap_tile_nt: the one kernel
+# three kernels, against the product's one kernel (K1 on a tile of 16 to 64
+# tokens, then K2 and K3 on it by the same workgroup).  premap_tile_nt: the one kernel
 # with nontemporal loads of x in its K1 part, so that its K3 part re-reads the
 # tile from HBM instead of the memory-side cache.
 VARIANTS = {"k1_valu": ["-DFMHC_K1_VALU=1"], "premap_three_kernels": ["-DFMHC_PREMAP_TILE=0"],

@@ -96,10 +96,10 @@ def test_k1_fwd_split_columns(T, C):
     """Few tokens: fmhc_k1_fwd_ws splits the nC axis over workgroups and adds
     the fp32 partials in a fixed order.  Both it and the one-pass fmhc_k1_fwd
     meet the oracle's bound; the split result is deterministic; where no split
-    is planned (workspace size 0, always from T = 8192 on) the two entry
+    is planned (workspace size 0, always from T = 2721 on) the two entry
     points run the same kernel: 16-token workgroups up to T = 4096 (T = 4095:
-    a ragged last one), 32-token tiles up to 8192, 64-token tiles from 8193
-    (T = 8193, 16417: ragged)."""
+    a ragged last one), 32-token tiles up to 8192, 48 up to 12288 (T = 8193:
+    ragged), 64 beyond (T = 16417: ragged)."""
     from flash_mhc import _abi
 
     nC = 4 * C
@@ -108,7 +108,7 @@ def test_k1_fwd_split_columns(T, C):
     lib = _abi.load()
     nbytes = int(lib.fmhc_k1_fwd_workspace_bytes(T, nC))
     assert nbytes > 0 if T <= 256 else True  # few tokens always split
-    assert nbytes == 0 if T >= 8192 else True
+    assert nbytes == 0 if T > 2720 else True
     a = K.k1_fwd(xd, Wd)
     b = K.k1_fwd(xd, Wd)
     one = (torch.empty(T, 32, dtype=torch.bfloat16, device=DEV), torch.empty(T, device=DEV))

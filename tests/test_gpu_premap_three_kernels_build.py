@@ -1,5 +1,6 @@
-"""The product's pre-map forward of many tokens is one kernel (K1 on a
-64-token tile, then K2 and K3 on it by the same workgroup).  The evidence
+"""The product's pre-map forward is one kernel wherever K1 is not split over
+the columns (K1 on a tile of 16 to 64 tokens, then K2 and K3 on it by the
+same workgroup).  The evidence
 builds of build.py time it against K1, K2, K3 as three kernels
 ("premap_three_kernels") and against the one kernel with nontemporal loads of
 x ("premap_tile_nt").  Loaded beside the product library through the same C
@@ -50,7 +51,8 @@ def _run(lib, x, W, params, T, C, with_li):
     return out
 
 
-@pytest.mark.parametrize("T,C,with_li", [(16384, 1024, True), (16417, 1024, True), (20000, 256, True),
+@pytest.mark.parametrize("T,C,with_li", [(3000, 1024, True), (5000, 512, True), (7000, 1024, False),
+                                         (16384, 1024, True), (16417, 1024, True), (20000, 256, True),
                                          (16400, 4096, False), (65536, 1024, True)])
 def test_tile_kernel_equals_three_kernels(three_lib, T, C, with_li):
     g = torch.Generator().manual_seed(T + C)
