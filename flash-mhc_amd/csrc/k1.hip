@@ -98,9 +98,9 @@ struct FwdFrag {
 // token) to part[t][33][S4] (S4 = gridDim.y rounded up to 4) instead of the
 // outputs; k1_fwd_finish adds the gridDim.y partials in order.
 // TILE (the pre-map region without the column split, premap.hip): after a
-// tile's projections, the same workgroup runs K2 on the tile's tokens (one
-// lane per token, the K2 kernel's per-token chain) and then K3 (each wave its
-// own blocks; with fewer blocks than waves, all waves over the tile), mixing the tile's
+// tile's projections, the same workgroup runs K2 on the tile's tokens (four
+// lanes per token, k2_token4) and then K3 (each wave its own blocks; with
+// fewer blocks than waves, all waves over the tile), mixing the tile's
 // streams into the layer input while L2 and the memory-side cache may still
 // hold the rows it just read (its x loads are ordinary loads, which allocate
 // there).  Same values as K1 -> K2 -> K3 launched separately.
@@ -400,32 +400,25 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
   }
   if constexpr (TILE) {
     // Wave w owns blocks w, w + SPLIT, ... (the blocks whose projections it
-    // stored above) and runs K2 for their tokens on lanes 0-15.  With at least
-    // a block per wave it also runs K3 over its blocks: same-wave LDS
-    // operations are ordered, so those projections and the h_pre written below
-    // need no barrier.  With fewer blocks than waves, every wave takes a share
-    // of the tile's tokens in K3, after a barrier.
+    // stored above) and runs K2 for their tokens, four lanes per token
+    // (k2_token4; one lane per token measured 4-6 us slower per launch).
+    // With at least a block per wave it also runs K3 over its blocks:
+    // same-wave LDS operations are ordered, so those projections and the h_pre
+    // written below need no barrier.  With fewer blocks than waves, every wave
+    // takes a share of the tile's tokens in K3, after a barrier.
     for (int r = wave; r < R; r += SPLIT) {
-    if (lane < 16) {
-#pragma clang fp contract(off)
-      const int64_t t = t0 + 16 * r + lane;
-      float p[kDk];
-#pragma unroll
-      for (int k = 0; k < kDk; ++k) p[k] = tile_sm.proj[16 * r + lane][k];
-      float ap, apo, ar, b[kDk];
-      load_params(tile_sm.k2, ap, apo, ar, b);
-      K2Fwd f;
-      k2_chain(p, ap, apo, ar, b, f);
-      f32x4 Hm[kN];
-      k2_h_merged(f, tile_sm.k2.perm, Hm);
-      const f32x4 hp = {f.hp[0], f.hp[1], f.hp[2], f.hp[3]};
+    {
+      const int i = lane >> 2, qd = lane & 3;
+      const int64_t t = t0 + 16 * r + i;
+      float hp, hq, hp_all[kN];
+      f32x4 hrow;
+      k2_token4(tile_sm.proj[16 * r + i], tile_sm.k2, qd, hp, hq, hrow, hp_all);
       if (t < T) {
-        reinterpret_cast<f32x4*>(pt.h_pre)[t] = hp;
-        reinterpret_cast<f32x4*>(pt.h_post)[t] = f32x4{f.hq[0], f.hq[1], f.hq[2], f.hq[3]};
-#pragma unroll
-        for (int i = 0; i < kN; ++i) reinterpret_cast<f32x4*>(pt.H)[t * kN + i] = Hm[i];
+        pt.h_pre[t * kN + qd] = hp;
+        pt.h_post[t * kN + qd] = hq;
+        reinterpret_cast<f32x4*>(pt.H)[t * kN + qd] = hrow;
       }
-      tile_sm.hpre[16 * r + lane] = hp;
+      if (qd == 0) tile_sm.hpre[16 * r + i] = f32x4{hp_all[0], hp_all[1], hp_all[2], hp_all[3]};
     }
     if (R >= SPLIT && pt.layer_input) {
       for (int tt = 0; tt < 16; ++tt) {

@@ -178,6 +178,67 @@ __device__ __forceinline__ void k2_h_merged(const K2Fwd& f, const f32x4 sperm[kN
     for (int j = 0; j < kN; ++j) H[i][j] = rb(rb(acc[i * kN + j]) - rb(f.hq[i] * f.hp[j]));
 }
 
+// Lane K of the calling lane's quad (DPP quad_perm [K, K, K, K]).
+template <int K>
+__device__ __forceinline__ float quad_lane(float v) {
+  return __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), K * 0x55, 0xf, 0xf, false));
+}
+
+// K2 forward of one token on the four lanes of a quad (qd = lane & 3; p: the
+// token's 32 projections as bf16 values).  Lane qd computes logit qd (h_pre),
+// 4 + qd (h_post) and the softmax terms m = qd, qd + 4, ..., 20 + qd, gathers
+// the quad's exponentials and weights to add them in k2_chain's order (m = 0,
+// 1, ..., 23), and computes H_merged row qd in k2_h_merged's order: the values
+// of k2_chain + k2_h_merged, bit for bit, at a quarter of the arithmetic per
+// lane.  hp_all receives h_pre[0..3].  Every lane of the quad must be active.
+__device__ __forceinline__ void k2_token4(const float* p, const K2Smem& sm, int qd, float& hp, float& hq,
+                                          f32x4& hrow, float hp_all[kN]) {
+#pragma clang fp contract(off)
+  hp = rb(sigmoid_f32(rb(rb(sm.sc[0] * p[qd]) + sm.sc[3 + qd])));
+  hq = rb(2.f * rb(sigmoid_f32(rb(rb(sm.sc[1] * p[kN + qd]) + sm.sc[3 + kN + qd]))));
+  constexpr int kS = kNF / 4;  // softmax terms per lane
+  float z[kS];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int s = 0; s < kS; ++s) {
+    const int m = 4 * s + qd;
+    z[s] = rb(rb(sm.sc[2] * p[2 * kN + m]) + sm.sc[3 + 2 * kN + m]);
+    mx = fmaxf(mx, z[s]);
+  }
+  // The quad's maximum (quad_perm [1, 0, 3, 2], then [2, 3, 0, 1]); a maximum
+  // is exact in any order.
+  mx = fmaxf(mx, __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(mx), 0xb1, 0xf, 0xf, false)));
+  mx = fmaxf(mx, __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(mx), 0x4e, 0xf, 0xf, false)));
+  float sum = 0.f;
+#pragma unroll
+  for (int s = 0; s < kS; ++s) {
+    z[s] = expf(z[s] - mx);
+    const float e0 = quad_lane<0>(z[s]), e1 = quad_lane<1>(z[s]), e2 = quad_lane<2>(z[s]), e3 = quad_lane<3>(z[s]);
+    sum = sum + e0;
+    sum = sum + e1;
+    sum = sum + e2;
+    sum = sum + e3;
+  }
+  float acc[kN] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < kS; ++s) {
+    const float a = rb(z[s] / sum);
+    const float am[4] = {quad_lane<0>(a), quad_lane<1>(a), quad_lane<2>(a), quad_lane<3>(a)};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const f32x4 pm = sm.perm[(4 * s + k) * 4 + qd];
+#pragma unroll
+      for (int j = 0; j < kN; ++j) acc[j] = acc[j] + am[k] * pm[j];
+    }
+  }
+  hp_all[0] = quad_lane<0>(hp);
+  hp_all[1] = quad_lane<1>(hp);
+  hp_all[2] = quad_lane<2>(hp);
+  hp_all[3] = quad_lane<3>(hp);
+#pragma unroll
+  for (int j = 0; j < kN; ++j) hrow[j] = rb(rb(acc[j]) - rb(hq * hp_all[j]));
+}
+
 // K2 forward of token t with 32 lanes (lane q of a 32-lane group, p = the
 // token's projection q as a bf16 value): lane q computes logit q (q < 4:
 // h_pre, q < 8: h_post, else a softmax term), then lanes 0-15 one H_merged

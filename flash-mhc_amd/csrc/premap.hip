@@ -15,7 +15,7 @@
 // T > 2720 at C >= 128): one kernel (k1_premap_tile, k1.hip).  Each workgroup
 // runs K1 on its tile (16, 32, 48 or 64 tokens, the fewest that keep the
 // launch to one round on the CUs) with ordinary loads of x, then
-// K2 on the tile's tokens (one lane per token) and K3 on the tile, whose
+// K2 on the tile's tokens (four lanes per token) and K3 on the tile, whose
 // re-read of the tile's rows finds them in L2 or the memory-side cache: x
 // comes from HBM about once (T = 65536, C = 1024: 178 us against 209 us for
 // three kernels; with nontemporal K1 loads, which do not leave the rows in
