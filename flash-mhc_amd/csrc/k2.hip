@@ -1,5 +1,5 @@
 // K2: the mHC-lite coefficient math of the fused path (block.py:161-170 of
-// alint77/flash-mHC), forward and backward, one thread per token.
+// alint77/flash-mHC), forward and backward, one to 32 lanes per token.
 //
 // The reference evaluates K2 as a chain of PyTorch ops on bf16 tensors: every
 // op computes in fp32 from bf16 inputs and rounds its output to bf16 (RNE), and
@@ -29,45 +29,59 @@ namespace fmhc {
 namespace {
 
 constexpr int kK2Threads = 256;
-// 32 lanes per token (k2_fwd_small, k2_bwd_small) up to this many tokens, one
-// thread per token above.  The one-thread kernels take T / 256 workgroups,
-// too few to hide their chain's latency until about 12000 tokens: at
-// T = 4097 / 8192 / 12000 / 16384 the backward takes 13.2 / 13.4 / 13.2 /
-// 13.3 us against 6.9 / 9.7 / 12.7 / 15.3 us with 32 lanes, the forward
-// 7.7 / 7.9 / 8.0 / 8.1 against 4.7 / 6.3 / 7.6 / 9.0 us.
+// 32 lanes per token (k2_fwd_small, k2_bwd_small) up to this many tokens,
+// four lanes per token (k2_fwd_quad, k2_bwd_quad) above.  Kernels with one
+// thread per token took T / 256 workgroups, too few to hide their chain's
+// latency: at T = 4097 / 8192 / 12000 / 16384 the one-thread backward took
+// 13.2 / 13.4 / 13.2 / 13.3 us against 6.9 / 9.7 / 12.7 / 15.3 us with 32
+// lanes, the forward 7.7 / 7.9 / 8.0 / 8.1 against 4.7 / 6.3 / 7.6 / 9.0 us.
+// With four lanes, T = 12000 / 16384 / 65536 / 262144: forward 4.7 / 4.8 /
+// 8.8 / 24.5 us (one thread: 8.2 / 8.2 / 9.8 / 20.2), backward 8.8 / 8.8 /
+// 15.4 / 41.1 us (13.8 / 13.6 / 14.7 / 38.8); from T = 65536 on both forms
+// are bound by their arithmetic.
 constexpr int64_t kK2SmallT = 8192;
+constexpr int kK2QuadTok = kK2Threads / 4;  // tokens per workgroup of the four-lane kernels
 
+// Forward with four lanes per token (k2_token4: lane qd writes h_pre[qd],
+// h_post[qd] and H_merged row qd), kK2QuadTok tokens per workgroup; the
+// values of k2_chain + k2_h_merged, bit for bit.
 template <bool VEC>
-__global__ __launch_bounds__(kK2Threads) void k2_fwd_kernel(
-    const uint16_t* __restrict__ proj, const K2Params P, float* __restrict__ h_pre,
-    float* __restrict__ h_post, float* __restrict__ H, int64_t T, const ZeroWords z) {
-#pragma clang fp contract(off)
+__global__ __launch_bounds__(kK2Threads) void k2_fwd_quad(const uint16_t* __restrict__ proj, const K2Params P,
+                                                         float* __restrict__ h_pre, float* __restrict__ h_post,
+                                                         float* __restrict__ H, int64_t T, const ZeroWords z) {
   __shared__ K2Smem sm;
+  __shared__ float prow[kK2QuadTok][kDk];
   zero_words(z);
-  stage_params<kK2Threads>(P, sm);
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * kK2Threads + threadIdx.x;
-  if (t >= T) return;
-  float p[kDk];
-  load_proj<VEC>(proj + t * kDk, p);
-  float ap, apo, ar, b[kDk];
-  load_params(sm, ap, apo, ar, b);
-  K2Fwd f;
-  k2_chain(p, ap, apo, ar, b, f);
-  f32x4 hp = {f.hp[0], f.hp[1], f.hp[2], f.hp[3]};
-  f32x4 hq = {f.hq[0], f.hq[1], f.hq[2], f.hq[3]};
-  reinterpret_cast<f32x4*>(h_pre)[t] = hp;
-  reinterpret_cast<f32x4*>(h_post)[t] = hq;
-  f32x4 Hm[kN];
-  k2_h_merged(f, sm.perm, Hm);
+  const int qd = threadIdx.x & 3;
+  const int slot = static_cast<int>(threadIdx.x) >> 2;
+  const int64_t tq = static_cast<int64_t>(blockIdx.x) * kK2QuadTok + slot;
+  const bool valid = tq < T;
+  const int64_t t = valid ? tq : T - 1;  // idle slots recompute the last token, store nothing
+  float p[8];
+  if constexpr (VEC) {
+    unpack8(*reinterpret_cast<const u32x4*>(proj + t * kDk + 8 * qd), p);
+  } else {
 #pragma unroll
-  for (int i = 0; i < kN; ++i) reinterpret_cast<f32x4*>(H)[t * kN + i] = Hm[i];
+    for (int u = 0; u < 8; ++u) p[u] = bf16_to_f32(proj[t * kDk + 8 * qd + u]);
+  }
+#pragma unroll
+  for (int u = 0; u < 8; ++u) prow[slot][8 * qd + u] = p[u];
+  stage_params<kK2Threads>(P, sm);  // ends with the barrier that also covers prow
+  float hp, hq, hp_all[kN];
+  f32x4 hrow;
+  k2_token4(prow[slot], sm, qd, hp, hq, hrow, hp_all);
+  if (valid) {
+    h_pre[t * kN + qd] = hp;
+    h_post[t * kN + qd] = hq;
+    reinterpret_cast<f32x4*>(H)[t * kN + qd] = hrow;
+  }
 }
 
 // Few tokens: 32 lanes per token.  Lane q computes logit q (q < 4: h_pre,
 // q < 8: h_post, else a softmax term), then lanes 0-15 one H_merged entry
 // each.  Every sum keeps k2_chain's / k2_h_merged's order (the softmax
 // denominator and each H_res entry are added sequentially over m), so the
-// results are bit-identical to k2_fwd_kernel's.
+// results are bit-identical to k2_chain + k2_h_merged.
 __global__ __launch_bounds__(kK2Threads) void k2_fwd_small(const uint16_t* __restrict__ proj, const K2Params P,
                                                           float* __restrict__ h_pre, float* __restrict__ h_post,
                                                           float* __restrict__ H, int64_t T, const ZeroWords z) {
@@ -83,121 +97,21 @@ __global__ __launch_bounds__(kK2Threads) void k2_fwd_small(const uint16_t* __res
 
 // Backward of one token (autograd's rounding points on the GPU; gradients of
 // the fp32 outputs are first rounded to bf16, as the .float() casts' backward
-// does).
-// Writes grad_proj and accumulates this token's terms of the 35 parameter
-// gradients into par[]: sum_j rb(gz_pre p_pre), sum_j rb(gz_post p_post),
-// sum_m rb(gz_res p_res), and the 32 logit gradients (the bias terms).
-template <bool VEC>
-__global__ __launch_bounds__(kK2Threads) void k2_bwd_kernel(
-    const uint16_t* __restrict__ proj, const K2Params P,
-    const float* __restrict__ g_hpre, const float* __restrict__ g_hpost,
-    const float* __restrict__ g_H, uint16_t* __restrict__ grad_proj,
-    float* __restrict__ partial, int64_t T) {
-#pragma clang fp contract(off)
-  __shared__ K2Smem sm;
-  stage_params<kK2Threads>(P, sm);
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * kK2Threads + threadIdx.x;
-  float par[kNPar];
-#pragma unroll
-  for (int k = 0; k < kNPar; ++k) par[k] = 0.f;
-
-  if (t < T) {
-    float p[kDk];
-    load_proj<VEC>(proj + t * kDk, p);
-    float ap, apo, ar, b[kDk];
-    load_params(sm, ap, apo, ar, b);
-    K2Fwd f;
-    k2_chain(p, ap, apo, ar, b, f);
-
-    float gH[kN * kN], ghp[kN], ghq[kN];
-#pragma unroll
-    for (int ij = 0; ij < kN * kN; ++ij) gH[ij] = g_H ? rb(g_H[t * kN * kN + ij]) : 0.f;
-    // H_merged = H_res - outer(h_post, h_pre): the outer product's gradient
-    // is -gH; its two factors get the sums over the other index.
-#pragma unroll
-    for (int i = 0; i < kN; ++i) {
-      float s = 0.f;
-#pragma unroll
-      for (int j = 0; j < kN; ++j) s = s + rb(-gH[i * kN + j] * f.hp[j]);
-      ghq[i] = rb((g_hpost ? rb(g_hpost[t * kN + i]) : 0.f) + rb(s));
-    }
-#pragma unroll
-    for (int j = 0; j < kN; ++j) {
-      float s = 0.f;
-#pragma unroll
-      for (int i = 0; i < kN; ++i) s = s + rb(-gH[i * kN + j] * f.hq[i]);
-      ghp[j] = rb((g_hpre ? rb(g_hpre[t * kN + j]) : 0.f) + rb(s));
-    }
-    // H_res = a @ perm, then the softmax backward as PyTorch's GPU kernel
-    // rounds it for bf16: gy = rb(g a), gz = rb(gy - a sum(gy)).
-    float gy[kNF];
-    float s = 0.f;
-#pragma unroll
-    for (int m = 0; m < kNF; ++m) {
-      float acc = 0.f;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const f32x4 pm = sm.perm[m * 4 + q];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) acc = acc + gH[4 * q + e] * pm[e];
-      }
-      gy[m] = rb(rb(acc) * f.a[m]);
-      s = s + gy[m];
-    }
-    float gz[kDk];
-#pragma unroll
-    for (int m = 0; m < kNF; ++m) gz[2 * kN + m] = rb(gy[m] - f.a[m] * s);
-    // Sigmoid backward, grad (1 - y) y with every step rounded to bf16 as
-    // PyTorch's GPU kernel does for bf16; h_post = 2 sigmoid gives the factor 2 first.
-#pragma unroll
-    for (int j = 0; j < kN; ++j) {
-      gz[j] = rb(rb(ghp[j] * rb(1.f - f.hp[j])) * f.hp[j]);
-      const float gs = rb(ghq[j] * 2.f);
-      gz[kN + j] = rb(rb(gs * rb(1.f - f.sq[j])) * f.sq[j]);
-    }
-    float gp[kDk];
-#pragma unroll
-    for (int k = 0; k < kDk; ++k) {
-      const float a = k < kN ? ap : (k < 2 * kN ? apo : ar);
-      gp[k] = rb(gz[k] * a);
-      par[k < kN ? 0 : (k < 2 * kN ? 1 : 2)] += rb(gz[k] * p[k]);
-      par[3 + k] = gz[k];
-    }
-    uint16_t* row = grad_proj + t * kDk;
-    if constexpr (VEC) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) reinterpret_cast<u32x4*>(row)[i] = pack8(gp + 8 * i);
-    } else {
-#pragma unroll
-      for (int k = 0; k < kDk; ++k) row[k] = f32_to_bf16(gp[k]);
-    }
-  }
-
-  // Block partial sums: in-wave butterfly (every lane is here), then the
-  // four waves in order.
-  __shared__ float red[kK2Threads / kWave][kNPar];
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
-#pragma unroll
-  for (int k = 0; k < kNPar; ++k) {
-    const float v = wave_sum(par[k]);
-    if (lane == 0) red[wave][k] = v;
-  }
-  __syncthreads();
-  if (threadIdx.x < kNPar) {
-    float v = 0.f;
-#pragma unroll
-    for (int w = 0; w < kK2Threads / kWave; ++w) v += red[w][threadIdx.x];
-    partial[static_cast<int64_t>(blockIdx.x) * kNPar + threadIdx.x] = v;
-  }
-}
-
-// Backward for few tokens, 32 lanes per token (lane q: logit q) and 8 tokens
-// per workgroup.  Every per-token value is k2_bwd_kernel's: the forward is
-// k2_token32's (bit-identical to the chain), and each sum over a token's
-// terms runs through shuffles in the chain's order.  The workgroup's
-// parameter partials add its 8 tokens in order (a different order over tokens
-// than k2_bwd_kernel's, still fixed).
+// does), in the chain's order:
+//   gH = rb(grad_H), ghq[i] = rb(rb(grad_h_post[i]) + rb(sum_j rb(-gH[i, j] h_pre[j]))),
+//   ghp[j] = rb(rb(grad_h_pre[j]) + rb(sum_i rb(-gH[i, j] h_post[i]))),
+//   gy[m] = rb(rb(sum_ij gH[ij] perm[m, ij]) a[m]), gz_res[m] = rb(gy[m] - a[m] sum_m gy[m])
+//   (PyTorch's bf16 softmax backward), gz_pre[j] = rb(rb(ghp[j] rb(1 - h_pre[j])) h_pre[j]),
+//   gz_post[j] = rb(rb(rb(2 ghq[j]) rb(1 - s[j])) s[j]) (s: the post sigmoid),
+//   grad_proj[k] = rb(gz[k] alpha_k);
+// each sum in index order.  The 35 parameter terms of a token are
+// sum_j rb(gz_pre p_pre), sum_j rb(gz_post p_post), sum_m rb(gz_res p_res)
+// and the 32 logit gradients gz (the bias terms); a workgroup writes their
+// sums over its tokens, in token order, to its partial.
+//
+// Few tokens: 32 lanes per token (lane q: logit q) and 8 tokens per
+// workgroup.  The forward is k2_token32's (bit-identical to the chain), and
+// each sum over a token's terms runs through shuffles in the chain's order.
 constexpr int kK2BwdTok = kK2Threads / 32;
 
 __global__ __launch_bounds__(kK2Threads) void k2_bwd_small(
@@ -293,6 +207,171 @@ __global__ __launch_bounds__(kK2Threads) void k2_bwd_small(
   }
 }
 
+// Backward with four lanes per token: lane qd of a quad owns projections
+// 8 qd .. 8 qd + 7, so lane 0 holds the eight sigmoid logits (h_pre, then
+// h_post's) and lanes 1-3 eight softmax terms each (m = 8 (qd - 1) + u).
+// Every lane evaluates one exponential and one division per value (lane 0:
+// 1 / (1 + exp(-z)), the others exp(z - max) / sum), and the sums over a
+// token's terms gather the quad's values with DPP moves and add them in the
+// chain's order, so every per-token value is k2_bwd_small's bit for bit.
+// grad_proj leaves as one 16-byte row piece per lane.  The workgroup's
+// parameter partials add its tokens in order.
+template <int THREADS, bool VEC>
+__global__ __launch_bounds__(THREADS) void k2_bwd_quad(
+    const uint16_t* __restrict__ proj, const K2Params P, const float* __restrict__ g_hpre,
+    const float* __restrict__ g_hpost, const float* __restrict__ g_H, uint16_t* __restrict__ grad_proj,
+    float* __restrict__ partial, int64_t T) {
+#pragma clang fp contract(off)
+  constexpr int kTok = THREADS / 4;
+  __shared__ K2Smem sm;
+  __shared__ float red[kTok][kNPar];
+  stage_params<THREADS>(P, sm);
+  const int qd = threadIdx.x & 3;
+  const int slot = static_cast<int>(threadIdx.x) >> 2;
+  const int64_t tq = static_cast<int64_t>(blockIdx.x) * kTok + slot;
+  const bool valid = tq < T;
+  const int64_t t = valid ? tq : T - 1;  // idle slots recompute the last token, store nothing
+
+  float p[8];
+  if constexpr (VEC) {
+    unpack8(*reinterpret_cast<const u32x4*>(proj + t * kDk + 8 * qd), p);
+  } else {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) p[u] = bf16_to_f32(proj[t * kDk + 8 * qd + u]);
+  }
+  // Forward.  Lane 0: y[u] = h_pre[u] (u < 4), the sigmoid of post logit u - 4
+  // (u >= 4); lanes 1-3: y[u] = the softmax weight of their term u.
+  float alpha[8], z[8];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    alpha[u] = qd == 0 ? (u < kN ? sm.sc[0] : sm.sc[1]) : sm.sc[2];
+    z[u] = rb(rb(alpha[u] * p[u]) + sm.sc[3 + 8 * qd + u]);
+    if (qd != 0) mx = fmaxf(mx, z[u]);
+  }
+  // The quad's maximum (quad_perm [1, 0, 3, 2], then [2, 3, 0, 1]); exact in any order.
+  mx = fmaxf(mx, __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(mx), 0xb1, 0xf, 0xf, false)));
+  mx = fmaxf(mx, __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(mx), 0x4e, 0xf, 0xf, false)));
+  float ex[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) ex[u] = expf(qd == 0 ? -z[u] : z[u] - mx);
+  float sum = 0.f;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) sum = sum + quad_lane<1>(ex[u]);
+#pragma unroll
+  for (int u = 0; u < 8; ++u) sum = sum + quad_lane<2>(ex[u]);
+#pragma unroll
+  for (int u = 0; u < 8; ++u) sum = sum + quad_lane<3>(ex[u]);
+  float y[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) y[u] = qd == 0 ? rb(1.f / (1.f + ex[u])) : rb(ex[u] / sum);
+  float hp[kN], sq[kN], hq[kN];
+  hp[0] = quad_lane<0>(y[0]);
+  hp[1] = quad_lane<0>(y[1]);
+  hp[2] = quad_lane<0>(y[2]);
+  hp[3] = quad_lane<0>(y[3]);
+  sq[0] = quad_lane<0>(y[4]);
+  sq[1] = quad_lane<0>(y[5]);
+  sq[2] = quad_lane<0>(y[6]);
+  sq[3] = quad_lane<0>(y[7]);
+#pragma unroll
+  for (int i = 0; i < kN; ++i) hq[i] = rb(2.f * sq[i]);
+
+  // Incoming gradients, rounded to bf16 (the .float() casts' backward).
+  float gH[kN * kN];
+#pragma unroll
+  for (int ij = 0; ij < kN * kN; ++ij) gH[ij] = g_H ? rb(g_H[t * kN * kN + ij]) : 0.f;
+  float gz[8];
+  if (qd == 0) {
+    // H_merged = H_res - outer(h_post, h_pre), then the sigmoid backward.
+#pragma unroll
+    for (int i = 0; i < kN; ++i) {
+      float s = 0.f;
+#pragma unroll
+      for (int j = 0; j < kN; ++j) s = s + rb(-gH[i * kN + j] * hp[j]);
+      const float ghq = rb((g_hpost ? rb(g_hpost[t * kN + i]) : 0.f) + rb(s));
+      const float gs = rb(ghq * 2.f);
+      gz[kN + i] = rb(rb(gs * rb(1.f - sq[i])) * sq[i]);
+    }
+#pragma unroll
+    for (int j = 0; j < kN; ++j) {
+      float s = 0.f;
+#pragma unroll
+      for (int i = 0; i < kN; ++i) s = s + rb(-gH[i * kN + j] * hq[i]);
+      const float ghp = rb((g_hpre ? rb(g_hpre[t * kN + j]) : 0.f) + rb(s));
+      gz[j] = rb(rb(ghp * rb(1.f - hp[j])) * hp[j]);
+    }
+  } else {
+    // H_res = a @ perm: gy = rb(rb(gH . perm_m) a).
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int m = 8 * (qd - 1) + u;
+      float acc = 0.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 pm = sm.perm[m * 4 + q];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc = acc + gH[4 * q + e] * pm[e];
+      }
+      gz[u] = rb(rb(acc) * y[u]);  // gy for now
+    }
+  }
+  // Softmax backward: gz = rb(gy - a sum(gy)), the sum over m in order.
+  float sgy = 0.f;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) sgy = sgy + quad_lane<1>(gz[u]);
+#pragma unroll
+  for (int u = 0; u < 8; ++u) sgy = sgy + quad_lane<2>(gz[u]);
+#pragma unroll
+  for (int u = 0; u < 8; ++u) sgy = sgy + quad_lane<3>(gz[u]);
+  if (qd != 0) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) gz[u] = rb(gz[u] - y[u] * sgy);
+  }
+  float gp[8], pc[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    gp[u] = rb(gz[u] * alpha[u]);
+    pc[u] = rb(gz[u] * p[u]);
+  }
+  if (valid) {
+    uint16_t* row = grad_proj + t * kDk + 8 * qd;
+    if constexpr (VEC) {
+      *reinterpret_cast<u32x4*>(row) = pack8(gp);
+    } else {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) row[u] = f32_to_bf16(gp[u]);
+    }
+  }
+  // This token's parameter terms: the alphas' sums over their logits in
+  // order, the bias gradients gz.
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f;
+#pragma unroll
+  for (int u = 0; u < kN; ++u) s0 += pc[u];
+#pragma unroll
+  for (int u = kN; u < 8; ++u) s1 += pc[u];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) s2 += quad_lane<1>(pc[u]);
+#pragma unroll
+  for (int u = 0; u < 8; ++u) s2 += quad_lane<2>(pc[u]);
+#pragma unroll
+  for (int u = 0; u < 8; ++u) s2 += quad_lane<3>(pc[u]);
+#pragma unroll
+  for (int u = 0; u < 8; ++u) red[slot][3 + 8 * qd + u] = valid ? gz[u] : 0.f;
+  if (qd == 0) {
+    red[slot][0] = valid ? s0 : 0.f;
+    red[slot][1] = valid ? s1 : 0.f;
+    red[slot][2] = valid ? s2 : 0.f;
+  }
+  __syncthreads();
+  if (threadIdx.x < kNPar) {
+    float v = 0.f;
+#pragma unroll 8
+    for (int w = 0; w < kTok; ++w) v += red[w][threadIdx.x];
+    partial[static_cast<int64_t>(blockIdx.x) * kNPar + threadIdx.x] = v;
+  }
+}
+
 // One wave per parameter gradient (k2_param_sum).
 __global__ __launch_bounds__(kWave) void k2_param_reduce(const K2ParamSums r) {
   k2_param_sum(r, static_cast<int>(blockIdx.x), static_cast<int>(threadIdx.x));
@@ -300,10 +379,11 @@ __global__ __launch_bounds__(kWave) void k2_param_reduce(const K2ParamSums r) {
 
 bool k2_bad(int64_t T, int64_t n) { return T < 0 || n != kN; }
 
-int64_t k2_blocks(int64_t T) { return (T + kK2Threads - 1) / kK2Threads; }
 // Workgroups (and parameter partials) of the backward: k2_bwd_small up to
-// kK2SmallT tokens, k2_bwd_kernel above.
-int64_t k2_bwd_blocks(int64_t T) { return T <= kK2SmallT ? (T + kK2BwdTok - 1) / kK2BwdTok : k2_blocks(T); }
+// kK2SmallT tokens, k2_bwd_quad (kK2Threads / 4 tokens each) above.
+int64_t k2_bwd_blocks(int64_t T) {
+  return T <= kK2SmallT ? (T + kK2BwdTok - 1) / kK2BwdTok : (T + kK2QuadTok - 1) / kK2QuadTok;
+}
 
 }  // namespace
 
@@ -321,11 +401,11 @@ int k2_fwd_launch(const uint16_t* proj, const K2Params& P, float* h_pre, float* 
                                                                                 H_merged, T, z);
     return launch_status();
   }
-  const dim3 grid(static_cast<unsigned>(k2_blocks(T)));
+  const dim3 grid(static_cast<unsigned>((T + kK2QuadTok - 1) / kK2QuadTok));
   if (aligned16(proj))
-    k2_fwd_kernel<true><<<grid, kK2Threads, 0, s>>>(proj, P, h_pre, h_post, H_merged, T, z);
+    k2_fwd_quad<true><<<grid, kK2Threads, 0, s>>>(proj, P, h_pre, h_post, H_merged, T, z);
   else
-    k2_fwd_kernel<false><<<grid, kK2Threads, 0, s>>>(proj, P, h_pre, h_post, H_merged, T, z);
+    k2_fwd_quad<false><<<grid, kK2Threads, 0, s>>>(proj, P, h_pre, h_post, H_merged, T, z);
   return launch_status();
 }
 
@@ -368,11 +448,11 @@ int k2_bwd_partials(const uint16_t* proj, const K2Params& P, const float* grad_h
       k2_bwd_small<<<grid, kK2Threads, 0, s>>>(proj, P, grad_h_pre, grad_h_post, grad_H_merged, grad_proj,
                                                partial, T);
     else if (aligned16(proj) && aligned16(grad_proj))
-      k2_bwd_kernel<true><<<grid, kK2Threads, 0, s>>>(proj, P, grad_h_pre, grad_h_post, grad_H_merged,
-                                                      grad_proj, partial, T);
+      k2_bwd_quad<kK2Threads, true><<<grid, kK2Threads, 0, s>>>(proj, P, grad_h_pre, grad_h_post, grad_H_merged,
+                                                                grad_proj, partial, T);
     else
-      k2_bwd_kernel<false><<<grid, kK2Threads, 0, s>>>(proj, P, grad_h_pre, grad_h_post, grad_H_merged,
-                                                       grad_proj, partial, T);
+      k2_bwd_quad<kK2Threads, false><<<grid, kK2Threads, 0, s>>>(proj, P, grad_h_pre, grad_h_post,
+                                                                 grad_H_merged, grad_proj, partial, T);
     const int st = launch_status();
     if (st != FMHC_OK) return st;
   }

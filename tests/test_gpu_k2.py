@@ -107,6 +107,26 @@ def test_k2_null_grads_misaligned_and_empty():
     assert g0[0].shape == (0, 32) and all(float(t.abs().sum()) == 0.0 for t in g0[1:])
 
 
+@pytest.mark.parametrize("T", [8193, 9001])
+def test_k2_misaligned_many_tokens_equals_aligned(T):
+    """Above 8192 tokens (four lanes per token, 64 per workgroup; T = 9001
+    leaves a ragged last workgroup) proj at a 2-byte offset takes the
+    element-wise loads and stores and gives the aligned call's bits: outputs,
+    grad_proj and the parameter gradients."""
+    proj, alphas, bias, grads = _case(T, 30)
+    prm = _dev([*alphas, bias, PERM])
+    g = _dev(list(grads))
+    buf = torch.empty(T * 32 + 1, dtype=BF16, device=DEV)
+    pm = buf[1:].view(T, 32)
+    pm.copy_(proj.to(DEV))
+    assert pm.data_ptr() % 16 != 0
+    pa = proj.to(DEV)
+    for u, v in zip(K.k2_fwd(pm, *prm), K.k2_fwd(pa, *prm)):
+        assert torch.equal(u, v)
+    for u, v in zip(K.k2_bwd(pm, *prm, *g), K.k2_bwd(pa, *prm, *g)):
+        assert torch.equal(u, v)
+
+
 def test_k2_deterministic():
     proj, alphas, bias, grads = _case(20000, 30)
     args = _dev([proj, *alphas, bias, PERM, *grads])
@@ -226,7 +246,7 @@ def test_k2_bf16_parameters_equal_fp32():
 
 def test_k2_fwd_small_and_large_kernels_agree():
     """Up to 8192 tokens the forward gives each token 32 lanes (one per logit),
-    beyond that one thread; both keep the same operation order, so the first
+    beyond that four; both keep the same operation order, so the first
     8192 tokens of an 8193-token call equal an 8192-token call bit for bit."""
     proj, alphas, bias, _ = _case(8193, 90)
     prm = _dev([*alphas, bias, PERM])
@@ -237,8 +257,8 @@ def test_k2_fwd_small_and_large_kernels_agree():
 
 
 def test_k2_bwd_small_and_large_kernels_agree():
-    """The backward likewise: 32 lanes per token up to 8192 tokens, one thread
-    beyond, with the same per-token operation order, so grad_proj of the first
+    """The backward likewise: 32 lanes per token up to 8192 tokens, four lanes
+    per token beyond, with the same per-token operation order, so grad_proj of the first
     8192 tokens of an 8193-token call equals an 8192-token call bit for bit (the
     parameter gradients add the tokens in a different, fixed, order)."""
     proj, alphas, bias, grads = _case(8193, 91)
