@@ -29,17 +29,21 @@ namespace fmhc {
 namespace {
 
 constexpr int kK2Threads = 256;
-// 32 lanes per token (k2_fwd_small, k2_bwd_small) up to this many tokens,
-// four lanes per token (k2_fwd_quad, k2_bwd_quad) above.  Kernels with one
-// thread per token took T / 256 workgroups, too few to hide their chain's
-// latency: at T = 4097 / 8192 / 12000 / 16384 the one-thread backward took
-// 13.2 / 13.4 / 13.2 / 13.3 us against 6.9 / 9.7 / 12.7 / 15.3 us with 32
-// lanes, the forward 7.7 / 7.9 / 8.0 / 8.1 against 4.7 / 6.3 / 7.6 / 9.0 us.
-// With four lanes, T = 12000 / 16384 / 65536 / 262144: forward 4.7 / 4.8 /
-// 8.8 / 24.5 us (one thread: 8.2 / 8.2 / 9.8 / 20.2), backward 8.8 / 8.8 /
-// 15.4 / 41.1 us (13.8 / 13.6 / 14.7 / 38.8); from T = 65536 on both forms
-// are bound by their arithmetic.
-constexpr int64_t kK2SmallT = 8192;
+// 32 lanes per token (k2_fwd_small, k2_bwd_small) up to these many tokens,
+// four lanes per token (k2_fwd_quad, k2_bwd_quad) above.  Four lanes carry
+// eight logits each, so a token's chain takes longer (backward about 8 us at
+// any T up to 48000 against 5.6 us with 32 lanes at T <= 2048) but the lanes
+// do 8 times less redundant work per token: alone, T = 2048 / 4096 / 6000 /
+// 8192, forward 4.2 / 4.9 / 5.6 / 6.4 us with 32 lanes against 4.4 / 4.5 /
+// 4.5 / 4.4 us with four, backward 5.6 / 6.9 / 8.5 / 10.3 against 8.1 /
+// 8.1 / 8.2 / 8.0 us.  One thread per token, the earlier form above 8192
+// tokens, took T / 256 workgroups, too few to hide the chain's latency: at
+// T = 12000 / 16384 / 65536 / 262144 the forward took 8.2 / 8.2 / 9.8 /
+// 20.2 us (four lanes: 4.7 / 4.8 / 8.8 / 24.5), the backward 13.8 / 13.6 /
+// 14.7 / 38.8 us (8.8 / 8.8 / 15.4 / 41.1); from T = 65536 on both forms are
+// bound by their arithmetic.
+constexpr int64_t kK2FwdSmallT = 2048;
+constexpr int64_t kK2BwdSmallT = 6144;
 constexpr int kK2QuadTok = kK2Threads / 4;  // tokens per workgroup of the four-lane kernels
 
 // Forward with four lanes per token (k2_token4: lane qd writes h_pre[qd],
@@ -88,11 +92,12 @@ __global__ __launch_bounds__(kK2Threads) void k2_fwd_small(const uint16_t* __res
 #pragma clang fp contract(off)
   __shared__ K2Smem sm;
   zero_words(z);
-  stage_params<kK2Threads>(P, sm);
   const int q = threadIdx.x & 31;
   const int64_t t = static_cast<int64_t>(blockIdx.x) * (kK2Threads / 32) + (threadIdx.x >> 5);
+  const float p = t < T ? bf16_to_f32(proj[t * kDk + q]) : 0.f;  // loaded before the barrier
+  stage_params<kK2Threads>(P, sm);
   if (t >= T) return;  // a whole 32-lane group leaves together
-  k2_token32(sm, bf16_to_f32(proj[t * kDk + q]), q, t, h_pre, h_post, H);
+  k2_token32(sm, p, q, t, h_pre, h_post, H);
 }
 
 // Backward of one token (autograd's rounding points on the GPU; gradients of
@@ -121,16 +126,22 @@ __global__ __launch_bounds__(kK2Threads) void k2_bwd_small(
 #pragma clang fp contract(off)
   __shared__ K2Smem sm;
   __shared__ float red[kK2BwdTok][kNPar];
-  stage_params<kK2Threads>(P, sm);
   const int q = threadIdx.x & 31;
   const int slot = static_cast<int>(threadIdx.x) >> 5;
   const int64_t tq = static_cast<int64_t>(blockIdx.x) * kK2BwdTok + slot;
   const bool valid = tq < T;
   const int64_t t = valid ? tq : T - 1;  // idle slots recompute the last token, store nothing
+  const int i4 = (q - kN) & 3, j4 = q & 3;
+  // The token's operands are loaded before the parameters' barrier, so that
+  // the two loads' latencies overlap.
+  const float p = bf16_to_f32(proj[t * kDk + q]);
+  const float gh_in = (q < kN * kN && g_H) ? g_H[t * kN * kN + q] : 0.f;
+  const float gpost = g_hpost ? g_hpost[t * kN + i4] : 0.f;
+  const float gpre = g_hpre ? g_hpre[t * kN + j4] : 0.f;
+  stage_params<kK2Threads>(P, sm);
 
   // Forward, as k2_token32: y = h_pre (q < 4) or the post sigmoid (q < 8),
   // hq = h_post, a = the softmax weight of permutation q - 8.
-  const float p = bf16_to_f32(proj[t * kDk + q]);
   const float alpha = q < kN ? sm.sc[0] : (q < 2 * kN ? sm.sc[1] : sm.sc[2]);
   const float z = rb(rb(alpha * p) + sm.sc[3 + q]);
   const float y = q < 2 * kN ? rb(sigmoid_f32(z)) : 0.f;
@@ -145,18 +156,17 @@ __global__ __launch_bounds__(kK2Threads) void k2_bwd_small(
   const float a = rb(e / sum);
 
   // Incoming gradients, rounded to bf16 (the .float() casts' backward).
-  const float gh = (q < kN * kN && g_H) ? rb(g_H[t * kN * kN + q]) : 0.f;
+  const float gh = rb(gh_in);
   // grad of h_post[i] (lanes 4 + i) and of h_pre[j] (lanes j) through
   // H_merged = H_res - outer(h_post, h_pre), each sum in the chain's order.
-  const int i4 = (q - kN) & 3, j4 = q & 3;
   float sq = 0.f, sp = 0.f;
 #pragma unroll
   for (int k = 0; k < kN; ++k) {
     sq = sq + rb(-__shfl(gh, i4 * kN + k, 32) * __shfl(y, k, 32));
     sp = sp + rb(-__shfl(gh, k * kN + j4, 32) * __shfl(hq, kN + k, 32));
   }
-  const float ghq = rb((g_hpost ? rb(g_hpost[t * kN + i4]) : 0.f) + rb(sq));
-  const float ghp = rb((g_hpre ? rb(g_hpre[t * kN + j4]) : 0.f) + rb(sp));
+  const float ghq = rb(rb(gpost) + rb(sq));
+  const float ghp = rb(rb(gpre) + rb(sp));
   // Softmax backward (lanes 8 + m): gy = rb(rb(gH . perm_m) a), gz = rb(gy - a sum(gy)).
   const int m8 = q >= 2 * kN ? q - 2 * kN : 0;
   const float* pf = reinterpret_cast<const float*>(sm.perm);
@@ -225,13 +235,14 @@ __global__ __launch_bounds__(THREADS) void k2_bwd_quad(
   constexpr int kTok = THREADS / 4;
   __shared__ K2Smem sm;
   __shared__ float red[kTok][kNPar];
-  stage_params<THREADS>(P, sm);
   const int qd = threadIdx.x & 3;
   const int slot = static_cast<int>(threadIdx.x) >> 2;
   const int64_t tq = static_cast<int64_t>(blockIdx.x) * kTok + slot;
   const bool valid = tq < T;
   const int64_t t = valid ? tq : T - 1;  // idle slots recompute the last token, store nothing
 
+  // The token's operands are loaded before the parameters' barrier, so that
+  // the two loads' latencies overlap.
   float p[8];
   if constexpr (VEC) {
     unpack8(*reinterpret_cast<const u32x4*>(proj + t * kDk + 8 * qd), p);
@@ -239,6 +250,15 @@ __global__ __launch_bounds__(THREADS) void k2_bwd_quad(
 #pragma unroll
     for (int u = 0; u < 8; ++u) p[u] = bf16_to_f32(proj[t * kDk + 8 * qd + u]);
   }
+  float gH[kN * kN], gpost[kN], gpre[kN];
+#pragma unroll
+  for (int ij = 0; ij < kN * kN; ++ij) gH[ij] = g_H ? g_H[t * kN * kN + ij] : 0.f;
+#pragma unroll
+  for (int i = 0; i < kN; ++i) {
+    gpost[i] = g_hpost ? g_hpost[t * kN + i] : 0.f;
+    gpre[i] = g_hpre ? g_hpre[t * kN + i] : 0.f;
+  }
+  stage_params<THREADS>(P, sm);
   // Forward.  Lane 0: y[u] = h_pre[u] (u < 4), the sigmoid of post logit u - 4
   // (u >= 4); lanes 1-3: y[u] = the softmax weight of their term u.
   float alpha[8], z[8];
@@ -278,9 +298,8 @@ __global__ __launch_bounds__(THREADS) void k2_bwd_quad(
   for (int i = 0; i < kN; ++i) hq[i] = rb(2.f * sq[i]);
 
   // Incoming gradients, rounded to bf16 (the .float() casts' backward).
-  float gH[kN * kN];
 #pragma unroll
-  for (int ij = 0; ij < kN * kN; ++ij) gH[ij] = g_H ? rb(g_H[t * kN * kN + ij]) : 0.f;
+  for (int ij = 0; ij < kN * kN; ++ij) gH[ij] = rb(gH[ij]);
   float gz[8];
   if (qd == 0) {
     // H_merged = H_res - outer(h_post, h_pre), then the sigmoid backward.
@@ -289,7 +308,7 @@ __global__ __launch_bounds__(THREADS) void k2_bwd_quad(
       float s = 0.f;
 #pragma unroll
       for (int j = 0; j < kN; ++j) s = s + rb(-gH[i * kN + j] * hp[j]);
-      const float ghq = rb((g_hpost ? rb(g_hpost[t * kN + i]) : 0.f) + rb(s));
+      const float ghq = rb(rb(gpost[i]) + rb(s));
       const float gs = rb(ghq * 2.f);
       gz[kN + i] = rb(rb(gs * rb(1.f - sq[i])) * sq[i]);
     }
@@ -298,7 +317,7 @@ __global__ __launch_bounds__(THREADS) void k2_bwd_quad(
       float s = 0.f;
 #pragma unroll
       for (int i = 0; i < kN; ++i) s = s + rb(-gH[i * kN + j] * hq[i]);
-      const float ghp = rb((g_hpre ? rb(g_hpre[t * kN + j]) : 0.f) + rb(s));
+      const float ghp = rb(rb(gpre[j]) + rb(s));
       gz[j] = rb(rb(ghp * rb(1.f - hp[j])) * hp[j]);
     }
   } else {
@@ -380,9 +399,9 @@ __global__ __launch_bounds__(kWave) void k2_param_reduce(const K2ParamSums r) {
 bool k2_bad(int64_t T, int64_t n) { return T < 0 || n != kN; }
 
 // Workgroups (and parameter partials) of the backward: k2_bwd_small up to
-// kK2SmallT tokens, k2_bwd_quad (kK2Threads / 4 tokens each) above.
+// kK2BwdSmallT tokens, k2_bwd_quad (kK2QuadTok tokens each) above.
 int64_t k2_bwd_blocks(int64_t T) {
-  return T <= kK2SmallT ? (T + kK2BwdTok - 1) / kK2BwdTok : (T + kK2QuadTok - 1) / kK2QuadTok;
+  return T <= kK2BwdSmallT ? (T + kK2BwdTok - 1) / kK2BwdTok : (T + kK2QuadTok - 1) / kK2QuadTok;
 }
 
 }  // namespace
@@ -396,7 +415,7 @@ bool k2_params(const void* ap, const void* apo, const void* ar, const void* bias
 
 int k2_fwd_launch(const uint16_t* proj, const K2Params& P, float* h_pre, float* h_post, float* H_merged, int64_t T,
                   ZeroWords z, hipStream_t s) {
-  if (T <= kK2SmallT) {
+  if (T <= kK2FwdSmallT) {
     k2_fwd_small<<<dim3(static_cast<unsigned>((T + 7) / 8)), kK2Threads, 0, s>>>(proj, P, h_pre, h_post,
                                                                                 H_merged, T, z);
     return launch_status();
@@ -444,7 +463,7 @@ int k2_bwd_partials(const uint16_t* proj, const K2Params& P, const float* grad_h
     if (!proj || !grad_proj) return FMHC_ERR_INVALID_ARGUMENT;
     if (!workspace || workspace_bytes < fmhc_k2_bwd_workspace_bytes(T)) return FMHC_ERR_INVALID_ARGUMENT;
     const dim3 grid(static_cast<unsigned>(nblocks));
-    if (T <= kK2SmallT)
+    if (T <= kK2BwdSmallT)
       k2_bwd_small<<<grid, kK2Threads, 0, s>>>(proj, P, grad_h_pre, grad_h_post, grad_H_merged, grad_proj,
                                                partial, T);
     else if (aligned16(proj) && aligned16(grad_proj))

@@ -109,7 +109,7 @@ def test_k2_null_grads_misaligned_and_empty():
 
 @pytest.mark.parametrize("T", [8193, 9001])
 def test_k2_misaligned_many_tokens_equals_aligned(T):
-    """Above 8192 tokens (four lanes per token, 64 per workgroup; T = 9001
+    """Above 6144 tokens (four lanes per token, 64 per workgroup; T = 9001
     leaves a ragged last workgroup) proj at a 2-byte offset takes the
     element-wise loads and stores and gives the aligned call's bits: outputs,
     grad_proj and the parameter gradients."""
@@ -244,26 +244,29 @@ def test_k2_bf16_parameters_equal_fp32():
         assert v.dtype == BF16 and torch.equal(u, v.float())
 
 
-def test_k2_fwd_small_and_large_kernels_agree():
-    """Up to 8192 tokens the forward gives each token 32 lanes (one per logit),
-    beyond that four; both keep the same operation order, so the first
-    8192 tokens of an 8193-token call equal an 8192-token call bit for bit."""
-    proj, alphas, bias, _ = _case(8193, 90)
+@pytest.mark.parametrize("n", [2048, 8192])
+def test_k2_fwd_small_and_large_kernels_agree(n):
+    """Up to 2048 tokens the forward gives each token 32 lanes (one per logit),
+    beyond that four; both keep the same operation order, so the first n
+    tokens of an (n + 1)-token call equal an n-token call bit for bit (n = 2048:
+    the two kernels; 8192: four lanes both)."""
+    proj, alphas, bias, _ = _case(n + 1, 90)
     prm = _dev([*alphas, bias, PERM])
     big = K.k2_fwd(proj.to(DEV), *prm)
-    small = K.k2_fwd(proj[:8192].to(DEV), *prm)
+    small = K.k2_fwd(proj[:n].to(DEV), *prm)
     for u, v in zip(small, big):
-        assert torch.equal(u, v[:8192])
+        assert torch.equal(u, v[:n])
 
 
-def test_k2_bwd_small_and_large_kernels_agree():
-    """The backward likewise: 32 lanes per token up to 8192 tokens, four lanes
-    per token beyond, with the same per-token operation order, so grad_proj of the first
-    8192 tokens of an 8193-token call equals an 8192-token call bit for bit (the
-    parameter gradients add the tokens in a different, fixed, order)."""
-    proj, alphas, bias, grads = _case(8193, 91)
+@pytest.mark.parametrize("n", [6144, 8192])
+def test_k2_bwd_small_and_large_kernels_agree(n):
+    """The backward likewise: 32 lanes per token up to 6144 tokens, four lanes
+    per token beyond, with the same per-token operation order, so grad_proj of
+    the first n tokens of an (n + 1)-token call equals an n-token call bit for
+    bit (the parameter gradients add the tokens in a different, fixed, order)."""
+    proj, alphas, bias, grads = _case(n + 1, 91)
     prm = _dev([*alphas, bias, PERM])
     g = _dev(list(grads))
     big = K.k2_bwd(proj.to(DEV), *prm, *g)
-    small = K.k2_bwd(proj[:8192].to(DEV), *prm, *[t[:8192] for t in g])
-    assert torch.equal(small[0], big[0][:8192])
+    small = K.k2_bwd(proj[:n].to(DEV), *prm, *[t[:n] for t in g])
+    assert torch.equal(small[0], big[0][:n])
