@@ -64,4 +64,7 @@ int k2_bwd_partials(const uint16_t* proj, const K2Params& P, const float* grad_h
                     hipStream_t s, K2ParamSums* sums);
 void launch_k2_param_reduce(const K2ParamSums& sums, hipStream_t s);
 
+// Lanes per token of K3's backward (fmhc_k3_bwd) on its 16-byte path.
+int k3_bwd_lanes8(int C);
+
 }  // namespace fmhc

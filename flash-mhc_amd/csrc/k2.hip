@@ -42,8 +42,7 @@ constexpr int kK2Threads = 256;
 // 20.2 us (four lanes: 4.7 / 4.8 / 8.8 / 24.5), the backward 13.8 / 13.6 /
 // 14.7 / 38.8 us (8.8 / 8.8 / 15.4 / 41.1); from T = 65536 on both forms are
 // bound by their arithmetic.
-constexpr int64_t kK2FwdSmallT = 2048;
-constexpr int64_t kK2BwdSmallT = 6144;
+constexpr int64_t kK2FwdSmallT = 2048;  // kK2BwdSmallT: k2_chain.h
 constexpr int kK2QuadTok = kK2Threads / 4;  // tokens per workgroup of the four-lane kernels
 
 // Forward with four lanes per token (k2_token4: lane qd writes h_pre[qd],
@@ -117,7 +116,7 @@ __global__ __launch_bounds__(kK2Threads) void k2_fwd_small(const uint16_t* __res
 // Few tokens: 32 lanes per token (lane q: logit q) and 8 tokens per
 // workgroup.  The forward is k2_token32's (bit-identical to the chain), and
 // each sum over a token's terms runs through shuffles in the chain's order.
-constexpr int kK2BwdTok = kK2Threads / 32;
+static_assert(kK2BwdTok == kK2Threads / 32, "32 lanes per token");
 
 __global__ __launch_bounds__(kK2Threads) void k2_bwd_small(
     const uint16_t* __restrict__ proj, const K2Params P, const float* __restrict__ g_hpre,
@@ -140,74 +139,7 @@ __global__ __launch_bounds__(kK2Threads) void k2_bwd_small(
   const float gpre = g_hpre ? g_hpre[t * kN + j4] : 0.f;
   stage_params<kK2Threads>(P, sm);
 
-  // Forward, as k2_token32: y = h_pre (q < 4) or the post sigmoid (q < 8),
-  // hq = h_post, a = the softmax weight of permutation q - 8.
-  const float alpha = q < kN ? sm.sc[0] : (q < 2 * kN ? sm.sc[1] : sm.sc[2]);
-  const float z = rb(rb(alpha * p) + sm.sc[3 + q]);
-  const float y = q < 2 * kN ? rb(sigmoid_f32(z)) : 0.f;
-  const float hq = rb(2.f * y);
-  float mx = q >= 2 * kN ? z : -INFINITY;
-#pragma unroll
-  for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 32));
-  const float e = q >= 2 * kN ? expf(z - mx) : 0.f;
-  float sum = 0.f;
-#pragma unroll
-  for (int m = 0; m < kNF; ++m) sum = sum + __shfl(e, 2 * kN + m, 32);
-  const float a = rb(e / sum);
-
-  // Incoming gradients, rounded to bf16 (the .float() casts' backward).
-  const float gh = rb(gh_in);
-  // grad of h_post[i] (lanes 4 + i) and of h_pre[j] (lanes j) through
-  // H_merged = H_res - outer(h_post, h_pre), each sum in the chain's order.
-  float sq = 0.f, sp = 0.f;
-#pragma unroll
-  for (int k = 0; k < kN; ++k) {
-    sq = sq + rb(-__shfl(gh, i4 * kN + k, 32) * __shfl(y, k, 32));
-    sp = sp + rb(-__shfl(gh, k * kN + j4, 32) * __shfl(hq, kN + k, 32));
-  }
-  const float ghq = rb(rb(gpost) + rb(sq));
-  const float ghp = rb(rb(gpre) + rb(sp));
-  // Softmax backward (lanes 8 + m): gy = rb(rb(gH . perm_m) a), gz = rb(gy - a sum(gy)).
-  const int m8 = q >= 2 * kN ? q - 2 * kN : 0;
-  const float* pf = reinterpret_cast<const float*>(sm.perm);
-  float acc = 0.f;
-#pragma unroll
-  for (int k = 0; k < kN * kN; ++k) acc = acc + __shfl(gh, k, 32) * pf[m8 * kN * kN + k];
-  const float gy = q >= 2 * kN ? rb(rb(acc) * a) : 0.f;
-  float sgy = 0.f;
-#pragma unroll
-  for (int m = 0; m < kNF; ++m) sgy = sgy + __shfl(gy, 2 * kN + m, 32);
-  float gz;
-  if (q < kN) {
-    gz = rb(rb(ghp * rb(1.f - y)) * y);
-  } else if (q < 2 * kN) {
-    const float gs = rb(ghq * 2.f);
-    gz = rb(rb(gs * rb(1.f - y)) * y);
-  } else {
-    gz = rb(gy - a * sgy);
-  }
-  if (valid) grad_proj[t * kDk + q] = f32_to_bf16(rb(gz * alpha));
-
-  // This token's parameter terms: the alphas' sums over their logits in
-  // order, the bias gradients gz.
-  const float pc = rb(gz * p);
-  float s0 = 0.f, s1 = 0.f, s2 = 0.f;
-#pragma unroll
-  for (int k = 0; k < kDk; ++k) {
-    const float v = __shfl(pc, k, 32);
-    if (k < kN)
-      s0 += v;
-    else if (k < 2 * kN)
-      s1 += v;
-    else
-      s2 += v;
-  }
-  red[slot][3 + q] = valid ? gz : 0.f;
-  if (q == 0) {
-    red[slot][0] = valid ? s0 : 0.f;
-    red[slot][1] = valid ? s1 : 0.f;
-    red[slot][2] = valid ? s2 : 0.f;
-  }
+  k2_bwd_token32(sm, q, t, valid, true, p, gh_in, gpost, gpre, grad_proj, red[slot]);
   __syncthreads();
   if (threadIdx.x < kNPar) {
     float v = 0.f;

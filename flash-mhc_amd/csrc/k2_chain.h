@@ -12,6 +12,11 @@ constexpr int kN = 4;
 constexpr int kNF = 24;             // n! for n = 4
 constexpr int kDk = 2 * kN + kNF;   // 32 projection columns
 constexpr int kNPar = 3 + kDk;      // alpha_pre, alpha_post, alpha_res, bias[32]
+// K2's backward runs 32 lanes per token, kK2BwdTok tokens per workgroup, up to
+// kK2BwdSmallT tokens (k2_bwd_small, and the pre-map's k3_reduce_k2_bwd), four
+// lanes per token above (k2_bwd_quad); k2.hip gives the measurements.
+constexpr int64_t kK2BwdSmallT = 6144;
+constexpr int kK2BwdTok = 8;
 __device__ __forceinline__ float rb(float v) { return bf16_to_f32(f32_to_bf16(v)); }
 
 // The block parameters K2 reads, in their storage dtype: all fp32 or all bf16
@@ -64,6 +69,38 @@ __device__ __forceinline__ void stage_params(const K2Params& P, K2Smem& sm) {
   }
   __syncthreads();
 }
+
+// stage_params in two halves, so that a kernel can issue the parameter loads
+// early and store them to LDS later, before a barrier of its own: the same
+// values in the same places.
+template <int THREADS>
+struct K2ParamRegs {
+  static constexpr int kPerm = (kNF * kN * kN + THREADS - 1) / THREADS;
+  float perm[kPerm];
+  float sc = 0.f;
+
+  __device__ __forceinline__ void load(const K2Params& P) {
+#pragma unroll
+    for (int r = 0; r < kPerm; ++r) {
+      const int i = static_cast<int>(threadIdx.x) + r * THREADS;
+      perm[r] = i < kNF * kN * kN ? rb(ld_param(P.perm, i, P.bf16)) : 0.f;
+    }
+    const int i = static_cast<int>(threadIdx.x);
+    if (i < 3 + kDk) {
+      const void* src = i == 0 ? P.alpha_pre : (i == 1 ? P.alpha_post : (i == 2 ? P.alpha_res : P.bias));
+      sc = rb(ld_param(src, i < 3 ? 0 : i - 3, P.bf16));
+    }
+  }
+  __device__ __forceinline__ void store(K2Smem& sm) const {
+    float* pf = reinterpret_cast<float*>(sm.perm);
+#pragma unroll
+    for (int r = 0; r < kPerm; ++r) {
+      const int i = static_cast<int>(threadIdx.x) + r * THREADS;
+      if (i < kNF * kN * kN) pf[i] = perm[r];
+    }
+    if (threadIdx.x < 3 + kDk) sm.sc[threadIdx.x] = sc;
+  }
+};
 
 __device__ __forceinline__ void load_params(const K2Smem& sm, float& ap, float& apo, float& ar, float b[kDk]) {
   ap = sm.sc[0];
@@ -273,6 +310,92 @@ __device__ __forceinline__ float k2_token32(const K2Smem& sm, float p, int q, in
   else if (q < 2 * kN)
     h_post[t * kN + (q - kN)] = hq;
   return y;
+}
+
+// K2 backward of token t on a 32-lane group (lane q: logit q; the group's
+// lanes must all be active, width-32 shuffles).  p: the token's projection
+// q; gh_in: grad_H_merged[t, q] for q < 16; gpost / gpre: grad_h_post[t, (q -
+// 4) & 3] and grad_h_pre[t, q & 3], fp32 as they come in.  Writes
+// grad_proj[t, q] when valid and, when write, the token's 35 parameter terms
+// to red_row (zeros for an invalid token): the alphas' sums over their
+// logits in order, then the 32 bias terms gz.  The forward is k2_token32's
+// (bit-identical to the chain) and each sum over the token's terms runs
+// through shuffles in the chain's order.
+__device__ __forceinline__ void k2_bwd_token32(const K2Smem& sm, int q, int64_t t, bool valid, bool write, float p,
+                                               float gh_in, float gpost, float gpre, uint16_t* __restrict__ grad_proj,
+                                               float* red_row) {
+#pragma clang fp contract(off)
+  const int i4 = (q - kN) & 3, j4 = q & 3;
+  // Forward, as k2_token32: y = h_pre (q < 4) or the post sigmoid (q < 8),
+  // hq = h_post, a = the softmax weight of permutation q - 8.
+  const float alpha = q < kN ? sm.sc[0] : (q < 2 * kN ? sm.sc[1] : sm.sc[2]);
+  const float z = rb(rb(alpha * p) + sm.sc[3 + q]);
+  const float y = q < 2 * kN ? rb(sigmoid_f32(z)) : 0.f;
+  const float hq = rb(2.f * y);
+  float mx = q >= 2 * kN ? z : -INFINITY;
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 32));
+  const float e = q >= 2 * kN ? expf(z - mx) : 0.f;
+  float sum = 0.f;
+#pragma unroll
+  for (int m = 0; m < kNF; ++m) sum = sum + __shfl(e, 2 * kN + m, 32);
+  const float a = rb(e / sum);
+
+  // Incoming gradients, rounded to bf16 (the .float() casts' backward).
+  const float gh = rb(gh_in);
+  // grad of h_post[i] (lanes 4 + i) and of h_pre[j] (lanes j) through
+  // H_merged = H_res - outer(h_post, h_pre), each sum in the chain's order.
+  float sq = 0.f, sp = 0.f;
+#pragma unroll
+  for (int k = 0; k < kN; ++k) {
+    sq = sq + rb(-__shfl(gh, i4 * kN + k, 32) * __shfl(y, k, 32));
+    sp = sp + rb(-__shfl(gh, k * kN + j4, 32) * __shfl(hq, kN + k, 32));
+  }
+  const float ghq = rb(rb(gpost) + rb(sq));
+  const float ghp = rb(rb(gpre) + rb(sp));
+  // Softmax backward (lanes 8 + m): gy = rb(rb(gH . perm_m) a), gz = rb(gy - a sum(gy)).
+  const int m8 = q >= 2 * kN ? q - 2 * kN : 0;
+  const float* pf = reinterpret_cast<const float*>(sm.perm);
+  float acc = 0.f;
+#pragma unroll
+  for (int k = 0; k < kN * kN; ++k) acc = acc + __shfl(gh, k, 32) * pf[m8 * kN * kN + k];
+  const float gy = q >= 2 * kN ? rb(rb(acc) * a) : 0.f;
+  float sgy = 0.f;
+#pragma unroll
+  for (int m = 0; m < kNF; ++m) sgy = sgy + __shfl(gy, 2 * kN + m, 32);
+  float gz;
+  if (q < kN) {
+    gz = rb(rb(ghp * rb(1.f - y)) * y);
+  } else if (q < 2 * kN) {
+    const float gs = rb(ghq * 2.f);
+    gz = rb(rb(gs * rb(1.f - y)) * y);
+  } else {
+    gz = rb(gy - a * sgy);
+  }
+  if (valid) grad_proj[t * kDk + q] = f32_to_bf16(rb(gz * alpha));
+
+  // This token's parameter terms: the alphas' sums over their logits in
+  // order, the bias gradients gz.
+  const float pc = rb(gz * p);
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f;
+#pragma unroll
+  for (int k = 0; k < kDk; ++k) {
+    const float v = __shfl(pc, k, 32);
+    if (k < kN)
+      s0 += v;
+    else if (k < 2 * kN)
+      s1 += v;
+    else
+      s2 += v;
+  }
+  if (write) {
+    red_row[3 + q] = valid ? gz : 0.f;
+    if (q == 0) {
+      red_row[0] = valid ? s0 : 0.f;
+      red_row[1] = valid ? s1 : 0.f;
+      red_row[2] = valid ? s2 : 0.f;
+    }
+  }
 }
 
 // K2 forward for T tokens (k2.hip), also zeroing z: fmhc_k2_fwd's launch

@@ -233,6 +233,8 @@ bool bad_sizes(int64_t T, int64_t C, int64_t n) {
 }
 
 }  // namespace
+
+int k3_bwd_lanes8(int C) { return pick_lpt_bwd<8>(C); }
 }  // namespace fmhc
 
 extern "C" int fmhc_k3_fwd(const uint16_t* x, const float* h_pre, uint16_t* out, int64_t T,

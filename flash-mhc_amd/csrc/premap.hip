@@ -177,6 +177,84 @@ __global__ __launch_bounds__(kFinishThreads) void k1_finish_k2_k3(
   }
 }
 
+// Backward, few tokens (T <= kK2BwdSmallT) where K3's backward runs 32 or 64
+// lanes per token: K3's reduce-only pass and K2's backward in one kernel,
+// kK2BwdTok tokens per workgroup.  A token's four grad_h_pre sums are
+// k3_bwd_kernel's (the same lanes, loop order and group sums) and stay in
+// registers; the token's first 32 lanes then run k2_bwd_token32 as
+// k2_bwd_small does, and the workgroup adds its tokens' parameter terms in
+// token order.  grad_proj and the parameter partials are those of K3's
+// backward followed by k2_bwd_small, bit for bit, with one launch and one
+// chain of load latencies fewer.
+template <int LPT>
+__global__ __launch_bounds__(kK2BwdTok * LPT) void k3_reduce_k2_bwd(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ go3, const uint16_t* __restrict__ proj,
+    const K2Params P, const float* __restrict__ g_hpost, const float* __restrict__ g_H,
+    uint16_t* __restrict__ grad_proj, float* __restrict__ partial, int64_t T, int C) {
+  static_assert(LPT == 32 || LPT == 64, "half a wave or one wave per token");
+  constexpr int kThreads = kK2BwdTok * LPT;
+  __shared__ K2Smem sm;
+  __shared__ float red[kK2BwdTok][kNPar];
+  const int slot = static_cast<int>(threadIdx.x) / LPT;
+  const int sub = static_cast<int>(threadIdx.x) % LPT;
+  const int q = sub & 31;
+  const int64_t tq = static_cast<int64_t>(blockIdx.x) * kK2BwdTok + slot;
+  const bool valid = tq < T;
+  const int64_t t = valid ? tq : T - 1;  // idle slots recompute the last token, store nothing
+  // K2's operands and the parameters are loaded before K3's loop.
+  const float p = bf16_to_f32(proj[t * kDk + q]);
+  const float gh_in = (q < kN * kN && g_H) ? g_H[t * kN * kN + q] : 0.f;
+  const float gpost = g_hpost ? g_hpost[t * kN + ((q - kN) & 3)] : 0.f;
+  K2ParamRegs<kThreads> regs;
+  regs.load(P);
+
+  // K3's reduce-only backward of the token: s_j = sum_c x[t, j, c] go3[t, c].
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+  if (valid) {
+    const uint16_t* x0 = x + t * 4 * C;
+    const uint16_t* x1 = x0 + C;
+    const uint16_t* x2 = x1 + C;
+    const uint16_t* x3 = x2 + C;
+    const uint16_t* grow = go3 + t * C;
+    const int ng = C / 8;
+#pragma unroll 2
+    for (int g = sub; g < ng; g += LPT) {
+      float gq[8], a[8], b[8], c[8], d[8];
+      Lanes<8>::load(grow, g, gq);
+      Lanes<8>::load(x0, g, a);
+      Lanes<8>::load(x1, g, b);
+      Lanes<8>::load(x2, g, c);
+      Lanes<8>::load(x3, g, d);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        s0 = __builtin_fmaf(a[e], gq[e], s0);
+        s1 = __builtin_fmaf(b[e], gq[e], s1);
+        s2 = __builtin_fmaf(c[e], gq[e], s2);
+        s3 = __builtin_fmaf(d[e], gq[e], s3);
+      }
+    }
+  }
+  s0 = group_sum<LPT>(s0);
+  s1 = group_sum<LPT>(s1);
+  s2 = group_sum<LPT>(s2);
+  s3 = group_sum<LPT>(s3);
+
+  regs.store(sm);
+  __syncthreads();
+  const int j4 = q & 3;
+  const float gpre = j4 == 0 ? s0 : (j4 == 1 ? s1 : (j4 == 2 ? s2 : s3));
+  // With 64 lanes per token, lanes 32-63 repeat lanes 0-31 and store nothing.
+  const bool first = sub < 32;
+  k2_bwd_token32(sm, q, t, valid && first, first, p, gh_in, gpost, gpre, grad_proj, red[slot]);
+  __syncthreads();
+  if (threadIdx.x < kNPar) {
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < kK2BwdTok; ++w) v += red[w][threadIdx.x];
+    partial[static_cast<int64_t>(blockIdx.x) * kNPar + threadIdx.x] = v;
+  }
+}
+
 struct PremapWs {
   int64_t gh, gp, k2, k1, total;  // byte offsets / sizes
 };
@@ -363,16 +441,31 @@ extern "C" int fmhc_premap_bwd(const uint16_t* x, const uint16_t* W, const void*
   uint16_t* gp = T > 0 ? reinterpret_cast<uint16_t*>(ws + w.gp) : nullptr;
   int st = FMHC_OK;
   const bool fused = T > 0 && k1_bwd_premap_fused(x, W, gp, proj, inv_rms, grad_x, grad_layer_input, grad_x_in, C);
-  if (T > 0) st = fmhc_k3_bwd(x, h_pre, grad_layer_input, fused ? nullptr : grad_x, gh, T, C, n, stream);
-  // K2's backward, whose parameter partials K1's grad_W reduce also sums.
   K2Params P;
-  if (st == FMHC_OK && !k2_params(alpha_pre, alpha_post, alpha_res, bias, perm, param_dtype, P))
-    st = FMHC_ERR_INVALID_ARGUMENT;
+  if (!k2_params(alpha_pre, alpha_post, alpha_res, bias, perm, param_dtype, P)) return FMHC_ERR_INVALID_ARGUMENT;
+  // K2's backward, whose parameter partials K1's grad_W reduce also sums.
   K2ParamSums sums;
-  if (st == FMHC_OK)
-    st = k2_bwd_partials(proj, P, gh, grad_h_post, grad_H_merged, gp, grad_alpha_pre, grad_alpha_post,
-                         grad_alpha_res, grad_bias, T > 0 ? ws + w.k2 : nullptr, T > 0 ? w.k1 - w.k2 : 0, T, s,
-                         &sums);
+  const int lanes = C % 8 == 0 ? k3_bwd_lanes8(static_cast<int>(C)) : 0;
+  if (fused && T <= kK2BwdSmallT && (lanes == 32 || lanes == 64) && aligned16(x) && aligned16(grad_layer_input)) {
+    // Few tokens: K3's reduce-only pass and K2's backward as one kernel.
+    float* partial = reinterpret_cast<float*>(ws + w.k2);
+    const dim3 grid(static_cast<unsigned>((T + kK2BwdTok - 1) / kK2BwdTok));
+    if (lanes == 64)
+      k3_reduce_k2_bwd<64><<<grid, kK2BwdTok * 64, 0, s>>>(x, grad_layer_input, proj, P, grad_h_post,
+                                                            grad_H_merged, gp, partial, T, static_cast<int>(C));
+    else
+      k3_reduce_k2_bwd<32><<<grid, kK2BwdTok * 32, 0, s>>>(x, grad_layer_input, proj, P, grad_h_post,
+                                                            grad_H_merged, gp, partial, T, static_cast<int>(C));
+    st = launch_status();
+    sums = K2ParamSums{partial, static_cast<int64_t>(grid.x), grad_alpha_pre, grad_alpha_post, grad_alpha_res,
+                       grad_bias, P.bf16};
+  } else {
+    if (T > 0) st = fmhc_k3_bwd(x, h_pre, grad_layer_input, fused ? nullptr : grad_x, gh, T, C, n, stream);
+    if (st == FMHC_OK)
+      st = k2_bwd_partials(proj, P, gh, grad_h_post, grad_H_merged, gp, grad_alpha_pre, grad_alpha_post,
+                           grad_alpha_res, grad_bias, T > 0 ? ws + w.k2 : nullptr, T > 0 ? w.k1 - w.k2 : 0, T, s,
+                           &sums);
+  }
   if (st == FMHC_OK)
     st = k1_bwd_premap(x, W, gp, proj, inv_rms, grad_layer_input, h_pre, grad_x_in, grad_x, grad_W,
                        T > 0 ? ws + w.k1 : nullptr, T > 0 ? w.total - w.k1 : 0, T, C, sums, s);
