@@ -14,6 +14,8 @@
 // The backward keeps its 20 per-token partial sums in registers and finishes
 // them with an in-wave butterfly (and, when a token spans several waves, an
 // LDS sum over them in wave order): no atomics, deterministic.
+#include <type_traits>
+
 #include "fmhc_common.h"
 
 namespace fmhc {
@@ -98,7 +100,7 @@ __global__ __launch_bounds__(kBlock) void k4_fwd_kernel(const uint16_t* __restri
   }
 }
 
-template <int VEC, int LPT>
+template <int VEC, int LPT, bool EARLY>
 __global__ __launch_bounds__(kBlock) void k4_bwd_kernel(const uint16_t* __restrict__ x,
                                                         const uint16_t* __restrict__ lo,
                                                         const float* __restrict__ H,
@@ -161,6 +163,13 @@ __global__ __launch_bounds__(kBlock) void k4_bwd_kernel(const uint16_t* __restri
     for (int i = 0; i < 4; ++i) Lanes<VEC>::load(gr[i], g, q[i]);
     Lanes<VEC>::load(lrow, g, l);
 
+    // EARLY: the iteration's x rows load with grad_out and lo, before its
+    // first store (the compiler keeps a load behind an earlier store).
+    float xs[EARLY ? 4 : 1][VEC];
+    if constexpr (EARLY) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) Lanes<VEC>::load(xr[j], g, xs[j]);
+    }
     // grad_lo and the grad_h_post partial sums.
     {
       float o[VEC];
@@ -181,8 +190,12 @@ __global__ __launch_bounds__(kBlock) void k4_bwd_kernel(const uint16_t* __restri
     // One x stream at a time: grad_H partial sums and grad_x.
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      float xv[VEC], o[VEC];
-      Lanes<VEC>::load(xr[j], g, xv);
+      float xl[VEC], o[VEC];
+      const float* xv = xl;
+      if constexpr (EARLY)
+        xv = xs[j];
+      else
+        Lanes<VEC>::load(xr[j], g, xl);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -298,6 +311,8 @@ int launch_k4_fwd(const uint16_t* x, const uint16_t* lo, const float* H, const f
   return launch_status();
 }
 
+constexpr int64_t kK4EarlyLanes = int64_t{16384} * 64;
+
 template <int VEC>
 int launch_k4_bwd(const uint16_t* x, const uint16_t* lo, const float* H, const float* hp,
                   const uint16_t* go, uint16_t* gx, uint16_t* glo, float* gH, float* ghp,
@@ -305,14 +320,33 @@ int launch_k4_bwd(const uint16_t* x, const uint16_t* lo, const float* H, const f
   const int lpt = pick_lpt_bwd<VEC>(C);
   const int64_t tokens_per_block = lpt > kWave ? kBlock / lpt : (kBlock / kWave) * (kWave / lpt);
   const dim3 grid(blocks_for(T, tokens_per_block));
-  switch (lpt) {
-    case 256: k4_bwd_kernel<VEC, 256><<<grid, kBlock, 0, s>>>(x, lo, H, hp, go, gx, glo, gH, ghp, T, C); break;
-    case 128: k4_bwd_kernel<VEC, 128><<<grid, kBlock, 0, s>>>(x, lo, H, hp, go, gx, glo, gH, ghp, T, C); break;
-    case 64: k4_bwd_kernel<VEC, 64><<<grid, kBlock, 0, s>>>(x, lo, H, hp, go, gx, glo, gH, ghp, T, C); break;
-    case 32: k4_bwd_kernel<VEC, 32><<<grid, kBlock, 0, s>>>(x, lo, H, hp, go, gx, glo, gH, ghp, T, C); break;
-    case 16: k4_bwd_kernel<VEC, 16><<<grid, kBlock, 0, s>>>(x, lo, H, hp, go, gx, glo, gH, ghp, T, C); break;
-    default: k4_bwd_kernel<VEC, 8><<<grid, kBlock, 0, s>>>(x, lo, H, hp, go, gx, glo, gH, ghp, T, C); break;
+  // Few waves (up to 64 per CU): each iteration's loads go out before its
+  // stores, so a wave waits for one round trip per iteration instead of five
+  // (block step at C = 1024, HIP graph: T = 1024 96.5 -> 94.6 us, 6000 232.2
+  // -> 228.5 us; K4 backward alone at T = 16384 81.1 -> 79.0 us).  With more
+  // waves the extra registers (124 against 90: four waves per SIMD instead of
+  // five) cost more than the latency they hide (T = 32768 150.8 -> 153.5 us,
+  // 65536 302.2 -> 304.3 us).
+  auto launch = [&](auto early) {
+    constexpr bool E = decltype(early)::value;
+    switch (lpt) {
+      case 256: k4_bwd_kernel<VEC, 256, E><<<grid, kBlock, 0, s>>>(x, lo, H, hp, go, gx, glo, gH, ghp, T, C); break;
+      case 128: k4_bwd_kernel<VEC, 128, E><<<grid, kBlock, 0, s>>>(x, lo, H, hp, go, gx, glo, gH, ghp, T, C); break;
+      case 64: k4_bwd_kernel<VEC, 64, E><<<grid, kBlock, 0, s>>>(x, lo, H, hp, go, gx, glo, gH, ghp, T, C); break;
+      case 32: k4_bwd_kernel<VEC, 32, false><<<grid, kBlock, 0, s>>>(x, lo, H, hp, go, gx, glo, gH, ghp, T, C); break;
+      case 16: k4_bwd_kernel<VEC, 16, false><<<grid, kBlock, 0, s>>>(x, lo, H, hp, go, gx, glo, gH, ghp, T, C); break;
+      default: k4_bwd_kernel<VEC, 8, false><<<grid, kBlock, 0, s>>>(x, lo, H, hp, go, gx, glo, gH, ghp, T, C); break;
+    }
+  };
+  // Measured on the 16-byte path with a wave or more per token; narrower
+  // tokens (C < 512) keep the loop as it is.
+  if constexpr (VEC == 8) {
+    if (lpt >= kWave && T * lpt <= kK4EarlyLanes) {
+      launch(std::true_type{});
+      return launch_status();
+    }
   }
+  launch(std::false_type{});
   return launch_status();
 }
 

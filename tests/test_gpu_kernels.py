@@ -302,6 +302,20 @@ def test_k4_bwd(T, C):
     check_fp32("k4 grad_hp", ghp, *ref["grad_hp"], C)
 
 
+@pytest.mark.parametrize("n,C", [(16384, 1024), (4096, 4096)])
+def test_k4_bwd_early_and_late_loads_agree(n, C):
+    """K4's backward issues each iteration's loads before its stores up to
+    16384 tokens x 64 lanes (n tokens here) and keeps the plain loop above:
+    the same arithmetic in the same order, so the first n tokens of an
+    (n + 1)-token call equal an n-token call bit for bit."""
+    x, lo, H, hp = (t.to(DEV) for t in _k4_inputs(n + 1, C, 97))
+    go = randn((n + 1, 4, C), 98).to(DEV)
+    late = K.k4_bwd(go, x, lo, H, hp)
+    early = K.k4_bwd(go[:n], x[:n], lo[:n], H[:n], hp[:n])
+    for u, v in zip(early, late):
+        assert torch.equal(u, v[:n])
+
+
 def test_k4_misaligned():
     T, C = 129, 1000
     x, lo, H, hp = _k4_inputs(T, C, 90)
