@@ -1127,7 +1127,8 @@ int k1_fwd_run(const uint16_t* x_flat, const uint16_t* W, uint16_t* out, float* 
 // there is one wave per SIMD (kBwdFillWaves).  Measured with grad_W: T = 1024,
 // C = 1024 63 -> 14 us, T = 8192 70 -> 40 us; dx alone at T = 1024 16 -> 6 us.
 // Filling two waves per SIMD instead, or rounding large run counts to whole
-// rounds of resident waves, was slower at C = 4096.
+// rounds of resident waves, was slower at C = 4096; two waves per SIMD also
+// at C = 1024 (block step at T = 4096 / 6000: 170 -> 178 / 230 -> 236 us).
 int64_t k1_bwd_nruns(int64_t T, int64_t nC, int64_t max_blocks, int64_t min_blocks) {
   const int64_t nblocks = (T + 15) / 16;
   if (nblocks <= 0) return 1;
