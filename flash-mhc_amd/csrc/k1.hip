@@ -1062,34 +1062,32 @@ int k1_fwd_blocks(int64_t T) {
   return r < 1 ? 1 : (r < kFwdR ? static_cast<int>(r) : kFwdR);
 }
 
+// Waves per workgroup of the one-pass forward with R blocks: 8 for tiles of
+// 16 and 32 tokens, so that each wave walks half as many column chunks of
+// its few rows (pre-map forward at C = 1024, T = 4096 / 6000 / 8192:
+// 24.1 / 29.9 / 32.7 -> 22.6 / 28.7 / 32.0 us), 4 for larger tiles, whose
+// LDS then leaves room for two workgroups per CU.
+template <int R>
+constexpr int fwd_waves() {
+  return R <= 2 ? 8 : kFwdSplit;
+}
+
 // The one-pass forward with R blocks per workgroup (k1_fwd_blocks); TILE: the
 // pre-map forward on the same tiles.
 template <bool TILE>
 void launch_k1_fwd_onepass(int R, const uint16_t* x, const uint16_t* W, uint16_t* out, float* inv_rms,
                            int64_t T, int nc, const PremapTile& pt, hipStream_t s) {
-  const dim3 block(kWave * kFwdSplit);
   const dim3 grid(blocks_for(T, 16 * R));
-  if constexpr (TILE) {
-    switch (R) {
-      case 1:
-        k1_fwd_mfma<1, kFwdSplit, false, true><<<grid, block, 0, s>>>(x, W, out, inv_rms, nullptr, T, nc, 0, pt);
-        break;
-      case 2:
-        k1_fwd_mfma<2, kFwdSplit, false, true><<<grid, block, 0, s>>>(x, W, out, inv_rms, nullptr, T, nc, 0, pt);
-        break;
-      case 3:
-        k1_fwd_mfma<3, kFwdSplit, false, true><<<grid, block, 0, s>>>(x, W, out, inv_rms, nullptr, T, nc, 0, pt);
-        break;
-      default:
-        k1_fwd_mfma<4, kFwdSplit, false, true><<<grid, block, 0, s>>>(x, W, out, inv_rms, nullptr, T, nc, 0, pt);
-    }
-  } else {
-    switch (R) {
-      case 1: k1_fwd_mfma<1, kFwdSplit, false><<<grid, block, 0, s>>>(x, W, out, inv_rms, nullptr, T, nc, 0); break;
-      case 2: k1_fwd_mfma<2, kFwdSplit, false><<<grid, block, 0, s>>>(x, W, out, inv_rms, nullptr, T, nc, 0); break;
-      case 3: k1_fwd_mfma<3, kFwdSplit, false><<<grid, block, 0, s>>>(x, W, out, inv_rms, nullptr, T, nc, 0); break;
-      default: k1_fwd_mfma<4, kFwdSplit, false><<<grid, block, 0, s>>>(x, W, out, inv_rms, nullptr, T, nc, 0);
-    }
+  auto launch = [&](auto r) {
+    constexpr int kR = decltype(r)::value;
+    constexpr int kS = fwd_waves<kR>();
+    k1_fwd_mfma<kR, kS, false, TILE><<<grid, kWave * kS, 0, s>>>(x, W, out, inv_rms, nullptr, T, nc, 0, pt);
+  };
+  switch (R) {
+    case 1: launch(std::integral_constant<int, 1>{}); break;
+    case 2: launch(std::integral_constant<int, 2>{}); break;
+    case 3: launch(std::integral_constant<int, 3>{}); break;
+    default: launch(std::integral_constant<int, 4>{});
   }
 }
 
