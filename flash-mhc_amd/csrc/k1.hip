@@ -999,8 +999,14 @@ constexpr int64_t kFwdCUs = 256;
 // kSplitMax column ranges per block, aiming at kSplitTarget workgroups, each
 // range at least one 64-wide chunk per wave of the workgroup (narrower ranges
 // left waves idle: C = 1024, T = 1 ... 257 took 0.5-0.9 us longer); taken
-// when the plan has at least kSplitMinS ranges (T <= 2720 from C = 128 on):
-// from there on the one-pass kernel is faster (T = 3000 ... 6000: 20-40%).
+// when the plan has at least kSplitMinS ranges (T <= 2720 from C = 128 on),
+// twice that for rows of up to 64 chunks (C <= 1024: T <= 1024), whose
+// one-pass waves walk at most 8 chunks each.  At C = 1024 the pre-map forward
+// then takes 14.9 / 16.7 / 17.0 us at T = 1536 / 2048 / 2720 instead of
+// 18.8 / 18.6 / 24.8 (the K1 op 11.6 / 11.8 / 12.0 against 10.7 / 10.9 /
+// 13.7); at C = 4096 (32 chunks per wave) the split stays the faster form
+// (T = 1536: pre-map 39.0 against 48.6 us).  Above these counts the one-pass
+// kernel is faster (T = 3000 ... 6000: 20-40%).
 constexpr int kSplitR = 1;
 constexpr int64_t kSplitTarget = 512;
 constexpr int64_t kSplitMax = 64;
@@ -1043,7 +1049,7 @@ K1FwdSplit k1_fwd_split(int64_t T, int64_t nC) {
   if (T <= 0 || nC % 8 != 0 || nC > (int64_t{1} << 24) || nall < 2) return p;
   const int64_t nblk = (T + 16 * kSplitR - 1) / (16 * kSplitR);
   int64_t S = (kSplitTarget + nblk - 1) / nblk;
-  if (S < kSplitMinS) return p;
+  if (S < (nall <= 64 ? 2 * kSplitMinS : kSplitMinS)) return p;
   S = S < kSplitMax ? S : kSplitMax;
   S = S < nall / kFwdSplit ? S : nall / kFwdSplit;
   if (S < 2) return p;

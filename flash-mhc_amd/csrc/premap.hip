@@ -12,9 +12,10 @@
 // autograd's separate accumulation pass (1.5 x T x nC x 2 bytes).
 //
 // Forward, from the token count where K1 runs one pass on (no column split;
-// T > 2720 at C >= 128): one kernel (k1_premap_tile, k1.hip).  Each workgroup
-// runs K1 on its tile (16, 32, 48 or 64 tokens, the fewest that keep the
-// launch to one round on the CUs) with ordinary loads of x, then
+// T > 1024 up to C = 1024, T > 2720 above): one kernel (k1_premap_tile,
+// k1.hip).  Each workgroup runs K1 on its tile (16, 32, 48 or 64 tokens, the
+// fewest that keep the launch to one round on the CUs) with ordinary loads of
+// x, then
 // K2 on the tile's tokens (four lanes per token) and K3 on the tile, whose
 // re-read of the tile's rows finds them in L2 or the memory-side cache: x
 // comes from HBM about once (T = 65536, C = 1024: 178 us against 209 us for
@@ -337,8 +338,8 @@ int premap_fwd_run(const uint16_t* x, const uint16_t* W, const void* alpha_pre, 
 }
 
 // Scratch of fmhc_premap_fwd_noalloc: the column-split forward's partial sums
-// (T x 33 x S4 fp32 for T <= 2048 tokens; at most 2,145,792 bytes over every
-// (T, C), at T = 2032, C = 320).  Each device holds its own copy for the life
+// (T x 33 x S4 fp32 for T <= 2720 tokens; at most 2,145,792 bytes over every
+// (T, C), at T = 2032, C = 1040).  Each device holds its own copy for the life
 // of the process.  In host code `scratch` names a host-side stand-in, so its
 // device address is looked up once per device (scratch_on_device) and only
 // that address is used.

@@ -53,7 +53,8 @@ extern "C" {
  *           src/flash_mhc/kernels.py:250-303 (_fused_rmsnorm_project_fwd_kernel). */
 int fmhc_k1_fwd(const uint16_t* x_flat, const uint16_t* W, uint16_t* out, float* inv_rms,
                 int64_t T, int64_t nC, int64_t D_out, void* stream);
-/* fmhc_k1_fwd with a workspace: for few tokens (T <= 2048) the nC axis is split
+/* fmhc_k1_fwd with a workspace: for few tokens (T <= 1024 up to nC = 4096,
+ * T <= 2720 above) the nC axis is split
  * over up to 64 workgroups per 16-token block, whose fp32 partial sums (in
  * `workspace`) a second kernel adds in a fixed order.  `workspace`: at least
  * fmhc_k1_fwd_workspace_bytes(T, nC) bytes, 16-byte aligned (may be NULL when
@@ -155,7 +156,7 @@ int64_t fmhc_premap_fwd_workspace_bytes(int64_t T, int64_t C);
  * allocation).  The few-token forward's partial sums go to a static 4 MiB
  * device array of the library (one per device, held until the process ends),
  * which covers every shape (at most 2,145,792 bytes are needed, at T = 2032,
- * C = 320); a shape needing more returns FMHC_ERR_SCRATCH_LIMIT.  The array's
+ * C = 1040); a shape needing more returns FMHC_ERR_SCRATCH_LIMIT.  The array's
  * device address is looked up on the first call on each device.  `stream`
  * must belong to the current device (else FMHC_ERR_INVALID_ARGUMENT).  Every
  * call on a device shares that device's array and overwrites what the last

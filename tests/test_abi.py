@@ -164,14 +164,16 @@ def test_ctypes_signatures_cover_argument_counts():
 def test_noalloc_scratch_covers_every_shape():
     """fmhc_premap_fwd_noalloc's static scratch (4 MiB) holds the column-split
     partial sums of every shape: the workspace sizing (a host computation) over
-    every T the split takes (T <= 2048) and C up to 4096 peaks at 2,145,792
-    bytes, reached at T = 2032, C = 320."""
+    every T the split takes (T <= 1024 up to C = 1024, T <= 2720 above) and C
+    up to 4096 peaks at 2,145,792 bytes, reached at T = 2032, C = 1040."""
     lib = _abi.load()
     f = lib.fmhc_premap_fwd_workspace_bytes
-    assert f(2032, 320) == 2145792
+    assert f(2032, 1040) == 2145792
+    assert f(2032, 1024) == 0 and f(1024, 1024) > 0  # rows up to 64 chunks: T <= 1024
+    assert f(2721, 4096) == 0 and f(2720, 4096) > 0
     assert f(4096, 1024) == 0 and f(0, 1024) == 0
     peak = 0
     for C in range(8, 4097, 8):
-        for T in list(range(1, 129)) + list(range(1904, 2049)):
+        for T in list(range(1, 129)) + list(range(1904, 2721)):
             peak = max(peak, f(T, C))
     assert peak == 2145792 <= 4 << 20
