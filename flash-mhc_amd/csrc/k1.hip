@@ -1005,7 +1005,9 @@ constexpr int64_t kFwdCUs = 256;
 // then takes 14.9 / 16.7 / 17.0 us at T = 1536 / 2048 / 2720 instead of
 // 18.8 / 18.6 / 24.8 (the K1 op 11.6 / 11.8 / 12.0 against 10.7 / 10.9 /
 // 13.7); at C = 4096 (32 chunks per wave) the split stays the faster form
-// (T = 1536: pre-map 39.0 against 48.6 us).  Above these counts the one-pass
+// (T = 1536: pre-map 39.0 against 48.6 us), and at C = 2048 it is up to
+// T = 2048 (K1 op 16.2 against 19.4 us at T = 1536, though 35.2 against
+// 28.4 us for the pre-map at 2720).  Above these counts the one-pass
 // kernel is faster (T = 3000 ... 6000: 20-40%).
 constexpr int kSplitR = 1;
 constexpr int64_t kSplitTarget = 512;
