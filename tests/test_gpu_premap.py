@@ -146,7 +146,8 @@ def test_block_premap_equals_separate_ops(ckpt):
         assert bool(((a - b).abs() <= tol).all()), f"{n}: max diff {float((a - b).abs().max()):.3e}"
 
 
-@pytest.mark.parametrize("T,C", [(4096, 1024), (257, 1024), (1, 256), (2000, 2048), (300, 1000), (333, 100), (45, 24)])
+@pytest.mark.parametrize("T,C", [(4096, 1024), (257, 1024), (1, 256), (777, 256), (6144, 1024), (6145, 1024),
+                                 (2000, 2048), (300, 1000), (333, 100), (45, 24)])
 def test_premap_bwd_equals_composed_kernels(T, C):
     """The fused pre-map backward equals K3 backward + K2 backward + K1
     backward (with grad_W) + the bf16 sum of x's two gradients: bit for bit on
@@ -154,7 +155,10 @@ def test_premap_bwd_equals_composed_kernels(T, C):
     C % 8 != 0 K3 writes its term and K1's element-wise kernel adds dx to it,
     while the separate K1 op can still take its MFMA kernel (n C % 8 == 0):
     their fp32 summation orders differ, so those shapes are held to the bf16
-    chain bound."""
+    chain bound.  Up to 6144 tokens with 32 or 64 lanes per token in K3's
+    backward (C = 256 ... 2040) K3's reduce and K2's backward run as one kernel
+    (T = 777 at C = 256: half a wave per token, a ragged last workgroup;
+    6144 / 6145: the last fused size and the first separate one)."""
     nC = 4 * C
     x = randn((T, 4, C), 3000 + T + C).to(DEV)
     W = randn((32, nC), 3001 + C, 0.02).to(DEV)
