@@ -127,6 +127,28 @@ def test_k2_misaligned_many_tokens_equals_aligned(T):
         assert torch.equal(u, v)
 
 
+@pytest.mark.parametrize("which", ["h_post only", "h_pre and H"])
+def test_k2_bwd_many_tokens_null_grads(which):
+    """Above 6144 tokens (four lanes per token) a missing output gradient counts
+    as zero, as in the 32-lane kernel: grad_proj and the parameter gradients
+    against the chain's oracle, T = 7001 (a ragged last workgroup)."""
+    T = 7001
+    proj, alphas, bias, grads = _case(T, 40)
+    g = list(grads)
+    if which == "h_post only":
+        g[0], g[2] = None, None
+    else:
+        g[1] = None
+    gp, ga1, ga2, ga3, gb = K.k2_bwd(*_dev([proj, *alphas, bias, PERM]), *[None if t is None else t.to(DEV) for t in g])
+    torch.cuda.synchronize()
+    r = K2O.k2_bwd(proj, *alphas, bias, PERM, *g)
+    check_chain("k2 grad_proj (null grads)", gp, r["grad_proj"])
+    for name, got, n in (("grad_alpha_pre", ga1, 4 * T), ("grad_alpha_post", ga2, 4 * T),
+                         ("grad_alpha_res", ga3, 24 * T)):
+        R, S = r[name]
+        check_bf16(name, got.to(BF16), torch.tensor([R], dtype=F64), torch.tensor([S], dtype=F64), n)
+
+
 def test_k2_deterministic():
     proj, alphas, bias, grads = _case(20000, 30)
     args = _dev([proj, *alphas, bias, PERM, *grads])
