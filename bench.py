@@ -276,7 +276,7 @@ def block_step_graphed(T: int = 4096, C: int = 1024, iters: int = 20) -> dict:
     g = torch.cuda.CUDAGraph()
     blk.zero_grad(set_to_none=True)
     x.grad = None
-    with torch.cuda.graph(g):
+    with torch.cuda.graph(g, stream=s):  # the warm-up's stream (autograd's AccumulateGrad streams)
         blk(x).backward(up)
     out["graph_ms"] = timed(g.replay)
     out["workload"] = f"MHCLiteBlock(4, {C}, Linear({C}, {C})) forward + backward, T={T}, bf16"

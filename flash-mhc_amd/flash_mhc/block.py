@@ -32,7 +32,6 @@ from contextlib import nullcontext
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
-from torch.utils._python_dispatch import _get_current_dispatch_mode
 from torch.utils.checkpoint import checkpoint as _checkpoint
 
 from . import ops as _ops
@@ -54,14 +53,36 @@ def build_permutation_matrices(n: int) -> tuple[torch.Tensor, int]:
     return mats.reshape(images.shape[0], n * n), 0
 
 
+def _private_probe(get):
+    """A private torch query, or None where this torch build lacks it."""
+    try:
+        return get()
+    except (AttributeError, ImportError):
+        return None
+
+
+# Two private torch queries the eager fast paths rely on.  Where a torch
+# build lacks either, _plain_eager is always False and every forward takes the
+# torch.library ops (the same kernels, through the dispatcher).
+def _dispatch_mode_query():
+    from torch.utils._python_dispatch import _get_current_dispatch_mode
+
+    return _get_current_dispatch_mode
+
+
+_dispatch_mode = _private_probe(_dispatch_mode_query)
+_functorch_active = _private_probe(lambda: torch._C._are_functorch_transforms_active)
+
+
 def _plain_eager(x: torch.Tensor) -> bool:
     """x is an ordinary GPU tensor in eager mode: not traced or compiled, no
     Python dispatch mode (fake tensors, functionalization) and no functorch
     transform is active, so the ops' device implementations can be called
     without going through the ops."""
+    if _dispatch_mode is None or _functorch_active is None:
+        return False
     return (type(x) is torch.Tensor and x.is_cuda and not torch.compiler.is_compiling()
-            and not torch.jit.is_tracing() and _get_current_dispatch_mode() is None
-            and not torch._C._are_functorch_transforms_active())
+            and not torch.jit.is_tracing() and _dispatch_mode() is None and not _functorch_active())
 
 
 class MHCLiteBlock(nn.Module):

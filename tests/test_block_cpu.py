@@ -109,6 +109,25 @@ def test_cpu_input_takes_plain_path(monkeypatch):
     assert out.shape == (4, 4, 16)
 
 
+def test_private_torch_queries_fall_back(monkeypatch):
+    """The eager fast paths rely on two private torch queries; a torch build
+    without them must still import the package and make _plain_eager False
+    (the torch.library ops then run), not raise."""
+    from flash_mhc import block as B
+
+    assert B._private_probe(lambda: torch._C._no_such_query_in_torch) is None
+
+    def missing():
+        from torch.utils._python_dispatch import _no_such_function  # noqa: F401
+
+    assert B._private_probe(missing) is None
+    x = torch.empty(1)
+    monkeypatch.setattr(B, "_dispatch_mode", None)
+    assert B._plain_eager(x) is False
+    monkeypatch.setattr(B, "_functorch_active", None)
+    assert B._plain_eager(x) is False
+
+
 def test_kwargs_reach_the_layer():
     class L(torch.nn.Module):
         def forward(self, x, *, scale=1.0):

@@ -389,9 +389,16 @@ def test_graph_capture_training_step(T, ckpt):
     g = torch.cuda.CUDAGraph()
     blk.zero_grad(set_to_none=True)
     sx.grad = None
-    with torch.cuda.graph(g):
+    # Captured on the warm-up's stream: the parameters' AccumulateGrad nodes
+    # keep the stream of their first backward, and a capture on another one
+    # makes autograd add cross-stream syncs (and warn).
+    with torch.cuda.graph(g, stream=s):
         sout = blk(sx)
         sout.backward(sup)
+    # Keep only the output buffer: a live reference to the captured autograd
+    # graph would keep its AccumulateGrad nodes (stream s) for the eager
+    # steps below, which run on the default stream.
+    sout = sout.detach()
     # The gradients the captured backward writes (the eager steps below
     # attach new ones to the parameters).
     names = [n for n, _ in blk.named_parameters()]

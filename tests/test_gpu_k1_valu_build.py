@@ -34,7 +34,8 @@ def randn(shape, seed, scale=1.0):
 def valu():
     _abi.load()  # torch's HIP runtime first, then the variant (same soname resolution)
     path = build.variant_path("k1_valu")
-    assert path.exists(), f"build the evidence variant first: {path}"
+    if not path.exists():
+        pytest.skip(f"evidence build not present: {path} (python -m flash_mhc.build --variants)")
     lib = ctypes.CDLL(str(path), mode=ctypes.RTLD_LOCAL)
     for name, argtypes in _abi.SIGNATURES.items():
         fn = getattr(lib, name)
