@@ -37,6 +37,17 @@ struct PremapTile {
 bool k1_premap_tile(const uint16_t* x, const uint16_t* W, uint16_t* proj, float* inv_rms, const PremapTile& pt,
                     int64_t T, int64_t C, hipStream_t s, int* status);
 
+// The pre-map forward with one read of x for rows of C = 512 or 1024 per
+// stream (premap_resident.hip): W resident on each CU, a 16-token block of
+// rows in registers from K1 to K3.  Returns false (nothing launched) when the
+// shape, token count (below kResidentMinT), layer input or alignment does not
+// allow it.  Against the tile kernel at C = 1024 (cold): T = 16384 51.9
+// against 49.9 us, 32768 89.9 against 89.8, 65536 159 against 174, 131072 296
+// against 331.
+constexpr int64_t kResidentMinT = 32768;
+bool premap_resident(const uint16_t* x, const uint16_t* W, uint16_t* proj, float* inv_rms, const PremapTile& pt,
+                     int64_t T, int64_t C, hipStream_t s, int* status);
+
 int k1_fwd_partials(const uint16_t* x_flat, const uint16_t* W, void* ws, int64_t ws_bytes, int64_t T,
                     int64_t nC, hipStream_t s);
 

@@ -11,22 +11,22 @@
 // (bf16(grad_x_in + pre-map gradient), autograd's sum), which replaces
 // autograd's separate accumulation pass (1.5 x T x nC x 2 bytes).
 //
-// Forward, from the token count where K1 runs one pass on (no column split;
-// T > 1024 up to C = 1024, T > 2720 above): one kernel (k1_premap_tile,
-// k1.hip).  Each workgroup runs K1 on its tile (16, 32, 48 or 64 tokens, the
-// fewest that keep the launch to one round on the CUs) with ordinary loads of
-// x, then
-// K2 on the tile's tokens (four lanes per token) and K3 on the tile, whose
-// re-read of the tile's rows finds them in L2 or the memory-side cache: x
-// comes from HBM about once (T = 65536, C = 1024: 178 us against 209 us for
-// three kernels; with nontemporal K1 loads, which do not leave the rows in
-// the caches, the one kernel is no faster than three).  Keeping the tile in
-// LDS instead does not fit beside K1's pipeline: tiles of 8-16 tokens make
-// every tile re-read all of W (32 x nC) from L2.  Fewer tokens, and shapes
-// off the matrix-core path: K1 -> K2 -> K3, the kernels of k1.hip, k2.hip,
-// k3.hip; for few tokens K1 is split over the columns (partial sums in the
-// caller's workspace), and its second stage runs inside the K2 kernel
-// (k1_finish_k2; with K3 too when the layer input is wanted,
+// Forward.  Rows of C = 512 or 1024 per stream with at least 32768 tokens
+// and a layer input: the single-read kernel (premap_resident.hip), which
+// keeps W on each CU and reads every row of x once.  Other shapes from the
+// token count where K1 runs one pass (no column split; T > 1024 up to
+// C = 1024, T > 2720 above): one tile kernel (k1_premap_tile, k1.hip).  Each
+// workgroup runs K1 on its tile (16, 32, 48 or 64 tokens, the fewest that
+// keep the launch to one round on the CUs) with ordinary loads of x, then K2
+// on the tile's tokens (four lanes per token) and K3 on the tile.  K3's
+// re-read of the tile misses L2: past L2 the kernel moves x twice (FETCH_SIZE
+// 2 x x), as three kernels do, in 15% less time (T = 65536, C = 1024: 174
+// against 209 us cold), and the same kernel with nontemporal K1 loads is no
+// faster than three kernels, which places the gain in the re-read.  Fewer
+// tokens, and shapes off the matrix-core path: K1 -> K2 -> K3, the kernels of
+// k1.hip, k2.hip, k3.hip; for few tokens K1 is split over the columns
+// (partial sums in the caller's workspace), and its second stage runs inside
+// the K2 kernel (k1_finish_k2; with K3 too when the layer input is wanted,
 // k1_finish_k2_k3).
 
 #include <hip/hip_runtime.h>
@@ -43,6 +43,12 @@
 // as three kernels, each reading x from HBM.
 #ifndef FMHC_PREMAP_TILE
 #define FMHC_PREMAP_TILE 1
+#endif
+// 1: rows of C = 512 or 1024 per stream and many tokens take the kernel that
+// keeps W and the rows on chip (premap_resident.hip, x read once); 0 (an
+// evidence build): they take the tile kernel, whose K3 part re-reads x.
+#ifndef FMHC_PREMAP_RESIDENT
+#define FMHC_PREMAP_RESIDENT 1
 #endif
 
 namespace {
@@ -307,6 +313,7 @@ int premap_fwd_run(const uint16_t* x, const uint16_t* W, const void* alpha_pre, 
     pt.C = static_cast<int>(C);
     pt.z = z;
     int st = FMHC_OK;
+    if (FMHC_PREMAP_RESIDENT && fmhc::premap_resident(x, W, proj, inv_rms, pt, T, C, s, &st)) return st;
     if (fmhc::k1_premap_tile(x, W, proj, inv_rms, pt, T, C, s, &st)) return st;
   }
   const int S = fmhc::k1_fwd_partials(x, W, workspace, workspace_bytes, T, n * C, s);

@@ -1,0 +1,472 @@
+// The pre-map forward (K1 -> K2 -> K3 of block.py:157-177 of alint77/flash-mHC)
+// with one read of x, for rows of C = 512 or 1024 per stream: a workgroup per
+// CU keeps all of W (32 x 4C bf16, 256 KiB at C = 1024) on its CU for the
+// whole launch -- at C = 1024 half in registers, half in LDS; at C = 512 all
+// in LDS -- and walks 16-token blocks of rows held in registers.  Each
+// block's rows are read once: K1 runs on them (matrix cores), K2 on its 16
+// projections, then K3 mixes the same registers into the layer input.  No
+// other workgroup is involved, so nothing waits on another CU.
+//
+// Why W has to be on chip: the vector memory counter of gfx950 is in order,
+// so a load issued after the next block's prefetch cannot be consumed before
+// that prefetch lands.  Streaming W from L2 while x is prefetched a block
+// ahead would wait for the prefetch at every k-step.  With W in registers and
+// LDS the only global loads are the rows of x.
+//
+// Layout.  Four waves per workgroup (one per SIMD, up to 512 registers each);
+// wave w owns columns w CPW .. + CPW of each of the four streams (CPW = C / 4),
+// i.e. KS = C / 32 k-steps of the 16x16x32 MFMA.  A block is held as two
+// halves of KS / 2 k-steps, each half the same pieces of all four streams
+// (col_of below); for a k-step over 32 columns c0 .. c0 + 32 of stream j, lane
+// l holds
+//   x  (MFMA B):  x[t0 + (l & 15), j, c0 + 8 (l >> 4) + e]
+//   W  (MFMA A):  W[d, j C + c0 + 8 (l >> 4) + e], d = l & 15 and 16 + (l & 15)
+// so every lane holds the same token and columns of all four streams: K3 is
+// lane-local, with k3_token's arithmetic.  The sum of squares is the diagonal
+// of x x^T, a third MFMA on the same registers (exact bf16 products, fp32
+// sums), as in K1's one-pass kernel.  The waves' partial sums are added in
+// wave order through LDS.  K2 runs 16 lanes per token (k2_token16_lds: the
+// chain's bits, its cross-lane values exchanged through LDS), and the block's
+// K1 / K2 outputs are staged in LDS and stored as whole 16-byte pieces of
+// contiguous rows (per-lane scattered stores of them cost 40 us at
+// T = 65536).
+//
+// Outputs: proj, inv_rms, h_pre, h_post, H_merged and the layer input, the
+// values of K1 -> K2 -> K3 up to K1's fp32 summation order (this kernel
+// partitions the contraction over four waves of C columns each).
+//
+// Measured at T = 65536 (cold caches): C = 1024 159 us against 174 us for the
+// tile kernel that re-reads x, C = 512 90 against 93 us; T = 131072, C = 1024:
+// 296 against 331 us.  The memory floor of the same loads and stores without
+// any arithmetic is 121-124 us at C = 1024: W (256 KiB) and one and a half
+// blocks of rows (192 KiB) fill the CU's registers and LDS, so the second
+// half of each block is issued only once the previous block is mixed, and
+// every step waits about one memory latency for it.
+
+#include <hip/hip_runtime.h>
+
+#include "fmhc_common.h"
+#include "k1_premap.h"
+#include "k2_chain.h"
+
+namespace fmhc {
+namespace {
+
+
+__device__ __forceinline__ bf16x8 as_bf(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+__device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(a), as_bf(b), c, 0, 0, 0);
+}
+
+// K2's exchanges within a token: its softmax exponentials and weights and its
+// sigmoid values (h_pre 0-3, h_post 4-7), written by the lanes that compute
+// them and read back by all 32 lanes of the token (broadcast reads).
+struct K2Xchg {
+  float e[16][kNF];
+  float a[16][kNF];
+  float y[16][2 * kN];
+};
+
+// A block's K1 and K2 outputs, staged for whole-row stores (h_pre: hp below).
+struct K2Out {
+  uint16_t pj[16][kDk];
+  float inv[16];
+  float hq[16][kN];
+  float H[16][kN * kN];
+};
+
+// NW waves per workgroup, KS k-steps per wave, the first KR of them with W in
+// registers, the rest in LDS.
+template <int NW, int KS, int KR>
+struct ResidentSmem {
+  u32x4 w[NW][KS > KR ? KS - KR : 1][2][kWave];  // W A operands kept in LDS (rows 0-15, 16-31)
+  union {
+    struct {
+      float red[NW][8][kWave];  // per-wave partial projections, MFMA D layout
+      float red_ss[NW][16];     // per-wave partial sums of squares
+    } r;
+    K2Xchg x;  // used once the partial sums have been added
+  } u;
+  float tok[16][kDk + 1];    // a block's sums: projections [t][d], squares [t][32]
+  float hp[16][kN];          // a block's h_pre, for K3 and its store
+  K2Out out;
+  float permT[kN * kN][kNF];  // perm transposed: H_res entry r, permutation m
+  K2Smem k2;
+};
+
+// K2 forward of token tt on lanes q = 0..31 of a 32-lane group (p: the
+// token's projection q as a bf16 value): k2_token32's operations in its
+// order -- logit q, the maximum over the softmax logits, the softmax
+// denominator added over m = 0..23, weight q - 8, H_res entry q & 15 added
+// over m = 0..23, H_merged -- with the values other lanes hold read from LDS
+// instead of shuffled, so the results are k2_token32's (and the chain's) bit
+// for bit.  Outputs go to the block's staging area; returns the lane's
+// sigmoid value (h_pre[q] for q < 4).
+__device__ __forceinline__ float k2_token32_lds(const K2Smem& k2, const float (&permT)[kN * kN][kNF], K2Xchg& xc,
+                                                K2Out& out, float* hp_out, int tt, int q, float p) {
+#pragma clang fp contract(off)
+  const float alpha = q < kN ? k2.sc[0] : (q < 2 * kN ? k2.sc[1] : k2.sc[2]);
+  const float z = rb(rb(alpha * p) + k2.sc[3 + q]);
+  const float y = q < 2 * kN ? rb(sigmoid_f32(z)) : 0.f;  // h_pre (q < 4), sigmoid of the post logit
+  const float hq = rb(2.f * y);                             // h_post for 4 <= q < 8
+  float mx = q >= 2 * kN ? z : -INFINITY;
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 32));
+  const float e = q >= 2 * kN ? expf(z - mx) : 0.f;
+  if (q >= 2 * kN) xc.e[tt][q - 2 * kN] = e;
+  if (q < 2 * kN) xc.y[tt][q] = q < kN ? y : hq;
+  // The group is one wave's half: its LDS writes above precede these reads.
+  const f32x4* ev = reinterpret_cast<const f32x4*>(xc.e[tt]);
+  float sum = 0.f;
+#pragma unroll
+  for (int m4 = 0; m4 < kNF / 4; ++m4) {
+    const f32x4 v = ev[m4];
+    sum = sum + v[0];
+    sum = sum + v[1];
+    sum = sum + v[2];
+    sum = sum + v[3];
+  }
+  const float a = rb(e / sum);
+  if (q >= 2 * kN) xc.a[tt][q - 2 * kN] = a;
+  const int r = q & 15;
+  const f32x4* av = reinterpret_cast<const f32x4*>(xc.a[tt]);
+  const f32x4* pv = reinterpret_cast<const f32x4*>(permT[r]);
+  float acc = 0.f;
+#pragma unroll
+  for (int m4 = 0; m4 < kNF / 4; ++m4) {
+    const f32x4 am = av[m4], pm = pv[m4];
+    acc = acc + am[0] * pm[0];
+    acc = acc + am[1] * pm[1];
+    acc = acc + am[2] * pm[2];
+    acc = acc + am[3] * pm[3];
+  }
+  const float hp_j = xc.y[tt][q & 3];
+  const float hq_i = xc.y[tt][kN + (r >> 2)];
+  if (q < kN * kN) out.H[tt][q] = rb(rb(acc) - rb(hq_i * hp_j));
+  if (q < kN)
+    hp_out[q] = y;
+  else if (q < 2 * kN)
+    out.hq[tt][q - kN] = hq;
+  return y;
+}
+
+// The same with 16 lanes per token, so that four waves take a block's 16
+// tokens at once: lane r (0-15) computes logits r and 16 + r (r < 4: h_pre,
+// r < 8: h_post, otherwise softmax terms r - 8 and 8 + r), and H_res /
+// H_merged entry r.  Every value is k2_token32's expression in its order;
+// p0 / p1 are projections r and 16 + r as bf16 values.
+__device__ __forceinline__ void k2_token16_lds(const K2Smem& k2, const float (&permT)[kN * kN][kNF], K2Xchg& xc,
+                                               K2Out& out, float* hp_out, int tt, int r, float p0, float p1) {
+#pragma clang fp contract(off)
+  const float alpha0 = r < kN ? k2.sc[0] : (r < 2 * kN ? k2.sc[1] : k2.sc[2]);
+  const float z0 = rb(rb(alpha0 * p0) + k2.sc[3 + r]);
+  const float z1 = rb(rb(k2.sc[2] * p1) + k2.sc[3 + 16 + r]);
+  const float y = r < 2 * kN ? rb(sigmoid_f32(z0)) : 0.f;  // h_pre (r < 4), sigmoid of the post logit
+  const float hq = rb(2.f * y);                             // h_post for 4 <= r < 8
+  float mx = r >= 2 * kN ? fmaxf(z0, z1) : z1;
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 16));
+  const float e0 = r >= 2 * kN ? expf(z0 - mx) : 0.f;
+  const float e1 = expf(z1 - mx);
+  if (r >= 2 * kN) xc.e[tt][r - 2 * kN] = e0;
+  xc.e[tt][8 + r] = e1;
+  if (r < 2 * kN) xc.y[tt][r] = r < kN ? y : hq;
+  // The 16-lane group is part of one wave: its LDS writes precede these reads.
+  const f32x4* ev = reinterpret_cast<const f32x4*>(xc.e[tt]);
+  float sum = 0.f;
+#pragma unroll
+  for (int m4 = 0; m4 < kNF / 4; ++m4) {
+    const f32x4 v = ev[m4];
+    sum = sum + v[0];
+    sum = sum + v[1];
+    sum = sum + v[2];
+    sum = sum + v[3];
+  }
+  if (r >= 2 * kN) xc.a[tt][r - 2 * kN] = rb(e0 / sum);
+  xc.a[tt][8 + r] = rb(e1 / sum);
+  const f32x4* av = reinterpret_cast<const f32x4*>(xc.a[tt]);
+  const f32x4* pv = reinterpret_cast<const f32x4*>(permT[r]);
+  float acc = 0.f;
+#pragma unroll
+  for (int m4 = 0; m4 < kNF / 4; ++m4) {
+    const f32x4 am = av[m4], pm = pv[m4];
+    acc = acc + am[0] * pm[0];
+    acc = acc + am[1] * pm[1];
+    acc = acc + am[2] * pm[2];
+    acc = acc + am[3] * pm[3];
+  }
+  const float hp_j = xc.y[tt][r & 3];
+  const float hq_i = xc.y[tt][kN + (r >> 2)];
+  out.H[tt][r] = rb(rb(acc) - rb(hq_i * hp_j));
+  if (r < kN)
+    hp_out[r] = y;
+  else if (r < 2 * kN)
+    out.hq[tt][r - kN] = hq;
+}
+
+template <int NW, int KS, int KR>
+__global__ __launch_bounds__(NW * kWave) void premap_resident_fwd(const uint16_t* __restrict__ x,
+                                                                 const uint16_t* __restrict__ W,
+                                                                 uint16_t* __restrict__ proj,
+                                                                 float* __restrict__ inv_rms, const PremapTile pt,
+                                                                 int64_t T) {
+  static_assert(KS % 4 == 0 && KR <= KS, "k-steps come in groups of four streams");
+  constexpr int HPS = KS / 4;      // k-steps per stream
+  constexpr int CPW = 32 * HPS;    // columns per wave and stream
+  constexpr int C = CPW * NW;
+  constexpr int NC = 4 * C;
+  constexpr int NT = NW * kWave;
+  __shared__ ResidentSmem<NW, KS, KR> sm;
+
+  const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+  const int row = lane & 15;
+  const int grp = lane >> 4;
+  const int cbase = wave * CPW + 8 * grp;  // the lane's column within each stream, piece 0
+
+  const int64_t nblocks = (T + 15) / 16;
+  const int64_t g0 = blockIdx.x;
+  const int64_t G = gridDim.x;
+  const int nb = g0 < nblocks ? static_cast<int>((nblocks - 1 - g0) / G + 1) : 0;
+
+  // A block is loaded in two halves of NP k-steps, each half the pieces of
+  // all four streams: k-step q = NP half + HH j + p holds piece HH half + p
+  // of stream j.  (Halves by stream, streams 0-1 then 2-3, put every CU's
+  // requests on the same 4 KiB of its rows at a time: 3.6 TB/s.)
+  constexpr int NP = KS / 2;
+  constexpr int HH = HPS / 2;  // pieces per stream in a half
+  static_assert(HPS % 2 == 0, "two halves of pieces");
+  auto col_of = [](int q) {  // offset of k-step q within a token row, past the lane's cbase
+    const int half = q / NP, j = (q % NP) / HH, p = (q % NP) % HH;
+    return j * C + 32 * (HH * half + p);
+  };
+
+  // W, loaded once: k-steps below KR stay in registers, the others go to LDS.
+  // Their loads are issued before the first blocks of x, so waiting for them
+  // does not wait for x.
+  u32x4 wr[KR > 0 ? KR : 1][2];
+  u32x4 wl[KS > KR ? KS - KR : 1][2];
+#pragma unroll
+  for (int q = 0; q < KS; ++q) {
+    const int k = cbase + col_of(q);
+    const u32x4 a = *reinterpret_cast<const u32x4*>(W + static_cast<int64_t>(row) * NC + k);
+    const u32x4 b = *reinterpret_cast<const u32x4*>(W + static_cast<int64_t>(16 + row) * NC + k);
+    if (q < KR) {
+      wr[q][0] = a;
+      wr[q][1] = b;
+    } else {
+      wl[q - KR][0] = a;
+      wl[q - KR][1] = b;
+    }
+  }
+  zero_words(pt.z);
+
+  // Half `half` of block g0 + i G: tail rows re-read the last token (not
+  // stored).  Blocks past the workgroup's last re-read that one: prefetches
+  // are issued unconditionally, so that every path reaches a step with the
+  // same loads in flight and the compiler's in-order wait counts stay exact
+  // (with a conditional prefetch the wait for a block also waited for the
+  // next one's loads).
+  auto load_half = [&](u32x4 (&X)[NP], int i, int half) __attribute__((always_inline)) {
+    const int ic = i < nb ? i : nb - 1;
+    const int64_t t0 = (g0 + static_cast<int64_t>(ic) * G) * 16;
+    const int64_t t = t0 + row < T ? t0 + row : T - 1;
+    const uint16_t* base = x + t * NC + cbase;
+#pragma unroll
+    for (int q = 0; q < NP; ++q) X[q] = *reinterpret_cast<const u32x4*>(base + col_of(half * NP + q));
+  };
+
+  // Three half-block buffers in rotation: block i's halves are loaded one
+  // and two steps ahead, so while a block is reduced, mixed and stored about
+  // one block of loads is in flight.
+  u32x4 H0[NP], H1[NP], H2[NP];
+  __builtin_amdgcn_sched_barrier(0);  // W's loads first: waiting for them does not wait for x
+  load_half(H0, 0, 0);  // nb >= 1: the grid has at most one workgroup per block
+  load_half(H1, 0, 1);
+  __builtin_amdgcn_sched_barrier(0);
+  load_half(H2, 1, 0);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int q = KR; q < KS; ++q) {
+    sm.w[wave][q - KR][0][lane] = wl[q - KR][0];
+    sm.w[wave][q - KR][1][lane] = wl[q - KR][1];
+  }
+  stage_params<NT>(pt.P, sm.k2);  // ends with a barrier
+  {
+    const float* pf = reinterpret_cast<const float*>(sm.k2.perm);  // perm[m][r], 24 x 16
+    for (int i = threadIdx.x; i < kNF * kN * kN; i += NT) sm.permT[i % (kN * kN)][i / (kN * kN)] = pf[i];
+  }  // read after the first block's barriers
+
+  // Block i with streams 0-1 in A and streams 2-3 in B.
+  auto step = [&](u32x4 (&A)[NP], u32x4 (&B)[NP], int i) __attribute__((always_inline)) {
+    const int64_t t0 = (g0 + static_cast<int64_t>(i) * G) * 16;
+    // K1: this wave's share of the 32 projections and of the sum of squares.
+    f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0, gm = a0;
+#pragma unroll
+    for (int q = 0; q < KS; ++q) {
+      const u32x4 xq = q < NP ? A[q < NP ? q : 0] : B[q < NP ? 0 : q - NP];
+      const u32x4 wa = q < KR ? wr[q < KR ? q : 0][0] : sm.w[wave][q < KR ? 0 : q - KR][0][lane];
+      const u32x4 wb = q < KR ? wr[q < KR ? q : 0][1] : sm.w[wave][q < KR ? 0 : q - KR][1][lane];
+      a0 = mfma(wa, xq, a0);
+      a1 = mfma(wb, xq, a1);
+      gm = mfma(xq, xq, gm);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      sm.u.r.red[wave][r][lane] = a0[r];
+      sm.u.r.red[wave][4 + r][lane] = a1[r];
+    }
+    // The diagonal G[row][row] sits in lane row + 16 (row >> 2), register row & 3.
+    if (grp == (row >> 2)) sm.u.r.red_ss[wave][row] = gm[row & 3];
+    __syncthreads();
+    // Thread (r, l) adds D element r of lane l over the waves, in wave order:
+    // projection d = 4 (l >> 4) + (r & 3) + 16 (r >> 2) of token l & 15.
+#pragma unroll
+    for (int r = wave; r < 8; r += NW) {
+      float v = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) v += sm.u.r.red[w][r][lane];
+      sm.tok[lane & 15][4 * (lane >> 4) + (r & 3) + 16 * (r >> 2)] = v;
+    }
+    if (threadIdx.x < 16) {
+      float s2 = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) s2 += sm.u.r.red_ss[w][threadIdx.x];
+      sm.tok[threadIdx.x][kDk] = s2;
+    }
+    __syncthreads();
+    // K1's outputs and K2 on the block's 16 tokens at once: 16 lanes per
+    // token with four waves (token 4 wave + (lane >> 4)), 32 with eight
+    // (token 2 wave + (lane >> 5)).  Rows past T (the last block) hold
+    // re-reads of token T - 1: computed, never stored.
+    if constexpr (NW == 4) {
+      const int tt = 4 * wave + (lane >> 4);
+      const int r = lane & 15;
+      const float inv = rsqrtf(sm.tok[tt][kDk] / static_cast<float>(NC) + kRmsEps);
+      const uint16_t pj0 = f32_to_bf16(sm.tok[tt][r] * inv);
+      const uint16_t pj1 = f32_to_bf16(sm.tok[tt][16 + r] * inv);
+      sm.out.pj[tt][r] = pj0;
+      sm.out.pj[tt][16 + r] = pj1;
+      if (r == 0) sm.out.inv[tt] = inv;
+      k2_token16_lds(sm.k2, sm.permT, sm.u.x, sm.out, sm.hp[tt], tt, r, bf16_to_f32(pj0), bf16_to_f32(pj1));
+    } else {
+      static_assert(NW == 8, "four or eight waves");
+      const int tt = 2 * wave + (lane >> 5);
+      const int q = lane & 31;
+      const float inv = rsqrtf(sm.tok[tt][kDk] / static_cast<float>(NC) + kRmsEps);
+      const uint16_t pj = f32_to_bf16(sm.tok[tt][q] * inv);
+      sm.out.pj[tt][q] = pj;
+      if (q == 0) sm.out.inv[tt] = inv;
+      k2_token32_lds(sm.k2, sm.permT, sm.u.x, sm.out, sm.hp[tt], tt, q, bf16_to_f32(pj));
+    }
+    __syncthreads();
+    // The block's K1 and K2 outputs, whole 16-byte pieces of contiguous rows.
+    if (wave == 0) {  // proj: token lane >> 2, projections 8 (lane & 3) .. + 8
+      const int64_t t = t0 + (lane >> 2);
+      if (t < T)
+        *reinterpret_cast<u32x4*>(proj + t * kDk + 8 * (lane & 3)) =
+            reinterpret_cast<const u32x4*>(sm.out.pj[lane >> 2])[lane & 3];
+    } else if (wave == 1) {  // H_merged: token lane >> 2, row lane & 3
+      const int64_t t = t0 + (lane >> 2);
+      if (t < T)
+        reinterpret_cast<f32x4*>(pt.H)[t * kN + (lane & 3)] = reinterpret_cast<const f32x4*>(sm.out.H[lane >> 2])[lane & 3];
+    } else if (wave == 2) {  // h_pre (lanes 0-15), h_post (16-31), inv_rms (32-47)
+      const int64_t t = t0 + (lane & 15);
+      if (t < T) {
+        if (lane < 16)
+          reinterpret_cast<f32x4*>(pt.h_pre)[t] = *reinterpret_cast<const f32x4*>(sm.hp[lane]);
+        else if (lane < 32)
+          reinterpret_cast<f32x4*>(pt.h_post)[t] = *reinterpret_cast<const f32x4*>(sm.out.hq[lane & 15]);
+        else if (lane < 48)
+          inv_rms[t] = sm.out.inv[lane & 15];
+      }
+    }
+    // K3 on the rows still in registers, a half at a time: once a half is
+    // mixed its registers take the next loads (block i + 1's second half,
+    // then block i + 2's first half), so those are issued a half earlier.
+    const int64_t t = t0 + row;
+    const bool tv = t < T;
+    const float h0 = sm.hp[row][0], h1 = sm.hp[row][1], h2 = sm.hp[row][2], h3 = sm.hp[row][3];
+    uint16_t* orow = pt.layer_input + (tv ? t : 0) * C + cbase;
+    // Piece HH half + p of the four streams: k-steps HH j + p of that half.
+    auto mix = [&](const u32x4 (&X)[NP], int half) __attribute__((always_inline)) {
+#pragma unroll
+      for (int p = 0; p < HH; ++p) {
+        float a[8], b[8], c[8], d[8], o[8];
+        unpack8(X[p], a);
+        unpack8(X[HH + p], b);
+        unpack8(X[2 * HH + p], c);
+        unpack8(X[3 * HH + p], d);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float acc = h0 * a[e];
+          acc = __builtin_fmaf(h1, b[e], acc);
+          acc = __builtin_fmaf(h2, c[e], acc);
+          o[e] = __builtin_fmaf(h3, d[e], acc);
+        }
+        // Ordinary stores: each instruction writes half of 16 lines (64 of
+        // 128 bytes per row) and the next one the other half; L2 merges the
+        // two before writing back, where with the nontemporal hint about
+        // half the lines went out twice (WRITE_SIZE 1.44 x).
+        if (tv) *reinterpret_cast<u32x4*>(orow + 32 * (HH * half + p)) = pack8(o);
+      }
+    };
+    mix(A, 0);
+    load_half(A, i + 1, 1);
+    __builtin_amdgcn_sched_barrier(0);  // all of block i + 1 before block i + 2 (in-order wait counts)
+    mix(B, 1);
+    load_half(B, i + 2, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Block i in (H[2i % 3], H[(2i + 1) % 3]); its step reloads both halves
+  // with block i + 1's second half and block i + 2's first half.
+  for (int i = 0; i < nb; i += 3) {
+    step(H0, H1, i);
+    if (i + 1 >= nb) break;
+    step(H2, H0, i + 1);
+    if (i + 2 >= nb) break;
+    step(H1, H2, i + 2);
+  }
+}
+
+// Compute units of each device, looked up on the first launch there (a racing
+// first lookup stores the same value).
+constexpr int kMaxDevices = 64;
+int g_cus[kMaxDevices];
+
+int device_cus() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  if (g_cus[dev] <= 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    g_cus[dev] = n;
+  }
+  return g_cus[dev];
+}
+
+}  // namespace
+
+// The resident kernel for rows of C = 512 or 1024 per stream; returns false
+// (nothing launched) for other shapes, fewer than kResidentMinT tokens, no
+// layer input or misaligned pointers.
+bool premap_resident(const uint16_t* x, const uint16_t* W, uint16_t* proj, float* inv_rms, const PremapTile& pt,
+                     int64_t T, int64_t C, hipStream_t s, int* status) {
+  if (!(C == 1024 || C == 512) || T < kResidentMinT || !pt.layer_input || !aligned16(x) || !aligned16(W) ||
+      !aligned16(pt.layer_input) || !aligned16(proj) || !aligned16(pt.h_pre) || !aligned16(pt.h_post) ||
+      !aligned16(pt.H))
+    return false;
+  const int cus = device_cus();
+  if (cus <= 0) return false;
+  const int64_t nblocks = (T + 15) / 16;
+  const unsigned grid = static_cast<unsigned>(nblocks < cus ? nblocks : cus);
+  if (C == 1024)
+    premap_resident_fwd<4, 32, 16><<<grid, 4 * kWave, 0, s>>>(x, W, proj, inv_rms, pt, T);
+  else
+    premap_resident_fwd<4, 16, 0><<<grid, 4 * kWave, 0, s>>>(x, W, proj, inv_rms, pt, T);
+  *status = launch_status();
+  return true;
+}
+
+}  // namespace fmhc

@@ -32,7 +32,7 @@ LIB_NAME = "libflash_mhc_hip.so"
 LIB_PATH = LIB_DIR / LIB_NAME
 PROBE_LIB_PATH = LIB_DIR / "libflash_mhc_probe.so"
 
-SOURCES = ("k1.hip", "k2.hip", "k3.hip", "k4.hip", "premap.hip", "abi.hip")
+SOURCES = ("k1.hip", "k2.hip", "k3.hip", "k4.hip", "premap.hip", "premap_resident.hip", "abi.hip")
 PROBE_SOURCES = ("stream_probe.hip",)
 
 ARCH = "gfx950"
@@ -54,7 +54,8 @@ COMMON_FLAGS = [
 # (gfx950 allows VGPR srcC/dst).  Without it the compiler keeps the backward's
 # loop-carried weight-gradient accumulators in VGPRs and copies them to and
 # from AGPRs around every MFMA, which doubles the kernel's register footprint.
-SOURCE_FLAGS = {"k1.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+SOURCE_FLAGS = {"k1.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+                "premap_resident.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 # Evidence builds of the same library, selected at compile time.  k1_valu: the
 # K1 forward and backward-dx contractions as fp32 FMAs on the VALU instead of
@@ -65,7 +66,7 @@ SOURCE_FLAGS = {"k1.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 # with nontemporal loads of x in its K1 part, so that its K3 part re-reads the
 # tile from HBM instead of the memory-side cache.
 VARIANTS = {"k1_valu": ["-DFMHC_K1_VALU=1"], "premap_three_kernels": ["-DFMHC_PREMAP_TILE=0"],
-            "premap_tile_nt": ["-DFMHC_PREMAP_TILE_NT=1"]}
+            "premap_tile_nt": ["-DFMHC_PREMAP_TILE_NT=1"], "premap_reread": ["-DFMHC_PREMAP_RESIDENT=0"]}
 
 
 def variant_path(name: str) -> Path:
@@ -130,14 +131,23 @@ def build(verbose: bool = False, extra_flags: list[str] | None = None, out: Path
     return out
 
 
+def build_variants(verbose: bool = False) -> list[Path]:
+    """Every evidence variant (nothing on the product path loads them; their
+    GPU tests skip when they are absent)."""
+    return [build(verbose=verbose, extra_flags=flags, out=variant_path(name), probe=False)
+            for name, flags in VARIANTS.items()]
+
+
 def build_all(verbose: bool = False) -> Path:
     """The product library, the probe library and every evidence variant."""
     path = build(verbose=verbose)
-    for name, flags in VARIANTS.items():
-        build(verbose=verbose, extra_flags=flags, out=variant_path(name), probe=False)
+    build_variants(verbose=verbose)
     return path
 
 
 if __name__ == "__main__":
-    path = build_all(verbose="-v" in sys.argv)
+    # python -m flash_mhc.build [-v] [--variants]: the product and probe
+    # libraries, and with --variants the evidence builds too.
+    verbose = "-v" in sys.argv
+    path = build_all(verbose=verbose) if "--variants" in sys.argv else build(verbose=verbose)
     print(path)

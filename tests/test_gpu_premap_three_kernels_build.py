@@ -25,7 +25,8 @@ DEV = "cuda"
 def three_lib(request):
     _abi.load()
     path = build.variant_path(request.param)
-    assert path.exists(), f"build the evidence variant first: {path}"
+    if not path.exists():
+        pytest.skip(f"evidence build not present: {path} (python -m flash_mhc.build --variants)")
     lib = ctypes.CDLL(str(path), mode=ctypes.RTLD_LOCAL)
     for name, argtypes in _abi.SIGNATURES.items():
         fn = getattr(lib, name)
@@ -51,9 +52,13 @@ def _run(lib, x, W, params, T, C, with_li):
     return out
 
 
+# Rows of C = 512 or 1024 with a layer input and at least 32768 tokens take the
+# single-read kernel instead (tests/test_gpu_premap_resident.py); the
+# metric-size tile kernel is covered here without the layer input and at
+# C = 2048, and against the three kernels in the premap_reread build there.
 @pytest.mark.parametrize("T,C,with_li", [(3000, 1024, True), (5000, 512, True), (7000, 1024, False),
                                          (16384, 1024, True), (16417, 1024, True), (20000, 256, True),
-                                         (16400, 4096, False), (65536, 1024, True)])
+                                         (16400, 4096, False), (65536, 1024, False), (32768, 2048, True)])
 def test_tile_kernel_equals_three_kernels(three_lib, T, C, with_li):
     g = torch.Generator().manual_seed(T + C)
     x = torch.randn(T, 4, C, generator=g).to(torch.bfloat16)
