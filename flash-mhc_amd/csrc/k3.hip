@@ -16,21 +16,29 @@
 //   * the backward's four reductions over C finish with an in-wave butterfly
 //     and, when a token spans several waves, an LDS sum over them in wave
 //     order (no atomics), so grad_h_pre is deterministic.
+#include <type_traits>
+
 #include "fmhc_common.h"
 
 namespace fmhc {
 
 namespace {
 
-constexpr int kBlock = 256;  // 4 waves per workgroup
+constexpr int kBlock = 256;  // 4 waves per workgroup, or one token's LPT lanes when more
+
+// Threads per workgroup for LPT lanes per token.
+template <int LPT>
+constexpr int block_of() {
+  return LPT > kBlock ? LPT : kBlock;
+}
 
 // LPT <= 64: 64 / LPT tokens per wave.  LPT = 128 or 256: LPT / 64 waves per
-// token.
+// token; LPT a multiple of 64 above 256: one token per workgroup.
 template <int LPT>
 __device__ __forceinline__ int64_t token_of_lane(int lane) {
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
   if constexpr (LPT > kWave) {
-    return static_cast<int64_t>(blockIdx.x) * (kBlock / LPT) + wave / (LPT / kWave);
+    return static_cast<int64_t>(blockIdx.x) * (block_of<LPT>() / LPT) + wave / (LPT / kWave);
   } else {
     constexpr int TPW = kWave / LPT;
     const int64_t first = (static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) + wave) * TPW;
@@ -45,7 +53,7 @@ __device__ __forceinline__ int sub_of_lane() {
 }
 
 template <int VEC, int LPT>
-__global__ __launch_bounds__(kBlock) void k3_fwd_kernel(const uint16_t* __restrict__ x,
+__global__ __launch_bounds__(block_of<LPT>()) void k3_fwd_kernel(const uint16_t* __restrict__ x,
                                                         const float* __restrict__ h_pre,
                                                         uint16_t* __restrict__ out,
                                                         int64_t T, int C) {
@@ -61,7 +69,7 @@ __global__ __launch_bounds__(kBlock) void k3_fwd_kernel(const uint16_t* __restri
 // GX = false: grad_h_pre only (the pre-map backward adds h_pre * go into K1's
 // grad_x store instead of writing it here).
 template <int VEC, int LPT, bool GX>
-__global__ __launch_bounds__(kBlock) void k3_bwd_kernel(const uint16_t* __restrict__ x,
+__global__ __launch_bounds__(block_of<LPT>()) void k3_bwd_kernel(const uint16_t* __restrict__ x,
                                                         const float* __restrict__ h_pre,
                                                         const uint16_t* __restrict__ go,
                                                         uint16_t* __restrict__ grad_x,
@@ -130,7 +138,7 @@ __global__ __launch_bounds__(kBlock) void k3_bwd_kernel(const uint16_t* __restri
   s3 = group_sum<GS>(s3);
   if constexpr (WPT > 1) {
     // The token's waves add their sums in wave order (deterministic).
-    __shared__ float red[kBlock / kWave][4];
+    __shared__ float red[block_of<LPT>() / kWave][4];
     const int wave = static_cast<int>(threadIdx.x) >> 6;
     if (lane == 0) {
       red[wave][0] = s0;
@@ -171,6 +179,50 @@ int pick_lpt(int C) {
   return 8;
 }
 
+// Widest layout (16-byte path): a workgroup of exactly one 8-element group
+// per lane and stream when a row's groups (a multiple of 64, from 320 to
+// kMaxLpt) do not split evenly over 256 lanes: C = 2560, 3072, 3584.  With
+// 256 lanes at C = 2560 (320 groups) a quarter of the lanes took a second
+// group while the rest waited; 320 lanes took the six-kernel step at
+// T = 65536 from 5677 to 6054 GB/s (K4 backward 5378 -> 6307).  C = 4096
+// (512 groups, two per lane at 256) measured the same at 512 and 256 lanes
+// (T = 65536 and 262144, within 2%) and keeps 256.
+#ifndef FMHC_K34_MAX_LPT
+#define FMHC_K34_MAX_LPT 512
+#endif
+constexpr int kMaxLpt = FMHC_K34_MAX_LPT;
+
+template <int VEC>
+int wide_lpt(int groups) {
+  if constexpr (VEC == 8) {
+    if (groups % kWave == 0 && groups % 256 != 0 && groups > 256 && groups <= kMaxLpt) return groups;
+  }
+  return 256;
+}
+
+// f(std::integral_constant<int, L>{}) for the lanes per token L the kernels
+// are built for; threads per workgroup block_of<L>().
+template <typename F>
+void with_lpt(int lpt, F&& f) {
+  switch (lpt) {
+    case 512: f(std::integral_constant<int, 512>{}); break;
+    case 448: f(std::integral_constant<int, 448>{}); break;
+    case 384: f(std::integral_constant<int, 384>{}); break;
+    case 320: f(std::integral_constant<int, 320>{}); break;
+    case 256: f(std::integral_constant<int, 256>{}); break;
+    case 128: f(std::integral_constant<int, 128>{}); break;
+    case 64: f(std::integral_constant<int, 64>{}); break;
+    case 32: f(std::integral_constant<int, 32>{}); break;
+    case 16: f(std::integral_constant<int, 16>{}); break;
+    default: f(std::integral_constant<int, 8>{}); break;
+  }
+}
+
+// Tokens per workgroup with lpt lanes per token.
+int64_t tokens_per_block(int lpt) {
+  return lpt > kWave ? (lpt > kBlock ? 1 : kBlock / lpt) : (kBlock / kWave) * (kWave / lpt);
+}
+
 // The forward kernel spreads a token over more lanes (up to a workgroup),
 // so that each lane has one or two 8-element groups per stream instead of a
 // loop over them.  Measured at T x C = 64 Mi elements: with 256 lanes per
@@ -181,7 +233,7 @@ template <int VEC>
 int pick_lpt_fwd(int C, int64_t T) {
   const int lpt = pick_lpt<VEC>(C);
   const int groups = C / VEC;
-  if (groups >= 256) return 256;
+  if (groups >= 256) return wide_lpt<VEC>(groups);
   if (groups >= 128) return T * lpt < int64_t{256} * kBlock ? 128 : lpt;
   return lpt;
 }
@@ -190,16 +242,11 @@ template <int VEC>
 int launch_k3_fwd(const uint16_t* x, const float* h_pre, uint16_t* out, int64_t T, int C,
                   hipStream_t s) {
   const int lpt = pick_lpt_fwd<VEC>(C, T);
-  const int64_t tokens_per_block = lpt > kWave ? kBlock / lpt : (kBlock / kWave) * (kWave / lpt);
-  const dim3 grid(blocks_for(T, tokens_per_block));
-  switch (lpt) {
-    case 256: k3_fwd_kernel<VEC, 256><<<grid, kBlock, 0, s>>>(x, h_pre, out, T, C); break;
-    case 128: k3_fwd_kernel<VEC, 128><<<grid, kBlock, 0, s>>>(x, h_pre, out, T, C); break;
-    case 64: k3_fwd_kernel<VEC, 64><<<grid, kBlock, 0, s>>>(x, h_pre, out, T, C); break;
-    case 32: k3_fwd_kernel<VEC, 32><<<grid, kBlock, 0, s>>>(x, h_pre, out, T, C); break;
-    case 16: k3_fwd_kernel<VEC, 16><<<grid, kBlock, 0, s>>>(x, h_pre, out, T, C); break;
-    default: k3_fwd_kernel<VEC, 8><<<grid, kBlock, 0, s>>>(x, h_pre, out, T, C); break;
-  }
+  const dim3 grid(blocks_for(T, tokens_per_block(lpt)));
+  with_lpt(lpt, [&](auto l) {
+    constexpr int L = decltype(l)::value;
+    k3_fwd_kernel<VEC, L><<<grid, block_of<L>(), 0, s>>>(x, h_pre, out, T, C);
+  });
   return launch_status();
 }
 
@@ -209,22 +256,18 @@ int launch_k3_fwd(const uint16_t* x, const float* h_pre, uint16_t* out, int64_t 
 // 16% slower than one, which stays the choice below C = 2048.
 template <int VEC>
 int pick_lpt_bwd(int C) {
-  return C / VEC >= 256 ? 256 : pick_lpt<VEC>(C);
+  return C / VEC >= 256 ? wide_lpt<VEC>(C / VEC) : pick_lpt<VEC>(C);
 }
 
 template <int VEC, bool GX>
 int launch_k3_bwd(const uint16_t* x, const float* h_pre, const uint16_t* go, uint16_t* grad_x,
                   float* grad_h_pre, int64_t T, int C, hipStream_t s) {
   const int lpt = pick_lpt_bwd<VEC>(C);
-  const int64_t tokens_per_block = lpt > kWave ? kBlock / lpt : (kBlock / kWave) * (kWave / lpt);
-  const dim3 grid(blocks_for(T, tokens_per_block));
-  switch (lpt) {
-    case 256: k3_bwd_kernel<VEC, 256, GX><<<grid, kBlock, 0, s>>>(x, h_pre, go, grad_x, grad_h_pre, T, C); break;
-    case 64: k3_bwd_kernel<VEC, 64, GX><<<grid, kBlock, 0, s>>>(x, h_pre, go, grad_x, grad_h_pre, T, C); break;
-    case 32: k3_bwd_kernel<VEC, 32, GX><<<grid, kBlock, 0, s>>>(x, h_pre, go, grad_x, grad_h_pre, T, C); break;
-    case 16: k3_bwd_kernel<VEC, 16, GX><<<grid, kBlock, 0, s>>>(x, h_pre, go, grad_x, grad_h_pre, T, C); break;
-    default: k3_bwd_kernel<VEC, 8, GX><<<grid, kBlock, 0, s>>>(x, h_pre, go, grad_x, grad_h_pre, T, C); break;
-  }
+  const dim3 grid(blocks_for(T, tokens_per_block(lpt)));
+  with_lpt(lpt, [&](auto l) {
+    constexpr int L = decltype(l)::value;
+    k3_bwd_kernel<VEC, L, GX><<<grid, block_of<L>(), 0, s>>>(x, h_pre, go, grad_x, grad_h_pre, T, C);
+  });
   return launch_status();
 }
 

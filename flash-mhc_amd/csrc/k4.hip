@@ -22,15 +22,21 @@ namespace fmhc {
 
 namespace {
 
-constexpr int kBlock = 256;  // 4 waves per workgroup
+constexpr int kBlock = 256;  // 4 waves per workgroup, or one token's LPT lanes when more
+
+// Threads per workgroup for LPT lanes per token.
+template <int LPT>
+constexpr int block_of() {
+  return LPT > kBlock ? LPT : kBlock;
+}
 
 // LPT <= 64: 64 / LPT tokens per wave.  LPT = 128 or 256: LPT / 64 waves per
-// token.
+// token; LPT a multiple of 64 above 256: one token per workgroup.
 template <int LPT>
 __device__ __forceinline__ int64_t token_of_lane(int lane) {
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
   if constexpr (LPT > kWave) {
-    return static_cast<int64_t>(blockIdx.x) * (kBlock / LPT) + wave / (LPT / kWave);
+    return static_cast<int64_t>(blockIdx.x) * (block_of<LPT>() / LPT) + wave / (LPT / kWave);
   } else {
     constexpr int TPW = kWave / LPT;
     const int64_t first = (static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) + wave) * TPW;
@@ -45,7 +51,7 @@ __device__ __forceinline__ int sub_of_lane() {
 }
 
 template <int VEC, int LPT>
-__global__ __launch_bounds__(kBlock) void k4_fwd_kernel(const uint16_t* __restrict__ x,
+__global__ __launch_bounds__(block_of<LPT>()) void k4_fwd_kernel(const uint16_t* __restrict__ x,
                                                         const uint16_t* __restrict__ lo,
                                                         const float* __restrict__ H,
                                                         const float* __restrict__ h_post,
@@ -101,7 +107,7 @@ __global__ __launch_bounds__(kBlock) void k4_fwd_kernel(const uint16_t* __restri
 }
 
 template <int VEC, int LPT, bool EARLY>
-__global__ __launch_bounds__(kBlock) void k4_bwd_kernel(const uint16_t* __restrict__ x,
+__global__ __launch_bounds__(block_of<LPT>()) void k4_bwd_kernel(const uint16_t* __restrict__ x,
                                                         const uint16_t* __restrict__ lo,
                                                         const float* __restrict__ H,
                                                         const float* __restrict__ h_post,
@@ -221,7 +227,7 @@ __global__ __launch_bounds__(kBlock) void k4_bwd_kernel(const uint16_t* __restri
   }
   if constexpr (WPT > 1) {
     // The token's waves add their 20 sums in wave order (deterministic).
-    __shared__ float red[kBlock / kWave][20];
+    __shared__ float red[block_of<LPT>() / kWave][20];
     const int wave = static_cast<int>(threadIdx.x) >> 6;
     if (lane == 0) {
 #pragma unroll
@@ -271,6 +277,50 @@ int pick_lpt(int C) {
   return 8;
 }
 
+// Widest layout (16-byte path): a workgroup of exactly one 8-element group
+// per lane and stream when a row's groups (a multiple of 64, from 320 to
+// kMaxLpt) do not split evenly over 256 lanes: C = 2560, 3072, 3584.  With
+// 256 lanes at C = 2560 (320 groups) a quarter of the lanes took a second
+// group while the rest waited; 320 lanes took the six-kernel step at
+// T = 65536 from 5677 to 6054 GB/s (K4 backward 5378 -> 6307).  C = 4096
+// (512 groups, two per lane at 256) measured the same at 512 and 256 lanes
+// (T = 65536 and 262144, within 2%) and keeps 256.
+#ifndef FMHC_K34_MAX_LPT
+#define FMHC_K34_MAX_LPT 512
+#endif
+constexpr int kMaxLpt = FMHC_K34_MAX_LPT;
+
+template <int VEC>
+int wide_lpt(int groups) {
+  if constexpr (VEC == 8) {
+    if (groups % kWave == 0 && groups % 256 != 0 && groups > 256 && groups <= kMaxLpt) return groups;
+  }
+  return 256;
+}
+
+// f(std::integral_constant<int, L>{}) for the lanes per token L the kernels
+// are built for; threads per workgroup block_of<L>().
+template <typename F>
+void with_lpt(int lpt, F&& f) {
+  switch (lpt) {
+    case 512: f(std::integral_constant<int, 512>{}); break;
+    case 448: f(std::integral_constant<int, 448>{}); break;
+    case 384: f(std::integral_constant<int, 384>{}); break;
+    case 320: f(std::integral_constant<int, 320>{}); break;
+    case 256: f(std::integral_constant<int, 256>{}); break;
+    case 128: f(std::integral_constant<int, 128>{}); break;
+    case 64: f(std::integral_constant<int, 64>{}); break;
+    case 32: f(std::integral_constant<int, 32>{}); break;
+    case 16: f(std::integral_constant<int, 16>{}); break;
+    default: f(std::integral_constant<int, 8>{}); break;
+  }
+}
+
+// Tokens per workgroup with lpt lanes per token.
+int64_t tokens_per_block(int lpt) {
+  return lpt > kWave ? (lpt > kBlock ? 1 : kBlock / lpt) : (kBlock / kWave) * (kWave / lpt);
+}
+
 // The forward kernel spreads a token over more lanes (up to a workgroup),
 // so that each lane has one or two 8-element groups per stream instead of a
 // loop over them.  Measured at T x C = 64 Mi elements: with 256 lanes per
@@ -280,7 +330,7 @@ int pick_lpt(int C) {
 template <int VEC>
 int pick_lpt_fwd(int C) {
   const int groups = C / VEC;
-  if (groups >= 256) return 256;
+  if (groups >= 256) return wide_lpt<VEC>(groups);
   if (groups >= 128) return 128;
   return pick_lpt<VEC>(C);
 }
@@ -291,23 +341,18 @@ int pick_lpt_fwd(int C) {
 // under 1%, so one wave stays the choice below C = 2048.
 template <int VEC>
 int pick_lpt_bwd(int C) {
-  return C / VEC >= 256 ? 256 : pick_lpt<VEC>(C);
+  return C / VEC >= 256 ? wide_lpt<VEC>(C / VEC) : pick_lpt<VEC>(C);
 }
 
 template <int VEC>
 int launch_k4_fwd(const uint16_t* x, const uint16_t* lo, const float* H, const float* hp,
                   uint16_t* out, int64_t T, int C, hipStream_t s) {
   const int lpt = pick_lpt_fwd<VEC>(C);
-  const int64_t tokens_per_block = lpt > kWave ? kBlock / lpt : (kBlock / kWave) * (kWave / lpt);
-  const dim3 grid(blocks_for(T, tokens_per_block));
-  switch (lpt) {
-    case 256: k4_fwd_kernel<VEC, 256><<<grid, kBlock, 0, s>>>(x, lo, H, hp, out, T, C); break;
-    case 128: k4_fwd_kernel<VEC, 128><<<grid, kBlock, 0, s>>>(x, lo, H, hp, out, T, C); break;
-    case 64: k4_fwd_kernel<VEC, 64><<<grid, kBlock, 0, s>>>(x, lo, H, hp, out, T, C); break;
-    case 32: k4_fwd_kernel<VEC, 32><<<grid, kBlock, 0, s>>>(x, lo, H, hp, out, T, C); break;
-    case 16: k4_fwd_kernel<VEC, 16><<<grid, kBlock, 0, s>>>(x, lo, H, hp, out, T, C); break;
-    default: k4_fwd_kernel<VEC, 8><<<grid, kBlock, 0, s>>>(x, lo, H, hp, out, T, C); break;
-  }
+  const dim3 grid(blocks_for(T, tokens_per_block(lpt)));
+  with_lpt(lpt, [&](auto l) {
+    constexpr int L = decltype(l)::value;
+    k4_fwd_kernel<VEC, L><<<grid, block_of<L>(), 0, s>>>(x, lo, H, hp, out, T, C);
+  });
   return launch_status();
 }
 
@@ -318,8 +363,7 @@ int launch_k4_bwd(const uint16_t* x, const uint16_t* lo, const float* H, const f
                   const uint16_t* go, uint16_t* gx, uint16_t* glo, float* gH, float* ghp,
                   int64_t T, int C, hipStream_t s) {
   const int lpt = pick_lpt_bwd<VEC>(C);
-  const int64_t tokens_per_block = lpt > kWave ? kBlock / lpt : (kBlock / kWave) * (kWave / lpt);
-  const dim3 grid(blocks_for(T, tokens_per_block));
+  const dim3 grid(blocks_for(T, tokens_per_block(lpt)));
   // Few waves (up to 64 per CU): each iteration's loads go out before its
   // stores, so a wave waits for one round trip per iteration instead of five
   // (block step at C = 1024, HIP graph: T = 1024 96.5 -> 94.6 us, 6000 232.2
@@ -329,14 +373,11 @@ int launch_k4_bwd(const uint16_t* x, const uint16_t* lo, const float* H, const f
   // 65536 302.2 -> 304.3 us).
   auto launch = [&](auto early) {
     constexpr bool E = decltype(early)::value;
-    switch (lpt) {
-      case 256: k4_bwd_kernel<VEC, 256, E><<<grid, kBlock, 0, s>>>(x, lo, H, hp, go, gx, glo, gH, ghp, T, C); break;
-      case 128: k4_bwd_kernel<VEC, 128, E><<<grid, kBlock, 0, s>>>(x, lo, H, hp, go, gx, glo, gH, ghp, T, C); break;
-      case 64: k4_bwd_kernel<VEC, 64, E><<<grid, kBlock, 0, s>>>(x, lo, H, hp, go, gx, glo, gH, ghp, T, C); break;
-      case 32: k4_bwd_kernel<VEC, 32, false><<<grid, kBlock, 0, s>>>(x, lo, H, hp, go, gx, glo, gH, ghp, T, C); break;
-      case 16: k4_bwd_kernel<VEC, 16, false><<<grid, kBlock, 0, s>>>(x, lo, H, hp, go, gx, glo, gH, ghp, T, C); break;
-      default: k4_bwd_kernel<VEC, 8, false><<<grid, kBlock, 0, s>>>(x, lo, H, hp, go, gx, glo, gH, ghp, T, C); break;
-    }
+    with_lpt(lpt, [&](auto l) {
+      constexpr int L = decltype(l)::value;
+      k4_bwd_kernel<VEC, L, E && L >= kWave><<<grid, block_of<L>(), 0, s>>>(x, lo, H, hp, go, gx, glo, gH, ghp, T,
+                                                                            C);
+    });
   };
   // Measured on the 16-byte path with a wave or more per token; narrower
   // tokens (C < 512) keep the loop as it is.

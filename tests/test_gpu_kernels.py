@@ -52,9 +52,11 @@ def misaligned(t: torch.Tensor) -> torch.Tensor:
 # vector paths (K1: nC % 64 != 0; K3/K4: C/8 not a multiple of the lanes per
 # token); C=25 forces the element-wise paths (C % 8 != 0, nC % 8 != 0).  C=300
 # and 2050 run the element-wise K3/K4 paths with a workgroup per token (256
-# lanes, the per-token sums finished across waves).
+# lanes, the per-token sums finished across waves).  C=2560, 3072 and 3584 run
+# the 16-byte K3/K4 paths with a workgroup of one group per lane (320, 384 and
+# 448 lanes: five to seven waves).
 SHAPES = [(2048, 256), (257, 1024), (1, 4096), (64, 4096), (333, 100), (129, 1000), (31, 24), (17, 25),
-          (7, 300), (5, 2050)]
+          (7, 300), (5, 2050), (33, 2560), (9, 3072), (5, 3584)]
 
 
 # ---------------------------------------------------------------------------
@@ -332,13 +334,15 @@ def test_k4_misaligned():
 
 
 # ---------------------------------------------------------------------------
-# Metric size T=65536, n=4, C=1024: all six kernels, checked on 512 sampled
-# tokens (each kernel is independent per token, so the oracle runs on the
-# sampled rows only).
+# Metric size T=65536, n=4, C=1024, and the same T at C=2560 (K3/K4 with 320
+# lanes per token): all six kernels, checked on 512 sampled tokens (each
+# kernel is independent per token, so the oracle runs on the sampled rows
+# only).
 
 
-def test_metric_size_sampled():
-    T, C = 65536, 1024
+@pytest.mark.parametrize("C", [1024, 2560])
+def test_metric_size_sampled(C):
+    T = 65536
     nC = 4 * C
     g = torch.Generator().manual_seed(1234)
     idx = torch.randperm(T, generator=g)[:512]
