@@ -41,9 +41,11 @@ bool k1_premap_tile(const uint16_t* x, const uint16_t* W, uint16_t* proj, float*
 // stream (premap_resident.hip): W resident on each CU, a 16-token block of
 // rows in registers from K1 to K3.  Returns false (nothing launched) when the
 // shape, token count (below kResidentMinT), layer input or alignment does not
-// allow it.  Against the tile kernel at C = 1024 (cold): T = 16384 51.9
-// against 49.9 us, 32768 89.9 against 89.8, 65536 159 against 174, 131072 296
-// against 331.
+// allow it.  Against the tile kernel, each launch after a cache flush:
+// C = 1024, T = 32768 84.9 against 91.2 us, 65536 151 against 174, 131072
+// 281 against 335; C = 512, T = 32768 48.9 against 49.7, 65536 83.8 against
+// 93.6.  At T = 16384 (C = 1024) an earlier form of it lost, 51.9 against
+// 49.9 us: too few blocks per CU to pay for loading W.
 constexpr int64_t kResidentMinT = 32768;
 bool premap_resident(const uint16_t* x, const uint16_t* W, uint16_t* proj, float* inv_rms, const PremapTile& pt,
                      int64_t T, int64_t C, hipStream_t s, int* status);

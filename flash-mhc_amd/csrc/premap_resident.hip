@@ -35,9 +35,11 @@
 // values of K1 -> K2 -> K3 up to K1's fp32 summation order (this kernel
 // partitions the contraction over four waves of C columns each).
 //
-// Measured at T = 65536 (cold caches): C = 1024 159 us against 174 us for the
-// tile kernel that re-reads x, C = 512 90 against 93 us; T = 131072, C = 1024:
-// 296 against 331 us.  The memory floor of the same loads and stores without
+// Measured at T = 65536 (each launch after a cache flush): C = 1024 149 us
+// against 174 us for the tile kernel that re-reads x and 205 us for three
+// kernels, 1.04x the region's algorithmic bytes past L2 against 1.74x;
+// C = 512 86 against 94 us; T = 131072, C = 1024: 283 against 331 us.
+// The memory floor of the same loads and stores without
 // any arithmetic is 121-124 us at C = 1024: W (256 KiB) and one and a half
 // blocks of rows (192 KiB) fill the CU's registers and LDS, so the second
 // half of each block is issued only once the previous block is mixed, and
