@@ -183,6 +183,61 @@ __device__ __forceinline__ float rows_sum(float v) {
   return __uint_as_float(h[0]) + __uint_as_float(h[1]);
 }
 
+// Sum over each 16-lane row, every lane of the row receiving the total: the
+// butterfly lanes 1, 2, 4, 8 apart.  Quad permutations pair lane ^ 1 and
+// lane ^ 2; the half-row mirror (lane j with 7 - j within each 8) then pairs
+// the same values as lane ^ 4, since every quad holds one value by then, and
+// the row mirror (j with 15 - j) those of lane ^ 8.  All 16 lanes of a row
+// must be active.
+__device__ __forceinline__ float row16_sum(float v) {
+  // DPP controls: quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror.
+  v += __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0xb1, 0xf, 0xf, false));
+  v += __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0x4e, 0xf, 0xf, false));
+  v += __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0x141, 0xf, 0xf, false));
+  v += __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0x140, 0xf, 0xf, false));
+  return v;
+}
+
+// Slice order of the per-token stream sums s_j = sum_c x[t, j, c] g[t, c]
+// (K3's grad_h_pre) for rows with C a multiple of 128, shared by every kernel
+// that produces them, so that each gives the same bits however it splits a
+// row: each 8-element group's products as an FMA chain from zero, row16_sum
+// over the 16 groups of each 128-column slice, then the C / 128 slice sums
+// added in slice order (the first one taken as is).
+constexpr int kSliceCols = 128;
+constexpr int kMaxSlices = 64;  // C up to 8192 per stream
+constexpr int kCanonRounds = 4;  // 16-byte groups per lane
+
+// The slice order applies to a K3-backward layout of lpt lanes per token with
+// 16-byte groups: C a multiple of 128, at most kMaxSlices slices, at least 16
+// lanes per token and at most kCanonRounds groups per lane.
+inline bool k3_canon(int64_t C, int lpt) {
+  return C % kSliceCols == 0 && C / kSliceCols <= kMaxSlices && lpt >= 16 && C / 8 <= int64_t{kCanonRounds} * lpt;
+}
+
+// One round of a token held by LPT aligned lanes (16 <= LPT <= 64) whose lane
+// sub holds group sub + k LPT of the row: e[j] is that group's FMA chain
+// (zero past the row).  Adds slices k LPT / 16 ... of the round to s[j], in
+// slice order; ns = C / 128.  Every lane of the token must be active.
+template <int LPT>
+__device__ __forceinline__ void slice_sums_add(float (&e)[4], float (&s)[4], int k, int ns, int lane) {
+  static_assert(LPT >= 16 && LPT <= 64, "rows of 16 lanes within one wave");
+#pragma unroll
+  for (int j = 0; j < 4; ++j) e[j] = row16_sum(e[j]);
+  const int tb = lane & ~(LPT - 1);
+#pragma unroll
+  for (int r = 0; r < LPT / 16; ++r) {
+    const int sigma = k * (LPT / 16) + r;
+    if (sigma < ns) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float p = __shfl(e[j], tb + 16 * r, kWave);
+        s[j] = sigma == 0 ? p : s[j] + p;
+      }
+    }
+  }
+}
+
 // Sum over the LPT consecutive lanes that share one token (LPT a power of
 // two <= 64): a butterfly, lanes LPT / 2 apart first.  Every lane of the
 // group receives the total.  LPT = 64 runs wave_sum (same bits) and needs

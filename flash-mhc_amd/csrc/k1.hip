@@ -1214,7 +1214,20 @@ extern "C" int fmhc_k1_bwd_dx(const uint16_t* x_flat, const uint16_t* W, const u
 namespace fmhc {
 namespace {
 // Runs with grad_W fused.
-int64_t k1_bwd_runs(int64_t T, int64_t nC) { return k1_bwd_nruns(T, nC, kBwdDwNTB, kBwdDwMinNTB); }
+// Runs of the backward with grad_W.  Beyond one run per wave slot the count
+// is rounded up to a multiple of kBwdFillWaves / nslices, the run groups the
+// pre-map backward's split kernel walks side by side (premap_split.hip), so
+// that each group takes the same number of runs; it shares these runs, and so
+// grad_W's partial sums, with this kernel.
+int64_t k1_bwd_runs(int64_t T, int64_t nC) {
+  const int64_t n = k1_bwd_nruns(T, nC, kBwdDwNTB, kBwdDwMinNTB);
+  const int64_t nslices = (nC + 127) / 128;
+  const int64_t fill = kBwdFillWaves / nslices > 1 ? kBwdFillWaves / nslices : 1;
+  const int64_t nblocks = (T + 15) / 16;
+  if (n <= fill) return n;
+  const int64_t r = (n + fill - 1) / fill * fill;
+  return r < nblocks ? r : nblocks;
+}
 }  // namespace
 }  // namespace fmhc
 
@@ -1288,6 +1301,17 @@ int k1_fwd_partials(const uint16_t* x_flat, const uint16_t* W, void* ws, int64_t
   return st == FMHC_OK ? p.S : -st;
 }
 
+int64_t k1_bwd_dw_runs(int64_t T, int64_t nC) { return k1_bwd_runs(T, nC); }
+
+int k1_dw_finish(const float* partial, uint16_t* grad_W, int64_t nruns, int nslices, int nC,
+                 const K2ParamSums& sums, hipStream_t s) {
+  const int64_t per_part = static_cast<int64_t>(nslices) * (8 * 2 * 4 * kWave);
+  const unsigned nb = blocks_for(per_part / 4, 256);
+  constexpr unsigned k2_blocks = (kNPar + 3) / 4;  // one wave per K2 parameter
+  k1_dw_reduce<<<dim3(nb + k2_blocks), 256, 0, s>>>(partial, grad_W, nruns, nslices, nC, nb, sums);
+  return launch_status();
+}
+
 // K1 backward of the pre-map region (premap.hip): grad_W as fmhc_k1_bwd and
 // grad_x = bf16(bf16(h_pre[t, j] go3[t, c]) + bf16(dx)).  On the MFMA path the
 // K3 term is computed in the store; otherwise grad_x must already hold it
@@ -1322,11 +1346,7 @@ int k1_bwd_premap(const uint16_t* x_flat, const uint16_t* W, const uint16_t* gra
                                      nruns, go3, h_pre, static_cast<int>(C));
     const int st = launch_status();
     if (st != FMHC_OK) return st;
-    const int64_t per_part = static_cast<int64_t>(nslices) * (8 * 2 * 4 * kWave);
-    const unsigned nb = blocks_for(per_part / 4, 256);
-    constexpr unsigned k2_blocks = (kNPar + 3) / 4;  // one wave per K2 parameter
-    k1_dw_reduce<<<dim3(nb + k2_blocks), 256, 0, s>>>(partial, grad_W, nruns, nslices, nc, nb, k2_sums);
-    return launch_status();
+    return k1_dw_finish(partial, grad_W, nruns, nslices, nc, k2_sums, s);
   }
   k1_bwd_scalar<true><<<dim3(blocks_for(T, 4)), 256, 0, s>>>(x_flat, W, grad_proj, proj, inv_rms, grad_x,
                                                              grad_x_in, T, nc);

@@ -80,4 +80,28 @@ void launch_k2_param_reduce(const K2ParamSums& sums, hipStream_t s);
 // Lanes per token of K3's backward (fmhc_k3_bwd) on its 16-byte path.
 int k3_bwd_lanes8(int C);
 
+// The grad_W backward's runs (k1_bwd_mfma<true, ...>) for T tokens and nC
+// columns, and the reduce of its per-run partials into grad_W (32, nC) bf16
+// plus, in extra workgroups, K2's parameter gradients from `sums`
+// (k1_dw_reduce, k1.hip).
+int64_t k1_bwd_dw_runs(int64_t T, int64_t nC);
+int k1_dw_finish(const float* partial, uint16_t* grad_W, int64_t nruns, int nslices, int nC,
+                 const K2ParamSums& sums, hipStream_t s);
+
+// The pre-map backward with one read of x (premap_split.hip), for many tokens
+// (T >= kSplitMinT) and C a multiple of 128 with the MFMA path's alignments.
+constexpr int64_t kSplitMinT = 16384;
+bool premap_split_ok(const void* x, const void* W, const void* proj, const void* inv_rms, const void* gx,
+                     const void* go3, const void* gi, int64_t T, int64_t C);
+// Bytes of its exchange ring (zeroed by the call itself).
+int64_t premap_split_ring_bytes(int64_t T, int64_t C);
+// grad_x, grad_W and K2's parameter gradients as the three-kernel backward
+// gives them.  k2_partial: ceil(T / 16) x kNPar floats; dw_partial:
+// fmhc_k1_bwd_workspace_bytes(T, 4 C) bytes; ring: premap_split_ring_bytes.
+int premap_bwd_split(const uint16_t* x, const uint16_t* W, const uint16_t* proj, const float* inv_rms,
+                     const uint16_t* go3, const float* h_pre, const float* grad_h_post, const float* grad_H,
+                     const uint16_t* grad_x_in, uint16_t* grad_x, uint16_t* grad_W, const K2Params& P,
+                     void* grad_alpha_pre, void* grad_alpha_post, void* grad_alpha_res, void* grad_bias,
+                     float* k2_partial, float* dw_partial, void* ring, int64_t T, int64_t C, hipStream_t s);
+
 }  // namespace fmhc

@@ -44,6 +44,13 @@ constexpr int kK2Threads = 256;
 // bound by their arithmetic.
 constexpr int64_t kK2FwdSmallT = 2048;  // kK2BwdSmallT: k2_chain.h
 constexpr int kK2QuadTok = kK2Threads / 4;  // tokens per workgroup of the four-lane kernels
+// The four-lane backward's parameter partials sum 16 consecutive tokens
+// each (four per workgroup of 64 tokens): the unit in which the pre-map
+// backward's split kernel (premap_split.hip) runs K2, whose partials must be
+// the same sums.  (One 16-token workgroup per partial took 21.9 against
+// 17.5 us at T = 65536: the parameters staged four times as often.)
+constexpr int kK2BwdQuadThreads = kK2Threads;
+constexpr int kK2PartTok = 16;
 
 // Forward with four lanes per token (k2_token4: lane qd writes h_pre[qd],
 // h_post[qd] and H_merged row qd), kK2QuadTok tokens per workgroup; the
@@ -191,100 +198,8 @@ __global__ __launch_bounds__(THREADS) void k2_bwd_quad(
     gpre[i] = g_hpre ? g_hpre[t * kN + i] : 0.f;
   }
   stage_params<THREADS>(P, sm);
-  // Forward.  Lane 0: y[u] = h_pre[u] (u < 4), the sigmoid of post logit u - 4
-  // (u >= 4); lanes 1-3: y[u] = the softmax weight of their term u.
-  float alpha[8], z[8];
-  float mx = -INFINITY;
-#pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    alpha[u] = qd == 0 ? (u < kN ? sm.sc[0] : sm.sc[1]) : sm.sc[2];
-    z[u] = rb(rb(alpha[u] * p[u]) + sm.sc[3 + 8 * qd + u]);
-    if (qd != 0) mx = fmaxf(mx, z[u]);
-  }
-  // The quad's maximum (quad_perm [1, 0, 3, 2], then [2, 3, 0, 1]); exact in any order.
-  mx = fmaxf(mx, __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(mx), 0xb1, 0xf, 0xf, false)));
-  mx = fmaxf(mx, __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(mx), 0x4e, 0xf, 0xf, false)));
-  float ex[8];
-#pragma unroll
-  for (int u = 0; u < 8; ++u) ex[u] = expf(qd == 0 ? -z[u] : z[u] - mx);
-  float sum = 0.f;
-#pragma unroll
-  for (int u = 0; u < 8; ++u) sum = sum + quad_lane<1>(ex[u]);
-#pragma unroll
-  for (int u = 0; u < 8; ++u) sum = sum + quad_lane<2>(ex[u]);
-#pragma unroll
-  for (int u = 0; u < 8; ++u) sum = sum + quad_lane<3>(ex[u]);
-  float y[8];
-#pragma unroll
-  for (int u = 0; u < 8; ++u) y[u] = qd == 0 ? rb(1.f / (1.f + ex[u])) : rb(ex[u] / sum);
-  float hp[kN], sq[kN], hq[kN];
-  hp[0] = quad_lane<0>(y[0]);
-  hp[1] = quad_lane<0>(y[1]);
-  hp[2] = quad_lane<0>(y[2]);
-  hp[3] = quad_lane<0>(y[3]);
-  sq[0] = quad_lane<0>(y[4]);
-  sq[1] = quad_lane<0>(y[5]);
-  sq[2] = quad_lane<0>(y[6]);
-  sq[3] = quad_lane<0>(y[7]);
-#pragma unroll
-  for (int i = 0; i < kN; ++i) hq[i] = rb(2.f * sq[i]);
-
-  // Incoming gradients, rounded to bf16 (the .float() casts' backward).
-#pragma unroll
-  for (int ij = 0; ij < kN * kN; ++ij) gH[ij] = rb(gH[ij]);
-  float gz[8];
-  if (qd == 0) {
-    // H_merged = H_res - outer(h_post, h_pre), then the sigmoid backward.
-#pragma unroll
-    for (int i = 0; i < kN; ++i) {
-      float s = 0.f;
-#pragma unroll
-      for (int j = 0; j < kN; ++j) s = s + rb(-gH[i * kN + j] * hp[j]);
-      const float ghq = rb(rb(gpost[i]) + rb(s));
-      const float gs = rb(ghq * 2.f);
-      gz[kN + i] = rb(rb(gs * rb(1.f - sq[i])) * sq[i]);
-    }
-#pragma unroll
-    for (int j = 0; j < kN; ++j) {
-      float s = 0.f;
-#pragma unroll
-      for (int i = 0; i < kN; ++i) s = s + rb(-gH[i * kN + j] * hq[i]);
-      const float ghp = rb(rb(gpre[j]) + rb(s));
-      gz[j] = rb(rb(ghp * rb(1.f - hp[j])) * hp[j]);
-    }
-  } else {
-    // H_res = a @ perm: gy = rb(rb(gH . perm_m) a).
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int m = 8 * (qd - 1) + u;
-      float acc = 0.f;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const f32x4 pm = sm.perm[m * 4 + q];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) acc = acc + gH[4 * q + e] * pm[e];
-      }
-      gz[u] = rb(rb(acc) * y[u]);  // gy for now
-    }
-  }
-  // Softmax backward: gz = rb(gy - a sum(gy)), the sum over m in order.
-  float sgy = 0.f;
-#pragma unroll
-  for (int u = 0; u < 8; ++u) sgy = sgy + quad_lane<1>(gz[u]);
-#pragma unroll
-  for (int u = 0; u < 8; ++u) sgy = sgy + quad_lane<2>(gz[u]);
-#pragma unroll
-  for (int u = 0; u < 8; ++u) sgy = sgy + quad_lane<3>(gz[u]);
-  if (qd != 0) {
-#pragma unroll
-    for (int u = 0; u < 8; ++u) gz[u] = rb(gz[u] - y[u] * sgy);
-  }
-  float gp[8], pc[8];
-#pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    gp[u] = rb(gz[u] * alpha[u]);
-    pc[u] = rb(gz[u] * p[u]);
-  }
+  float gp[8], gz[8], s0, s1, s2;
+  k2_bwd_quad_token(sm, qd, p, gH, gpost, gpre, gp, gz, s0, s1, s2);
   if (valid) {
     uint16_t* row = grad_proj + t * kDk + 8 * qd;
     if constexpr (VEC) {
@@ -294,19 +209,6 @@ __global__ __launch_bounds__(THREADS) void k2_bwd_quad(
       for (int u = 0; u < 8; ++u) row[u] = f32_to_bf16(gp[u]);
     }
   }
-  // This token's parameter terms: the alphas' sums over their logits in
-  // order, the bias gradients gz.
-  float s0 = 0.f, s1 = 0.f, s2 = 0.f;
-#pragma unroll
-  for (int u = 0; u < kN; ++u) s0 += pc[u];
-#pragma unroll
-  for (int u = kN; u < 8; ++u) s1 += pc[u];
-#pragma unroll
-  for (int u = 0; u < 8; ++u) s2 += quad_lane<1>(pc[u]);
-#pragma unroll
-  for (int u = 0; u < 8; ++u) s2 += quad_lane<2>(pc[u]);
-#pragma unroll
-  for (int u = 0; u < 8; ++u) s2 += quad_lane<3>(pc[u]);
 #pragma unroll
   for (int u = 0; u < 8; ++u) red[slot][3 + 8 * qd + u] = valid ? gz[u] : 0.f;
   if (qd == 0) {
@@ -315,11 +217,18 @@ __global__ __launch_bounds__(THREADS) void k2_bwd_quad(
     red[slot][2] = valid ? s2 : 0.f;
   }
   __syncthreads();
-  if (threadIdx.x < kNPar) {
-    float v = 0.f;
-#pragma unroll 8
-    for (int w = 0; w < kTok; ++w) v += red[w][threadIdx.x];
-    partial[static_cast<int64_t>(blockIdx.x) * kNPar + threadIdx.x] = v;
+  // One partial per kK2PartTok tokens (the last workgroup's past T are not
+  // written: ceil(T / kK2PartTok) partials in all).
+  constexpr int kGroups = kTok / kK2PartTok;
+  if (threadIdx.x < kNPar * kGroups) {
+    const int g = static_cast<int>(threadIdx.x) / kNPar, k = static_cast<int>(threadIdx.x) % kNPar;
+    const int64_t part = static_cast<int64_t>(blockIdx.x) * kGroups + g;
+    if (part < (T + kK2PartTok - 1) / kK2PartTok) {
+      float v = 0.f;
+#pragma unroll
+      for (int w = 0; w < kK2PartTok; ++w) v += red[g * kK2PartTok + w][k];
+      partial[part * kNPar + k] = v;
+    }
   }
 }
 
@@ -333,7 +242,7 @@ bool k2_bad(int64_t T, int64_t n) { return T < 0 || n != kN; }
 // Workgroups (and parameter partials) of the backward: k2_bwd_small up to
 // kK2BwdSmallT tokens, k2_bwd_quad (kK2QuadTok tokens each) above.
 int64_t k2_bwd_blocks(int64_t T) {
-  return T <= kK2BwdSmallT ? (T + kK2BwdTok - 1) / kK2BwdTok : (T + kK2QuadTok - 1) / kK2QuadTok;
+  return T <= kK2BwdSmallT ? (T + kK2BwdTok - 1) / kK2BwdTok : (T + kK2PartTok - 1) / kK2PartTok;
 }
 
 }  // namespace
@@ -394,16 +303,16 @@ int k2_bwd_partials(const uint16_t* proj, const K2Params& P, const float* grad_h
   if (T > 0) {
     if (!proj || !grad_proj) return FMHC_ERR_INVALID_ARGUMENT;
     if (!workspace || workspace_bytes < fmhc_k2_bwd_workspace_bytes(T)) return FMHC_ERR_INVALID_ARGUMENT;
-    const dim3 grid(static_cast<unsigned>(nblocks));
+    const dim3 grid(static_cast<unsigned>(T <= kK2BwdSmallT ? nblocks : (T + kK2QuadTok - 1) / kK2QuadTok));
     if (T <= kK2BwdSmallT)
       k2_bwd_small<<<grid, kK2Threads, 0, s>>>(proj, P, grad_h_pre, grad_h_post, grad_H_merged, grad_proj,
                                                partial, T);
     else if (aligned16(proj) && aligned16(grad_proj))
-      k2_bwd_quad<kK2Threads, true><<<grid, kK2Threads, 0, s>>>(proj, P, grad_h_pre, grad_h_post, grad_H_merged,
-                                                                grad_proj, partial, T);
+      k2_bwd_quad<kK2BwdQuadThreads, true><<<grid, kK2BwdQuadThreads, 0, s>>>(
+          proj, P, grad_h_pre, grad_h_post, grad_H_merged, grad_proj, partial, T);
     else
-      k2_bwd_quad<kK2Threads, false><<<grid, kK2Threads, 0, s>>>(proj, P, grad_h_pre, grad_h_post,
-                                                                 grad_H_merged, grad_proj, partial, T);
+      k2_bwd_quad<kK2BwdQuadThreads, false><<<grid, kK2BwdQuadThreads, 0, s>>>(
+          proj, P, grad_h_pre, grad_h_post, grad_H_merged, grad_proj, partial, T);
     const int st = launch_status();
     if (st != FMHC_OK) return st;
   }

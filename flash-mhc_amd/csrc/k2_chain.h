@@ -221,6 +221,128 @@ __device__ __forceinline__ float quad_lane(float v) {
   return __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), K * 0x55, 0xf, 0xf, false));
 }
 
+// K2's backward of one token on a quad (the per-token body of k2_bwd_quad,
+// k2.hip; the pre-map backward's split kernel runs it too): lane qd holds
+// projections 8 qd .. 8 qd + 7 in p, and every lane the token's 16
+// grad_H_merged values (rounded in place), grad_h_post and grad_h_pre.  Gives
+// the lane's grad_proj values gp, its logit gradients gz (the bias terms) and
+// the alpha terms s0 (h_pre's), s1 (h_post's), s2 (the softmax's), valid on
+// lane qd = 0.  sm holds the staged parameters; the quad's four lanes must be
+// active.
+__device__ __forceinline__ void k2_bwd_quad_token(const K2Smem& sm, int qd, const float (&p)[8], float (&gH)[kN * kN],
+                                                  const float (&gpost)[kN], const float (&gpre)[kN], float (&gp)[8],
+                                                  float (&gz)[8], float& s0, float& s1, float& s2) {
+#pragma clang fp contract(off)
+  // Forward.  Lane 0: y[u] = h_pre[u] (u < 4), the sigmoid of post logit u - 4
+  // (u >= 4); lanes 1-3: y[u] = the softmax weight of their term u.
+  float alpha[8], z[8];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    alpha[u] = qd == 0 ? (u < kN ? sm.sc[0] : sm.sc[1]) : sm.sc[2];
+    z[u] = rb(rb(alpha[u] * p[u]) + sm.sc[3 + 8 * qd + u]);
+    if (qd != 0) mx = fmaxf(mx, z[u]);
+  }
+  // The quad's maximum (quad_perm [1, 0, 3, 2], then [2, 3, 0, 1]); exact in any order.
+  mx = fmaxf(mx, __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(mx), 0xb1, 0xf, 0xf, false)));
+  mx = fmaxf(mx, __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(mx), 0x4e, 0xf, 0xf, false)));
+  float ex[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) ex[u] = expf(qd == 0 ? -z[u] : z[u] - mx);
+  float sum = 0.f;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) sum = sum + quad_lane<1>(ex[u]);
+#pragma unroll
+  for (int u = 0; u < 8; ++u) sum = sum + quad_lane<2>(ex[u]);
+#pragma unroll
+  for (int u = 0; u < 8; ++u) sum = sum + quad_lane<3>(ex[u]);
+  float y[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) y[u] = qd == 0 ? rb(1.f / (1.f + ex[u])) : rb(ex[u] / sum);
+  float hp[kN], sq[kN], hq[kN];
+  hp[0] = quad_lane<0>(y[0]);
+  hp[1] = quad_lane<0>(y[1]);
+  hp[2] = quad_lane<0>(y[2]);
+  hp[3] = quad_lane<0>(y[3]);
+  sq[0] = quad_lane<0>(y[4]);
+  sq[1] = quad_lane<0>(y[5]);
+  sq[2] = quad_lane<0>(y[6]);
+  sq[3] = quad_lane<0>(y[7]);
+#pragma unroll
+  for (int i = 0; i < kN; ++i) hq[i] = rb(2.f * sq[i]);
+
+  // Incoming gradients, rounded to bf16 (the .float() casts' backward).
+#pragma unroll
+  for (int ij = 0; ij < kN * kN; ++ij) gH[ij] = rb(gH[ij]);
+  if (qd == 0) {
+    // H_merged = H_res - outer(h_post, h_pre), then the sigmoid backward.
+#pragma unroll
+    for (int i = 0; i < kN; ++i) {
+      float s = 0.f;
+#pragma unroll
+      for (int j = 0; j < kN; ++j) s = s + rb(-gH[i * kN + j] * hp[j]);
+      const float ghq = rb(rb(gpost[i]) + rb(s));
+      const float gs = rb(ghq * 2.f);
+      gz[kN + i] = rb(rb(gs * rb(1.f - sq[i])) * sq[i]);
+    }
+#pragma unroll
+    for (int j = 0; j < kN; ++j) {
+      float s = 0.f;
+#pragma unroll
+      for (int i = 0; i < kN; ++i) s = s + rb(-gH[i * kN + j] * hq[i]);
+      const float ghp = rb(rb(gpre[j]) + rb(s));
+      gz[j] = rb(rb(ghp * rb(1.f - hp[j])) * hp[j]);
+    }
+  } else {
+    // H_res = a @ perm: gy = rb(rb(gH . perm_m) a).
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int m = 8 * (qd - 1) + u;
+      float acc = 0.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 pm = sm.perm[m * 4 + q];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc = acc + gH[4 * q + e] * pm[e];
+      }
+      gz[u] = rb(rb(acc) * y[u]);  // gy for now
+    }
+  }
+  // Softmax backward: gz = rb(gy - a sum(gy)), the sum over m in order.
+  float sgy = 0.f;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) sgy = sgy + quad_lane<1>(gz[u]);
+#pragma unroll
+  for (int u = 0; u < 8; ++u) sgy = sgy + quad_lane<2>(gz[u]);
+#pragma unroll
+  for (int u = 0; u < 8; ++u) sgy = sgy + quad_lane<3>(gz[u]);
+  if (qd != 0) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) gz[u] = rb(gz[u] - y[u] * sgy);
+  }
+  float pc[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    gp[u] = rb(gz[u] * alpha[u]);
+    pc[u] = rb(gz[u] * p[u]);
+  }
+  // This token's parameter terms: the alphas' sums over their logits in
+  // order, the bias gradients gz.
+  s0 = 0.f;
+  s1 = 0.f;
+  s2 = 0.f;
+#pragma unroll
+  for (int u = 0; u < kN; ++u) s0 += pc[u];
+#pragma unroll
+  for (int u = kN; u < 8; ++u) s1 += pc[u];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) s2 += quad_lane<1>(pc[u]);
+#pragma unroll
+  for (int u = 0; u < 8; ++u) s2 += quad_lane<2>(pc[u]);
+#pragma unroll
+  for (int u = 0; u < 8; ++u) s2 += quad_lane<3>(pc[u]);
+}
+
 // K2 forward of one token on the four lanes of a quad (qd = lane & 3; p: the
 // token's 32 projections as bf16 values).  Lane qd computes logit qd (h_pre),
 // 4 + qd (h_post) and the softmax terms m = qd, qd + 4, ..., 20 + qd, gathers

@@ -67,14 +67,19 @@ __global__ __launch_bounds__(block_of<LPT>()) void k3_fwd_kernel(const uint16_t*
 }
 
 // GX = false: grad_h_pre only (the pre-map backward adds h_pre * go into K1's
-// grad_x store instead of writing it here).
-template <int VEC, int LPT, bool GX>
+// grad_x store instead of writing it here).  CANON (C a multiple of 128, at
+// most kMaxSlices slices, 16-byte groups): grad_h_pre in the slice order of
+// slice_sums_add (fmhc_common.h), which the pre-map backward's split kernel
+// reproduces; otherwise one FMA chain per lane over its groups, then
+// group_sum.
+template <int VEC, int LPT, bool GX, bool CANON>
 __global__ __launch_bounds__(block_of<LPT>()) void k3_bwd_kernel(const uint16_t* __restrict__ x,
                                                         const float* __restrict__ h_pre,
                                                         const uint16_t* __restrict__ go,
                                                         uint16_t* __restrict__ grad_x,
                                                         float* __restrict__ grad_h_pre,
                                                         int64_t T, int C) {
+  static_assert(!CANON || (VEC == 8 && LPT >= 16), "slice order: 16-byte groups, whole 16-lane rows");
   constexpr int WPT = LPT > kWave ? LPT / kWave : 1;  // waves per token
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t tok = token_of_lane<LPT>(lane);
@@ -85,8 +90,10 @@ __global__ __launch_bounds__(block_of<LPT>()) void k3_bwd_kernel(const uint16_t*
   const bool live = tok < T;
   const int sub = sub_of_lane<LPT>();
   const int ng = C / VEC;
+  // CANON with several waves per token: slice sums by slice.
+  __shared__ float slices[CANON && WPT > 1 ? kMaxSlices : 1][4];
 
-  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+  float s[4] = {0.f, 0.f, 0.f, 0.f};
   if (live) {
   const float* hp = h_pre + tok * 4;
   const float h0 = hp[0], h1 = hp[1], h2 = hp[2], h3 = hp[3];
@@ -100,8 +107,7 @@ __global__ __launch_bounds__(block_of<LPT>()) void k3_bwd_kernel(const uint16_t*
   uint16_t* gx2 = gx1 + C;
   uint16_t* gx3 = gx2 + C;
 
-#pragma unroll 2
-  for (int g = sub; g < ng; g += LPT) {
+  auto round = [&](int g, float (&acc)[4]) {
     float q[VEC], a[VEC], b[VEC], c[VEC], d[VEC], o[VEC];
     Lanes<VEC>::load(grow, g, q);
     Lanes<VEC>::load(x0, g, a);
@@ -124,45 +130,82 @@ __global__ __launch_bounds__(block_of<LPT>()) void k3_bwd_kernel(const uint16_t*
     }
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
-      s0 = __builtin_fmaf(a[e], q[e], s0);
-      s1 = __builtin_fmaf(b[e], q[e], s1);
-      s2 = __builtin_fmaf(c[e], q[e], s2);
-      s3 = __builtin_fmaf(d[e], q[e], s3);
+      acc[0] = __builtin_fmaf(a[e], q[e], acc[0]);
+      acc[1] = __builtin_fmaf(b[e], q[e], acc[1]);
+      acc[2] = __builtin_fmaf(c[e], q[e], acc[2]);
+      acc[3] = __builtin_fmaf(d[e], q[e], acc[3]);
     }
+  };
+  if constexpr (CANON) {
+    // Rounds k < kCanonRounds: lane sub takes group sub + k LPT (slice
+    // (sub + k LPT) / 16); whole 16-lane rows are inside or past the row.
+    // All rounds' loads first, then the slice sums.
+    const int ns = ng / 16;
+    float e[kCanonRounds][4];
+#pragma unroll
+    for (int k = 0; k < kCanonRounds; ++k) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) e[k][j] = 0.f;
+      if (sub + k * LPT < ng) round(sub + k * LPT, e[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < kCanonRounds; ++k) {
+      if (k * LPT >= ng) break;  // uniform
+      if constexpr (WPT == 1) {
+        slice_sums_add<LPT>(e[k], s, k, ns, lane);
+      } else {
+        const int g = sub + k * LPT;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) e[k][j] = row16_sum(e[k][j]);
+        if ((sub & 15) == 0 && g < ng) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) slices[g >> 4][j] = e[k][j];
+        }
+      }
+    }
+  } else {
+#pragma unroll 2
+    for (int g = sub; g < ng; g += LPT) round(g, s);
   }
   }
-  constexpr int GS = LPT < kWave ? LPT : kWave;
-  s0 = group_sum<GS>(s0);
-  s1 = group_sum<GS>(s1);
-  s2 = group_sum<GS>(s2);
-  s3 = group_sum<GS>(s3);
+  if constexpr (!CANON) {
+    constexpr int GS = LPT < kWave ? LPT : kWave;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s[j] = group_sum<GS>(s[j]);
+  }
   if constexpr (WPT > 1) {
-    // The token's waves add their sums in wave order (deterministic).
+    // The token's waves add their sums in wave order (deterministic), or
+    // with CANON its slices in slice order.
     __shared__ float red[block_of<LPT>() / kWave][4];
     const int wave = static_cast<int>(threadIdx.x) >> 6;
-    if (lane == 0) {
-      red[wave][0] = s0;
-      red[wave][1] = s1;
-      red[wave][2] = s2;
-      red[wave][3] = s3;
+    if (!CANON && lane == 0) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) red[wave][j] = s[j];
     }
     __syncthreads();
     if (live && sub == 0) {
       float t[4] = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (CANON) {
+        const int ns = ng / 16;
 #pragma unroll
-      for (int w = 0; w < WPT; ++w)
+        for (int j = 0; j < 4; ++j) t[j] = slices[0][j];
+        for (int sg = 1; sg < ns; ++sg)
 #pragma unroll
-        for (int k = 0; k < 4; ++k) t[k] += red[wave + w][k];
+          for (int j = 0; j < 4; ++j) t[j] += slices[sg][j];
+      } else {
+#pragma unroll
+        for (int w = 0; w < WPT; ++w)
+#pragma unroll
+          for (int k = 0; k < 4; ++k) t[k] += red[wave + w][k];
+      }
       float* dst = grad_h_pre + tok * 4;
 #pragma unroll
       for (int k = 0; k < 4; ++k) dst[k] = t[k];
     }
   } else if (sub == 0) {
     float* dst = grad_h_pre + tok * 4;
-    dst[0] = s0;
-    dst[1] = s1;
-    dst[2] = s2;
-    dst[3] = s3;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dst[j] = s[j];
   }
 }
 
@@ -264,9 +307,16 @@ int launch_k3_bwd(const uint16_t* x, const float* h_pre, const uint16_t* go, uin
                   float* grad_h_pre, int64_t T, int C, hipStream_t s) {
   const int lpt = pick_lpt_bwd<VEC>(C);
   const dim3 grid(blocks_for(T, tokens_per_block(lpt)));
+  const bool canon = VEC == 8 && k3_canon(C, lpt);
   with_lpt(lpt, [&](auto l) {
     constexpr int L = decltype(l)::value;
-    k3_bwd_kernel<VEC, L, GX><<<grid, block_of<L>(), 0, s>>>(x, h_pre, go, grad_x, grad_h_pre, T, C);
+    if constexpr (VEC == 8 && L >= 16) {
+      if (canon) {
+        k3_bwd_kernel<VEC, L, GX, true><<<grid, block_of<L>(), 0, s>>>(x, h_pre, go, grad_x, grad_h_pre, T, C);
+        return;
+      }
+    }
+    k3_bwd_kernel<VEC, L, GX, false><<<grid, block_of<L>(), 0, s>>>(x, h_pre, go, grad_x, grad_h_pre, T, C);
   });
   return launch_status();
 }

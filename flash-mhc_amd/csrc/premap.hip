@@ -32,11 +32,20 @@
 #include <hip/hip_runtime.h>
 
 #include <mutex>
+#include <type_traits>
 
 #include "flash_mhc_hip.h"
 #include "fmhc_common.h"
 #include "k1_premap.h"
 #include "k2_chain.h"
+
+// 1 (an evidence build): the backward of many tokens at C a multiple of 128
+// reads x once (premap_split.hip); 0: K3's reduce pass, K2's backward and K1's
+// backward, each reading x, which is faster (the split kernel waits on its
+// team's exchange).
+#ifndef FMHC_PREMAP_SPLIT
+#define FMHC_PREMAP_SPLIT 0
+#endif
 
 // 1: the forward without K1's column split runs as one kernel, K1 with K2
 // and K3 on each tile (k1_premap_tile); 0 (an evidence build): K1, K2 and K3
@@ -193,7 +202,7 @@ __global__ __launch_bounds__(kFinishThreads) void k1_finish_k2_k3(
 // token order.  grad_proj and the parameter partials are those of K3's
 // backward followed by k2_bwd_small, bit for bit, with one launch and one
 // chain of load latencies fewer.
-template <int LPT>
+template <int LPT, bool CANON>
 __global__ __launch_bounds__(kK2BwdTok * LPT) void k3_reduce_k2_bwd(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ go3, const uint16_t* __restrict__ proj,
     const K2Params P, const float* __restrict__ g_hpost, const float* __restrict__ g_H,
@@ -215,36 +224,56 @@ __global__ __launch_bounds__(kK2BwdTok * LPT) void k3_reduce_k2_bwd(
   K2ParamRegs<kThreads> regs;
   regs.load(P);
 
-  // K3's reduce-only backward of the token: s_j = sum_c x[t, j, c] go3[t, c].
-  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-  if (valid) {
-    const uint16_t* x0 = x + t * 4 * C;
-    const uint16_t* x1 = x0 + C;
-    const uint16_t* x2 = x1 + C;
-    const uint16_t* x3 = x2 + C;
-    const uint16_t* grow = go3 + t * C;
-    const int ng = C / 8;
-#pragma unroll 2
-    for (int g = sub; g < ng; g += LPT) {
-      float gq[8], a[8], b[8], c[8], d[8];
-      Lanes<8>::load(grow, g, gq);
-      Lanes<8>::load(x0, g, a);
-      Lanes<8>::load(x1, g, b);
-      Lanes<8>::load(x2, g, c);
-      Lanes<8>::load(x3, g, d);
+  // K3's reduce-only backward of the token: s_j = sum_c x[t, j, c] go3[t, c],
+  // in k3_bwd_kernel's order (with CANON the slice order of slice_sums_add).
+  float s[4] = {0.f, 0.f, 0.f, 0.f};
+  const int ng = C / 8;
+  const uint16_t* x0 = x + t * 4 * C;
+  const uint16_t* x1 = x0 + C;
+  const uint16_t* x2 = x1 + C;
+  const uint16_t* x3 = x2 + C;
+  const uint16_t* grow = go3 + t * C;
+  auto round = [&](int g, float (&acc)[4]) {
+    float gq[8], a[8], b[8], c[8], d[8];
+    Lanes<8>::load(grow, g, gq);
+    Lanes<8>::load(x0, g, a);
+    Lanes<8>::load(x1, g, b);
+    Lanes<8>::load(x2, g, c);
+    Lanes<8>::load(x3, g, d);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        s0 = __builtin_fmaf(a[e], gq[e], s0);
-        s1 = __builtin_fmaf(b[e], gq[e], s1);
-        s2 = __builtin_fmaf(c[e], gq[e], s2);
-        s3 = __builtin_fmaf(d[e], gq[e], s3);
-      }
+    for (int e = 0; e < 8; ++e) {
+      acc[0] = __builtin_fmaf(a[e], gq[e], acc[0]);
+      acc[1] = __builtin_fmaf(b[e], gq[e], acc[1]);
+      acc[2] = __builtin_fmaf(c[e], gq[e], acc[2]);
+      acc[3] = __builtin_fmaf(d[e], gq[e], acc[3]);
     }
+  };
+  if constexpr (CANON) {
+    // Every slot computes (idle ones on the last token), so the slot's lanes
+    // are all active for the row sums.
+    constexpr int kRounds = LPT == 64 ? 4 : 2;  // fewer than 256 (64) groups for 64 (32) lanes
+    float e[kRounds][4];
+#pragma unroll
+    for (int k = 0; k < kRounds; ++k) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) e[k][j] = 0.f;
+      if (sub + k * LPT < ng) round(sub + k * LPT, e[k]);
+    }
+    const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
+#pragma unroll
+    for (int k = 0; k < kRounds; ++k) {
+      if (k * LPT >= ng) break;  // uniform
+      slice_sums_add<LPT>(e[k], s, k, ng / 16, lane);
+    }
+  } else {
+    if (valid) {
+#pragma unroll 2
+      for (int g = sub; g < ng; g += LPT) round(g, s);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s[j] = group_sum<LPT>(s[j]);
   }
-  s0 = group_sum<LPT>(s0);
-  s1 = group_sum<LPT>(s1);
-  s2 = group_sum<LPT>(s2);
-  s3 = group_sum<LPT>(s3);
+  const float s0 = s[0], s1 = s[1], s2 = s[2], s3 = s[3];
 
   regs.store(sm);
   __syncthreads();
@@ -263,7 +292,7 @@ __global__ __launch_bounds__(kK2BwdTok * LPT) void k3_reduce_k2_bwd(
 }
 
 struct PremapWs {
-  int64_t gh, gp, k2, k1, total;  // byte offsets / sizes
+  int64_t gh, gp, k2, k1, ring, total;  // byte offsets / sizes
 };
 
 PremapWs premap_ws(int64_t T, int64_t C) {
@@ -272,7 +301,8 @@ PremapWs premap_ws(int64_t T, int64_t C) {
   w.gp = round_up(T * 4 * 4);                   // grad_proj (T, 32) bf16
   w.k2 = w.gp + round_up(T * 32 * 2);           // K2 parameter partials
   w.k1 = w.k2 + round_up(fmhc_k2_bwd_workspace_bytes(T));  // K1 grad_W partials
-  w.total = w.k1 + round_up(fmhc_k1_bwd_workspace_bytes(T, 4 * C));
+  w.ring = w.k1 + round_up(fmhc_k1_bwd_workspace_bytes(T, 4 * C));  // the split backward's exchange ring
+  w.total = w.ring + (T > 0 && C % kSliceCols == 0 ? round_up(premap_split_ring_bytes(T, C)) : 0);
   return w;
 }
 
@@ -445,6 +475,14 @@ extern "C" int fmhc_premap_bwd(const uint16_t* x, const uint16_t* W, const void*
   if (T > 0 && (!workspace || workspace_bytes < w.total || !aligned16(workspace))) return FMHC_ERR_INVALID_ARGUMENT;
   char* ws = static_cast<char*>(workspace);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (FMHC_PREMAP_SPLIT && premap_split_ok(x, W, proj, inv_rms, grad_x, grad_layer_input, grad_x_in, T, C)) {
+    K2Params P;
+    if (!k2_params(alpha_pre, alpha_post, alpha_res, bias, perm, param_dtype, P)) return FMHC_ERR_INVALID_ARGUMENT;
+    return premap_bwd_split(x, W, proj, inv_rms, grad_layer_input, h_pre, grad_h_post, grad_H_merged, grad_x_in,
+                            grad_x, grad_W, P, grad_alpha_pre, grad_alpha_post, grad_alpha_res, grad_bias,
+                            reinterpret_cast<float*>(ws + w.k2), reinterpret_cast<float*>(ws + w.k1), ws + w.ring, T,
+                            C, s);
+  }
   float* gh = T > 0 ? reinterpret_cast<float*>(ws + w.gh) : nullptr;
   uint16_t* gp = T > 0 ? reinterpret_cast<uint16_t*>(ws + w.gp) : nullptr;
   int st = FMHC_OK;
@@ -458,12 +496,18 @@ extern "C" int fmhc_premap_bwd(const uint16_t* x, const uint16_t* W, const void*
     // Few tokens: K3's reduce-only pass and K2's backward as one kernel.
     float* partial = reinterpret_cast<float*>(ws + w.k2);
     const dim3 grid(static_cast<unsigned>((T + kK2BwdTok - 1) / kK2BwdTok));
+    const bool canon = k3_canon(C, lanes);
+    auto launch = [&](auto lpt_c, auto canon_c) {
+      constexpr int L = decltype(lpt_c)::value;
+      k3_reduce_k2_bwd<L, decltype(canon_c)::value><<<grid, kK2BwdTok * L, 0, s>>>(
+          x, grad_layer_input, proj, P, grad_h_post, grad_H_merged, gp, partial, T, static_cast<int>(C));
+    };
+    using I64 = std::integral_constant<int, 64>;
+    using I32 = std::integral_constant<int, 32>;
     if (lanes == 64)
-      k3_reduce_k2_bwd<64><<<grid, kK2BwdTok * 64, 0, s>>>(x, grad_layer_input, proj, P, grad_h_post,
-                                                            grad_H_merged, gp, partial, T, static_cast<int>(C));
+      canon ? launch(I64{}, std::true_type{}) : launch(I64{}, std::false_type{});
     else
-      k3_reduce_k2_bwd<32><<<grid, kK2BwdTok * 32, 0, s>>>(x, grad_layer_input, proj, P, grad_h_post,
-                                                            grad_H_merged, gp, partial, T, static_cast<int>(C));
+      canon ? launch(I32{}, std::true_type{}) : launch(I32{}, std::false_type{});
     st = launch_status();
     sums = K2ParamSums{partial, static_cast<int64_t>(grid.x), grad_alpha_pre, grad_alpha_post, grad_alpha_res,
                        grad_bias, P.bf16};

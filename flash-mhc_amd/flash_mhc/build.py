@@ -32,7 +32,8 @@ LIB_NAME = "libflash_mhc_hip.so"
 LIB_PATH = LIB_DIR / LIB_NAME
 PROBE_LIB_PATH = LIB_DIR / "libflash_mhc_probe.so"
 
-SOURCES = ("k1.hip", "k2.hip", "k3.hip", "k4.hip", "premap.hip", "premap_resident.hip", "abi.hip")
+SOURCES = ("k1.hip", "k2.hip", "k3.hip", "k4.hip", "premap.hip", "premap_resident.hip", "premap_split.hip",
+           "abi.hip")
 PROBE_SOURCES = ("stream_probe.hip",)
 
 ARCH = "gfx950"
@@ -64,9 +65,13 @@ SOURCE_FLAGS = {"k1.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 # three kernels, against the product's one kernel (K1 on a tile of 16 to 64
 # tokens, then K2 and K3 on it by the same workgroup).  premap_tile_nt: the one kernel
 # with nontemporal loads of x in its K1 part, so that its K3 part re-reads the
-# tile from HBM instead of the memory-side cache.
+# tile from HBM instead of the memory-side cache.  premap_reread: the forward's
+# tile kernel instead of the single read.  premap_bwd_split: the pre-map
+# backward with one read of x (premap_split.hip) instead of K3's reduce pass,
+# K2 and K1.
 VARIANTS = {"k1_valu": ["-DFMHC_K1_VALU=1"], "premap_three_kernels": ["-DFMHC_PREMAP_TILE=0"],
-            "premap_tile_nt": ["-DFMHC_PREMAP_TILE_NT=1"], "premap_reread": ["-DFMHC_PREMAP_RESIDENT=0"]}
+            "premap_tile_nt": ["-DFMHC_PREMAP_TILE_NT=1"], "premap_reread": ["-DFMHC_PREMAP_RESIDENT=0"],
+            "premap_bwd_split": ["-DFMHC_PREMAP_SPLIT=1"]}
 
 
 def variant_path(name: str) -> Path:
