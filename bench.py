@@ -321,6 +321,48 @@ def premap_alone(T: int, C: int, iters: int = 10) -> dict:
             "workload": f"pre-map forward, T={T}, n=4, C={C}, bf16, each launch after a cache flush"}
 
 
+def premap_bwd_alone(T: int, C: int, iters: int = 10) -> dict:
+    """The block's pre-map backward (flash_mhc::mhc_pre_map_coeffs's backward:
+    K3's grad_h_pre, K2's backward, K1's backward with grad_W, and x's
+    incoming gradient added in grad_x's store) alone at (T, C), each launch
+    after a cache flush, for profiler runs that compare builds.  Algorithmic
+    bytes: x, the incoming gradient, grad_layer_input, proj, inv_rms, h_pre,
+    grad_h_post, grad_H_merged and W read once, grad_x and grad_W written
+    once."""
+    from flash_mhc import build_permutation_matrices
+    from flash_mhc import kernels as K
+
+    g = torch.Generator(device="cuda").manual_seed(0)
+    nC = 4 * C
+    x = torch.randn(T, 4, C, device="cuda", generator=g).to(torch.bfloat16)
+    W = (torch.randn(32, nC, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    p = [torch.tensor([0.8], device="cuda"), torch.tensor([1.2], device="cuda"), torch.tensor([1.7], device="cuda"),
+         torch.randn(32, device="cuda", generator=g) * 0.5, build_permutation_matrices(4)[0].cuda()]
+    _, _, _, hp, proj, inv = K.premap_fwd(x, W, *p)
+    g_li = torch.randn(T, C, device="cuda", generator=g).to(torch.bfloat16)
+    g_hq = torch.randn(T, 4, device="cuda", generator=g)
+    g_H = torch.randn(T, 4, 4, device="cuda", generator=g)
+    g_in = torch.randn(T, 4, C, device="cuda", generator=g).to(torch.bfloat16)
+    flush = CacheFlush(Probe())
+    times = []
+    for _ in range(iters):
+        flush()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        K.premap_bwd(x, W, *p, hp, proj, inv, g_li, g_hq, g_H, g_in)
+        e1.record()
+        times.append((e0, e1))
+    torch.cuda.synchronize()
+    nbytes = (3 * T * nC * 2 + T * C * 2 + T * 32 * 2 + T * 4 + T * 4 * 4 * 2 + T * 16 * 4
+              + 2 * 32 * nC * 2)
+    ts = [a.elapsed_time(b) * 1e3 for a, b in times]
+    med = statistics.median(ts)
+    return {"premap_bwd_cold_us": round(med, 1), "min_us": round(min(ts), 1), "bytes": nbytes,
+            "GBps": round(nbytes / (med * 1e-6) / 1e9, 1),
+            "workload": f"pre-map backward with x's incoming gradient, T={T}, n=4, C={C}, bf16, "
+                        "each launch after a cache flush"}
+
+
 def eval_latency(C: int = 4096, tokens=(1, 64, 257, 65537), variants=("fused", "reference_rules")) -> dict:
     """Eval-mode forward latency of MHCLiteBlock(4, C, Linear(C, C)) (bf16,
     random weights), the inference / ragged-tail shapes: eager and replayed from
@@ -635,7 +677,7 @@ def main() -> None:
                     help="skip the K1-backward and block-step fields (profiler runs: only the six kernels)")
     ap.add_argument("--traffic", type=str, default=str(ROOT / "profiles" / "traffic_k4_bwd_T65536_C1024.json"),
                     help="measured HBM traffic summary (rocprofv3 --pmc) for the dominant kernel")
-    ap.add_argument("--only", choices=("block", "eval", "premap"), default=None,
+    ap.add_argument("--only", choices=("block", "eval", "premap", "premap_bwd"), default=None,
                     help="run one extra alone, fused path only, and print its JSON (profiler runs of the "
                          "block step at --T/--C for --steps iterations, or of the eval latency at --eval-T)")
     ap.add_argument("--eval-T", type=str, default="1,64,257,65537", help="token counts of the eval latency")
@@ -669,6 +711,9 @@ def main() -> None:
         return
     if args.only == "premap":
         print(json.dumps({"premap_alone": premap_alone(args.T, args.C, iters=args.steps)}), flush=True)
+        return
+    if args.only == "premap_bwd":
+        print(json.dumps({"premap_bwd_alone": premap_bwd_alone(args.T, args.C, iters=args.steps)}), flush=True)
         return
     if args.only == "eval":
         print(json.dumps({"eval_latency": eval_latency(tokens=eval_tokens, variants=("fused",))}), flush=True)
