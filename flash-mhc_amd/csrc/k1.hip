@@ -827,15 +827,15 @@ __global__ __launch_bounds__(256) void k1_bwd_mfma(const uint16_t* __restrict__ 
 // i = (((slice * 8 + m) * 2 + h) * 4 + r) * 64 + lane stands for
 // d = 16 h + (lane & 15), k = 128 slice + 8 (4 (lane >> 4) + r) + m; each
 // thread sums four consecutive elements (16-byte loads, four parts per trip).
-// Workgroups from dw_blocks on sum K2's parameter gradients instead, one wave
-// per parameter (the pre-map backward; one launch fewer than K2's own reduce).
+// Workgroups from dw_blocks on sum K2's parameter gradients instead, one
+// workgroup per parameter (the pre-map backward; one launch fewer than K2's
+// own reduce).
 __global__ __launch_bounds__(256) void k1_dw_reduce(const float* __restrict__ partial,
                                                     uint16_t* __restrict__ dW, int64_t nparts,
                                                     int nslices, int nC, unsigned dw_blocks,
                                                     const K2ParamSums k2) {
-  if (blockIdx.x >= dw_blocks) {
-    const int k = static_cast<int>(blockIdx.x - dw_blocks) * 4 + static_cast<int>(threadIdx.x >> 6);
-    if (k < kNPar) k2_param_sum(k2, k, static_cast<int>(threadIdx.x & (kWave - 1)));  // whole waves
+  if (blockIdx.x >= dw_blocks) {  // one workgroup per K2 parameter
+    k2_param_sum(k2, static_cast<int>(blockIdx.x - dw_blocks));
     return;
   }
   const int64_t per_part = static_cast<int64_t>(nslices) * (8 * 2 * 4 * kWave);
@@ -1307,8 +1307,8 @@ int k1_dw_finish(const float* partial, uint16_t* grad_W, int64_t nruns, int nsli
                  const K2ParamSums& sums, hipStream_t s) {
   const int64_t per_part = static_cast<int64_t>(nslices) * (8 * 2 * 4 * kWave);
   const unsigned nb = blocks_for(per_part / 4, 256);
-  constexpr unsigned k2_blocks = (kNPar + 3) / 4;  // one wave per K2 parameter
-  k1_dw_reduce<<<dim3(nb + k2_blocks), 256, 0, s>>>(partial, grad_W, nruns, nslices, nC, nb, sums);
+  static_assert(kK2SumThreads == 256, "K2's parameter sums share the reduce's workgroups");
+  k1_dw_reduce<<<dim3(nb + kNPar), 256, 0, s>>>(partial, grad_W, nruns, nslices, nC, nb, sums);
   return launch_status();
 }
 

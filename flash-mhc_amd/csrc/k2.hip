@@ -232,9 +232,9 @@ __global__ __launch_bounds__(THREADS) void k2_bwd_quad(
   }
 }
 
-// One wave per parameter gradient (k2_param_sum).
-__global__ __launch_bounds__(kWave) void k2_param_reduce(const K2ParamSums r) {
-  k2_param_sum(r, static_cast<int>(blockIdx.x), static_cast<int>(threadIdx.x));
+// One workgroup per parameter gradient (k2_param_sum).
+__global__ __launch_bounds__(kK2SumThreads) void k2_param_reduce(const K2ParamSums r) {
+  k2_param_sum(r, static_cast<int>(blockIdx.x));
 }
 
 bool k2_bad(int64_t T, int64_t n) { return T < 0 || n != kN; }
@@ -323,7 +323,7 @@ int k2_bwd_partials(const uint16_t* proj, const K2Params& P, const float* grad_h
 }
 
 void launch_k2_param_reduce(const K2ParamSums& sums, hipStream_t s) {
-  k2_param_reduce<<<dim3(kNPar), kWave, 0, s>>>(sums);
+  k2_param_reduce<<<dim3(kNPar), kK2SumThreads, 0, s>>>(sums);
 }
 
 }  // namespace fmhc

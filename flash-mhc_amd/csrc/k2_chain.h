@@ -127,11 +127,12 @@ __device__ __forceinline__ void load_proj(const uint16_t* __restrict__ row, floa
   }
 }
 
-// K2 backward's parameter gradients from its per-workgroup partials
-// (partial[b * kNPar + k] for workgroup b): parameter k (0-2: the alphas,
-// 3 + j: bias j) as one wave's sum, lane l adding workgroups l, l + 64, ...
-// in order, then wave_sum; rounded to bf16 (the reference sums a bf16
-// tensor) and stored in the parameters' dtype.  nblocks = 0 writes zeros.
+// K2 backward's parameter gradients from its partials (partial[b * kNPar + k]
+// for partial b): parameter k (0-2: the alphas, 3 + j: bias j) as one
+// 256-thread workgroup's sum, thread t adding partials t, t + 256, ... in
+// order, then wave_sum in each wave and the four waves' sums in wave order;
+// rounded to bf16 (the reference sums a bf16 tensor) and stored in the
+// parameters' dtype.  nblocks = 0 writes zeros.
 struct K2ParamSums {
   const float* partial = nullptr;
   int64_t nblocks = 0;
@@ -142,18 +143,27 @@ struct K2ParamSums {
   bool bf16 = false;
 };
 
-// Every lane of the wave must be active (wave_sum).
-__device__ __forceinline__ void k2_param_sum(const K2ParamSums& r, int k, int lane) {
+constexpr int kK2SumThreads = 256;
+
+// Every thread of the workgroup must call it.
+__device__ __forceinline__ void k2_param_sum(const K2ParamSums& r, int k) {
+  __shared__ float wsum[kK2SumThreads / kWave];
+  const int t = static_cast<int>(threadIdx.x);
   float v = 0.f;
-  for (int64_t b = lane; b < r.nblocks; b += kWave) v += r.partial[b * kNPar + k];
+  for (int64_t b = t; b < r.nblocks; b += kK2SumThreads) v += r.partial[b * kNPar + k];
   v = wave_sum(v);
-  if (lane == 0) {
+  if ((t & (kWave - 1)) == 0) wsum[t / kWave] = v;
+  __syncthreads();
+  if (t == 0) {
+    float tot = wsum[0];
+#pragma unroll
+    for (int w = 1; w < kK2SumThreads / kWave; ++w) tot += wsum[w];
     void* dst = k == 0 ? r.g_ap : (k == 1 ? r.g_apo : (k == 2 ? r.g_ar : r.g_bias));
     const int i = k < 3 ? 0 : k - 3;
     if (r.bf16)
-      static_cast<uint16_t*>(dst)[i] = f32_to_bf16(v);
+      static_cast<uint16_t*>(dst)[i] = f32_to_bf16(tot);
     else
-      static_cast<float*>(dst)[i] = rb(v);
+      static_cast<float*>(dst)[i] = rb(tot);
   }
 }
 
