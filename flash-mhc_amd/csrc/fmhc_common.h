@@ -231,7 +231,9 @@ __device__ __forceinline__ void slice_sums_add(float (&e)[4], float (&s)[4], int
     if (sigma < ns) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float p = __shfl(e[j], tb + 16 * r, kWave);
+        // A whole wave per token: the row's sum is read as a scalar (no LDS).
+        const float p = LPT == kWave ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e[j]), 16 * r))
+                                     : __shfl(e[j], tb + 16 * r, kWave);
         s[j] = sigma == 0 ? p : s[j] + p;
       }
     }
