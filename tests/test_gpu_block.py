@@ -89,7 +89,7 @@ def check_param_grads(blk, pg, taps, tag):
             terms = (taps["z_" + part].grad * taps["p_" + part]).abs()
             if part == "res":
                 terms = torch.maximum(terms, (taps["a_res"] * taps["a_res"].grad * taps["p_res"]).abs())
-            t2 = float(terms.double().pow(2).sum().sqrt())
+            t2 = float(terms.detach().double().pow(2).sum().sqrt())
             err = abs(float(q.grad.float()) - float(ref))
             bound = 5e-2 * abs(float(ref)) + 2.0**-6 * t2
             assert err <= bound, (tag, name, float(q.grad.float()), float(ref), t2)
