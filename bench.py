@@ -238,6 +238,45 @@ def block_step(T: int, C: int, iters: int = 10, variants=("fused", "reference_ru
     return out
 
 
+def train_stack(T: int, C: int, layers: int = 12, iters: int = 3, warmup: int = 1, compiled: bool = True) -> dict:
+    """layers x MHCLiteBlock(4, C, Linear(C, C, bias=False)) forward + backward
+    (bf16, random weights, activation checkpointing on), eager or under
+    torch.compile (the first warmup step compiles): milliseconds per step and
+    the peak HBM allocated."""
+    import flash_mhc
+
+    torch.manual_seed(0)
+    blocks = torch.nn.Sequential(*[
+        flash_mhc.MHCLiteBlock(4, C, torch.nn.Linear(C, C, bias=False), activation_checkpointing=True)
+        for _ in range(layers)
+    ]).to("cuda", torch.bfloat16)
+    g = torch.Generator(device="cuda").manual_seed(1)
+    x = torch.randn(T, 4, C, device="cuda", generator=g).to(torch.bfloat16).requires_grad_(True)
+    up = torch.randn(T, 4, C, device="cuda", generator=g).to(torch.bfloat16)
+    run = torch.compile(blocks) if compiled else blocks
+
+    def one():
+        for p in blocks.parameters():
+            p.grad = None
+        x.grad = None
+        run(x).backward(up)
+
+    for _ in range(max(1, warmup)):
+        one()
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        one()
+    e1.record()
+    torch.cuda.synchronize()
+    return {"ms_per_step": round(e0.elapsed_time(e1) / iters, 2),
+            "peak_GB": round(torch.cuda.max_memory_allocated() / 1e9, 1),
+            "workload": (f"{layers} x MHCLiteBlock(4, {C}, Linear({C}, {C}, bias=False)), activation checkpointing, "
+                         f"forward + backward, T={T}, bf16, {'torch.compile' if compiled else 'eager'}")}
+
+
 def block_step_graphed(T: int = 4096, C: int = 1024, iters: int = 20) -> dict:
     """MHCLiteBlock(4, C, Linear(C, C)) forward + backward at few tokens, where
     the host's launches bound an eager step: eager, and the whole step (forward
@@ -677,9 +716,11 @@ def main() -> None:
                     help="skip the K1-backward and block-step fields (profiler runs: only the six kernels)")
     ap.add_argument("--traffic", type=str, default=str(ROOT / "profiles" / "traffic_k4_bwd_T65536_C1024.json"),
                     help="measured HBM traffic summary (rocprofv3 --pmc) for the dominant kernel")
-    ap.add_argument("--only", choices=("block", "eval", "premap", "premap_bwd"), default=None,
+    ap.add_argument("--only", choices=("block", "eval", "premap", "premap_bwd", "train"), default=None,
                     help="run one extra alone, fused path only, and print its JSON (profiler runs of the "
                          "block step at --T/--C for --steps iterations, or of the eval latency at --eval-T)")
+    ap.add_argument("--layers", type=int, default=12, help="blocks of the --only train stack")
+    ap.add_argument("--eager", action="store_true", help="--only train without torch.compile")
     ap.add_argument("--eval-T", type=str, default="1,64,257,65537", help="token counts of the eval latency")
     args = ap.parse_args()
     if args.n != 4:
@@ -714,6 +755,10 @@ def main() -> None:
         return
     if args.only == "premap_bwd":
         print(json.dumps({"premap_bwd_alone": premap_bwd_alone(args.T, args.C, iters=args.steps)}), flush=True)
+        return
+    if args.only == "train":
+        print(json.dumps({"train_stack": train_stack(args.T, args.C, layers=args.layers, iters=args.steps,
+                                                     warmup=args.warmup, compiled=not args.eager)}), flush=True)
         return
     if args.only == "eval":
         print(json.dumps({"eval_latency": eval_latency(tokens=eval_tokens, variants=("fused",))}), flush=True)

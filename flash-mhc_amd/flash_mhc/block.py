@@ -264,7 +264,13 @@ class MHCLiteBlock(nn.Module):
         if _ops.fused_premap_enabled() and _plain_eager(x_streams):
             if not torch.is_grad_enabled():
                 return self._forward_nograd(x_streams, **kwargs)
-            if not self._use_activation_checkpointing(x_streams) and _ops.fused_xgrad_flag():
+            if _ops.fused_xgrad_flag():
+                # Also under activation checkpointing: in eager mode the
+                # checkpointed K3 op saves nothing, so nothing is ever
+                # recomputed, and the layer keeps the layer input if its
+                # backward needs it.  The single pre-map op saves the same
+                # tensors as the two ops and reads x once where the
+                # single-read forward applies.
                 return self._forward_eager(x_streams, **kwargs)
         ctx = nullcontext() if self.training else _ops.disable_autotune_temporarily()
         # Only the pre-map region is checkpointed: post-res's backward needs

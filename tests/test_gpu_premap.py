@@ -130,6 +130,38 @@ def _block_run(flag, T, C, ckpt=False, seed=80):
             os.environ["FLASH_MHC_FUSED_PREMAP"] = old
 
 
+@pytest.mark.parametrize("T,C", [(4096, 1024), (20000, 2048), (257, 256), (5, 4096)])
+def test_checkpointed_two_op_region_equals_eager_block(T, C):
+    """With activation checkpointing the eager block runs the pre-map region
+    as the single op mhc_pre_map; under torch.compile and other dispatch
+    modes it runs mhc_pre_map_coeffs and a checkpointed mhc_pre_map_mix.  At
+    token counts where both take the same K1 kernel (below the single-read
+    forward's, or C above 1024) the two give the same output, x gradient and
+    parameter gradients, bit for bit."""
+    from contextlib import nullcontext
+
+    torch.manual_seed(81)
+    blk = flash_mhc.MHCLiteBlock(4, C, torch.nn.Linear(C, C, bias=False), activation_checkpointing=True)
+    blk = blk.to(DEV, BF16)
+    x0 = randn((T, 4, C), 82).to(DEV, BF16)
+    up = randn((T, 4, C), 83).to(DEV, BF16)
+    res = []
+    for two_op in (False, True):
+        blk.zero_grad(set_to_none=True)
+        x = x0.clone().requires_grad_(True)
+        if two_op:
+            out = blk._run(x, blk._mhc_pre_map_triton, blk._mhc_post_res_triton, nullcontext(), {},
+                           checkpoint_post_res=False)
+        else:
+            out = blk(x)
+        out.backward(up)
+        torch.cuda.synchronize()
+        res.append([out.detach(), x.grad] + [p.grad for p in blk.parameters()])
+    names = ["out", "grad_x"] + [n for n, _ in blk.named_parameters()]
+    for name, a, b in zip(names, *res):
+        assert torch.equal(a, b), f"{name}: {int((a != b).sum())} of {a.numel()} differ"
+
+
 @pytest.mark.parametrize("ckpt", [False, True])
 def test_block_premap_equals_separate_ops(ckpt):
     """The block with the pre-map op vs K1, K2, K3 as separate ops: the same
