@@ -37,6 +37,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import statistics
 import sys
@@ -236,6 +237,60 @@ def block_step(T: int, C: int, iters: int = 10, variants=("fused", "reference_ru
                 os.environ[f] = v
     out["workload"] = f"MHCLiteBlock(4, {C}, Linear({C}, {C})) forward + backward, T={T}, bf16"
     return out
+
+
+def placement_sweep(T: int, C: int, pads: tuple[int, ...], iters: int = 10) -> dict:
+    """K3 and K4 forward and backward at (T, C) with their tensors placed back
+    to back in one allocation, `pad` bytes apart (each start rounded up to
+    4 KiB first), for each pad: the kernels' GB/s (algorithmic bytes of
+    bytes_model over the event time of `iters` back-to-back launches, after
+    one untimed launch).  Shows how much the HBM rate depends on where the
+    tensors lie relative to each other."""
+    from flash_mhc import kernels as K
+
+    n = 4
+    bf, f4 = torch.bfloat16, torch.float32
+    specs = [("go", (T, n, C), bf), ("x", (T, n, C), bf), ("lo", (T, C), bf), ("gx", (T, n, C), bf),
+             ("glo", (T, C), bf), ("H", (T, n, n), f4), ("hp", (T, n), f4), ("hq", (T, n), f4),
+             ("gH", (T, n, n), f4), ("ghq", (T, n), f4), ("ghp", (T, n), f4)]
+    bm = bytes_model(T, n, C, 32)
+    out = {}
+    for pad in pads:
+        sizes = [math.prod(shape) * torch.empty((), dtype=dt).element_size() for _, shape, dt in specs]
+        offs, o = [], 0
+        for nb in sizes:
+            offs.append(o)
+            o += (nb + 4095) // 4096 * 4096 + pad
+        pool = torch.empty(o, dtype=torch.uint8, device="cuda")
+        t = {name: pool[off:off + nb].view(dt).view(shape) for (name, shape, dt), off, nb in zip(specs, offs, sizes)}
+        g = torch.Generator(device="cuda").manual_seed(0)
+        for k in ("go", "x", "lo", "H"):
+            t[k].normal_(generator=g)
+        t["hp"].uniform_(0, 1, generator=g)
+        t["hq"].uniform_(0, 2, generator=g)
+        launch = {
+            "k3_fwd": lambda: K.k3_fwd(t["x"], t["hp"], t["glo"]),
+            "k3_bwd": lambda: K.k3_bwd(t["lo"], t["x"], t["hp"], t["gx"], t["ghp"]),
+            "k4_fwd": lambda: K.k4_fwd(t["x"], t["lo"], t["H"], t["hq"], t["gx"]),
+            "k4_bwd": lambda: K.k4_bwd(t["go"], t["x"], t["lo"], t["H"], t["hq"], t["gx"], t["glo"], t["gH"],
+                                       t["ghq"]),
+        }
+        row = {}
+        for name, fn in launch.items():
+            fn()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(iters):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            row[name] = round(bm[name] / (e0.elapsed_time(e1) * 1e-3 / iters) / 1e9, 1)
+        out[str(pad)] = row
+        del pool, t, launch
+        torch.cuda.empty_cache()
+    return {"GBps_by_pad_bytes": out,
+            "workload": f"K3/K4 fwd+bwd, T={T}, n=4, C={C}, bf16, tensors back to back in one allocation "
+                        f"with pad bytes between them, {iters} launches per kernel"}
 
 
 def train_stack(T: int, C: int, layers: int = 12, iters: int = 3, warmup: int = 1, compiled: bool = True) -> dict:
@@ -716,11 +771,13 @@ def main() -> None:
                     help="skip the K1-backward and block-step fields (profiler runs: only the six kernels)")
     ap.add_argument("--traffic", type=str, default=str(ROOT / "profiles" / "traffic_k4_bwd_T65536_C1024.json"),
                     help="measured HBM traffic summary (rocprofv3 --pmc) for the dominant kernel")
-    ap.add_argument("--only", choices=("block", "eval", "premap", "premap_bwd", "train"), default=None,
+    ap.add_argument("--only", choices=("block", "eval", "premap", "premap_bwd", "train", "placement"), default=None,
                     help="run one extra alone, fused path only, and print its JSON (profiler runs of the "
                          "block step at --T/--C for --steps iterations, or of the eval latency at --eval-T)")
     ap.add_argument("--layers", type=int, default=12, help="blocks of the --only train stack")
     ap.add_argument("--eager", action="store_true", help="--only train without torch.compile")
+    ap.add_argument("--pads", type=str, default="0,4096,65536,262144,1048576,2097152,3149824",
+                    help="--only placement: bytes between consecutive tensors")
     ap.add_argument("--eval-T", type=str, default="1,64,257,65537", help="token counts of the eval latency")
     args = ap.parse_args()
     if args.n != 4:
@@ -759,6 +816,10 @@ def main() -> None:
     if args.only == "train":
         print(json.dumps({"train_stack": train_stack(args.T, args.C, layers=args.layers, iters=args.steps,
                                                      warmup=args.warmup, compiled=not args.eager)}), flush=True)
+        return
+    if args.only == "placement":
+        pads = tuple(int(p) for p in args.pads.split(","))
+        print(json.dumps({"placement": placement_sweep(args.T, args.C, pads, iters=args.steps)}), flush=True)
         return
     if args.only == "eval":
         print(json.dumps({"eval_latency": eval_latency(tokens=eval_tokens, variants=("fused",))}), flush=True)

@@ -45,7 +45,8 @@ def test_bench_accepts_the_reference_benchmark_command_line():
 def test_bench_accepts_the_extras_command_lines():
     # The profiler runs' flags (--only train and its options among them) parse;
     # without a GPU bench.py stops at the device check.
-    for extra in (["--only", "train", "--layers", "2", "--eager"], ["--only", "premap_bwd"], ["--only", "block"]):
+    for extra in (["--only", "train", "--layers", "2", "--eager"], ["--only", "premap_bwd"], ["--only", "block"],
+                  ["--only", "placement", "--pads", "0,4096"]):
         r = _bench("--T", "4096", "--C", "1024", "--steps", "1", *extra)
         assert r.returncode == 1, (extra, r.stderr)
         assert "needs a GPU" in r.stderr
