@@ -149,6 +149,28 @@ __device__ __forceinline__ void k3_token(const uint16_t* __restrict__ x0, const 
   }
 }
 
+// Residency caps for the K3 / K4 kernels.  They use registers for a few
+// dozen VGPRs, so eight 4-wave workgroups could share a CU; several run
+// faster with fewer (the host's launch reserves LDS the kernel does not use:
+// the CU's 160 KiB hold six workgroups of kLdsCapSix, five of kLdsCapFive).
+// Measured at T = 65536 (GB/s in the six-kernel step, eight workgroups per CU
+// against the cap): K3 forward 6047-6092 against 6344-6405 with six (C =
+// 1024; also 5.60-5.67 against 5.88-5.93 TB/s at T = 262144, C = 4096);
+// K3 backward 6015-6070 against 6123-6175 with five at C = 1024 and
+// 6195-6252 against 6436-6605 at C = 2048; K4 forward 6325-6368 against
+// 6440-6478 with five at C = 1024, 6135-6175 against 6364-6420 at C = 2048.
+// Where a cap lost it is not applied: K3 backward at C = 4096 (5.57 against
+// 5.35-5.41 TB/s at T = 262144) and in the pre-map backward's reduce-only
+// pass (C = 2048: 846 against 862-872 us), and K4 forward with few
+// workgroups per CU (T = 4096, C = 1024: a second round of workgroups).
+// Caps of five for K3 forward or six for K3 backward measured slower than
+// none, so the effect is not simply fewer memory requests in flight.
+#ifndef FMHC_K34_LDS_CAP
+#define FMHC_K34_LDS_CAP 1
+#endif
+constexpr unsigned kLdsCapSix = 24 * 1024;
+constexpr unsigned kLdsCapFive = 32 * 1024;
+
 // Sum over the wave's 64 lanes, every lane receiving the total, with the
 // pairs of group_sum<64>'s butterfly (lanes 32 apart first, then 16, 8, 4,
 // 2, 1), so the same bits, on the VALU's cross-lane moves instead of LDS

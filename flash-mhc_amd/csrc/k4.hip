@@ -349,9 +349,11 @@ int launch_k4_fwd(const uint16_t* x, const uint16_t* lo, const float* H, const f
                   uint16_t* out, int64_t T, int C, hipStream_t s) {
   const int lpt = pick_lpt_fwd<VEC>(C);
   const dim3 grid(blocks_for(T, tokens_per_block(lpt)));
+  // Residency cap (fmhc_common.h) from 16 workgroups per CU on.
+  const unsigned lds = VEC == 8 && FMHC_K34_LDS_CAP && grid.x >= 16u * 256u ? kLdsCapFive : 0u;
   with_lpt(lpt, [&](auto l) {
     constexpr int L = decltype(l)::value;
-    k4_fwd_kernel<VEC, L><<<grid, block_of<L>(), 0, s>>>(x, lo, H, hp, out, T, C);
+    k4_fwd_kernel<VEC, L><<<grid, block_of<L>(), lds, s>>>(x, lo, H, hp, out, T, C);
   });
   return launch_status();
 }
