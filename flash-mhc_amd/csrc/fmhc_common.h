@@ -149,10 +149,11 @@ __device__ __forceinline__ void k3_token(const uint16_t* __restrict__ x0, const 
   }
 }
 
-// Residency caps for the K3 / K4 kernels.  They use registers for a few
-// dozen VGPRs, so eight 4-wave workgroups could share a CU; several run
-// faster with fewer (the host's launch reserves LDS the kernel does not use:
-// the CU's 160 KiB hold six workgroups of kLdsCapSix, five of kLdsCapFive).
+// Residency caps.  The K3 / K4 kernels use a few dozen VGPRs, so eight
+// 4-wave workgroups could share a CU; several run faster with fewer (the
+// host's launch reserves LDS the kernel does not use: the CU's 160 KiB hold
+// six workgroups of kLdsCapSix, five of kLdsCapFive).  K1's backward dx
+// likewise runs faster with one workgroup per CU than with two (k1.hip).
 // Measured at T = 65536 (GB/s in the six-kernel step, eight workgroups per CU
 // against the cap): K3 forward 6047-6092 against 6344-6405 with six (C =
 // 1024; also 5.60-5.67 against 5.88-5.93 TB/s at T = 262144, C = 4096);
@@ -165,11 +166,24 @@ __device__ __forceinline__ void k3_token(const uint16_t* __restrict__ x0, const 
 // workgroups per CU (T = 4096, C = 1024: a second round of workgroups).
 // Caps of five for K3 forward or six for K3 backward measured slower than
 // none, so the effect is not simply fewer memory requests in flight.
-#ifndef FMHC_K34_LDS_CAP
-#define FMHC_K34_LDS_CAP 1
+#ifndef FMHC_LDS_CAP
+#define FMHC_LDS_CAP 1
 #endif
 constexpr unsigned kLdsCapSix = 24 * 1024;
 constexpr unsigned kLdsCapFive = 32 * 1024;
+// One workgroup per CU (K1 backward dx, k1.hip).
+constexpr unsigned kLdsCapOne = 96 * 1024;
+constexpr unsigned kLdsPerCu = 160 * 1024;
+
+// The reserve `dyn` for `kernel` if the kernel's own LDS plus dyn fit in a
+// CU's LDS, else 0 (no cap): a launch asking for more LDS than the CU holds
+// is not refused, and faults.  Callers keep the result in a static of the
+// launch site's kernel instantiation.
+inline unsigned lds_reserve(const void* kernel, unsigned dyn) {
+  hipFuncAttributes a;
+  if (dyn == 0 || hipFuncGetAttributes(&a, kernel) != hipSuccess) return 0u;
+  return a.sharedSizeBytes + dyn <= kLdsPerCu ? dyn : 0u;
+}
 
 // Sum over the wave's 64 lanes, every lane receiving the total, with the
 // pairs of group_sum<64>'s butterfly (lanes 32 apart first, then 16, 8, 4,

@@ -1155,12 +1155,27 @@ void launch_k1_bwd_mfma(hipStream_t s, const uint16_t* x, const uint16_t* W, con
                         int C = 1, const uint16_t* gi = nullptr) {
   const dim3 grid(blocks_for(nruns * nslices, 4));
   constexpr int nbuf = EPI ? kBwdEpiBufs : kBwdBufs;
-  if (nC % 128 == 0)
-    k1_bwd_mfma<DW, true, EPI, GI, nbuf><<<grid, 256, 0, s>>>(x, W, go, proj, inv_rms, gx, partial, go3, h_pre, gi,
-                                                              T, nC, nslices, nruns, C);
-  else
-    k1_bwd_mfma<DW, false, EPI, GI, nbuf><<<grid, 256, 0, s>>>(x, W, go, proj, inv_rms, gx, partial, go3, h_pre,
-                                                               gi, T, nC, nslices, nruns, C);
+  // dx alone: one workgroup per CU (LDS reserved that the kernel does not
+  // use; its registers allow two) up to C = 2560 per stream.  Measured in
+  // the six-kernel step (GB/s, two workgroups per CU against one): T = 65536,
+  // C = 1024 6185-6222 against 6436-6440 (cold 6129 against 6315-6355);
+  // C = 512 5864 against 6162; C = 2560 5599 against 5789; T = 16384 /
+  // 262144, C = 1024 5588 / 6183 against 5724 / 6577; at C = 4096 1-3%
+  // slower (T = 65536 and 262144).  With grad_W it changed nothing
+  // (202.7-203.1 against 201.8-203.3 us at T = 65536, C = 1024).
+  const bool cap = !DW && !EPI && FMHC_LDS_CAP && nC <= 4 * 2560;
+  if (nC % 128 == 0) {
+    static const unsigned lds =
+        lds_reserve(reinterpret_cast<const void*>(&k1_bwd_mfma<DW, true, EPI, GI, nbuf>), kLdsCapOne);
+    k1_bwd_mfma<DW, true, EPI, GI, nbuf><<<grid, 256, cap ? lds : 0u, s>>>(x, W, go, proj, inv_rms, gx, partial,
+                                                                          go3, h_pre, gi, T, nC, nslices, nruns, C);
+  } else {
+    static const unsigned lds =
+        lds_reserve(reinterpret_cast<const void*>(&k1_bwd_mfma<DW, false, EPI, GI, nbuf>), kLdsCapOne);
+    k1_bwd_mfma<DW, false, EPI, GI, nbuf><<<grid, 256, cap ? lds : 0u, s>>>(x, W, go, proj, inv_rms, gx, partial,
+                                                                           go3, h_pre, gi, T, nC, nslices, nruns,
+                                                                           C);
+  }
 }
 
 }  // namespace

@@ -286,9 +286,11 @@ int launch_k3_fwd(const uint16_t* x, const float* h_pre, uint16_t* out, int64_t 
                   hipStream_t s) {
   const int lpt = pick_lpt_fwd<VEC>(C, T);
   const dim3 grid(blocks_for(T, tokens_per_block(lpt)));
-  const unsigned lds = VEC == 8 && FMHC_K34_LDS_CAP ? kLdsCapSix : 0u;  // residency cap (fmhc_common.h)
   with_lpt(lpt, [&](auto l) {
     constexpr int L = decltype(l)::value;
+    // Residency cap (fmhc_common.h).
+    static const unsigned lds =
+        lds_reserve(reinterpret_cast<const void*>(&k3_fwd_kernel<VEC, L>), VEC == 8 && FMHC_LDS_CAP ? kLdsCapSix : 0u);
     k3_fwd_kernel<VEC, L><<<grid, block_of<L>(), lds, s>>>(x, h_pre, out, T, C);
   });
   return launch_status();
@@ -310,16 +312,22 @@ int launch_k3_bwd(const uint16_t* x, const float* h_pre, const uint16_t* go, uin
   const dim3 grid(blocks_for(T, tokens_per_block(lpt)));
   const bool canon = VEC == 8 && k3_canon(C, lpt);
   // Residency cap (fmhc_common.h): with grad_x, up to C = 2048.
-  const unsigned lds = VEC == 8 && GX && FMHC_K34_LDS_CAP && C <= 2048 ? kLdsCapFive : 0u;
+  const unsigned cap = VEC == 8 && GX && FMHC_LDS_CAP && C <= 2048 ? kLdsCapFive : 0u;
   with_lpt(lpt, [&](auto l) {
     constexpr int L = decltype(l)::value;
     if constexpr (VEC == 8 && L >= 16) {
       if (canon) {
-        k3_bwd_kernel<VEC, L, GX, true><<<grid, block_of<L>(), lds, s>>>(x, h_pre, go, grad_x, grad_h_pre, T, C);
+        static const unsigned lds =
+            lds_reserve(reinterpret_cast<const void*>(&k3_bwd_kernel<VEC, L, GX, true>), kLdsCapFive);
+        k3_bwd_kernel<VEC, L, GX, true><<<grid, block_of<L>(), cap ? lds : 0u, s>>>(x, h_pre, go, grad_x,
+                                                                                  grad_h_pre, T, C);
         return;
       }
     }
-    k3_bwd_kernel<VEC, L, GX, false><<<grid, block_of<L>(), lds, s>>>(x, h_pre, go, grad_x, grad_h_pre, T, C);
+    static const unsigned lds =
+        lds_reserve(reinterpret_cast<const void*>(&k3_bwd_kernel<VEC, L, GX, false>), kLdsCapFive);
+    k3_bwd_kernel<VEC, L, GX, false><<<grid, block_of<L>(), cap ? lds : 0u, s>>>(x, h_pre, go, grad_x, grad_h_pre,
+                                                                               T, C);
   });
   return launch_status();
 }

@@ -350,10 +350,11 @@ int launch_k4_fwd(const uint16_t* x, const uint16_t* lo, const float* H, const f
   const int lpt = pick_lpt_fwd<VEC>(C);
   const dim3 grid(blocks_for(T, tokens_per_block(lpt)));
   // Residency cap (fmhc_common.h) from 16 workgroups per CU on.
-  const unsigned lds = VEC == 8 && FMHC_K34_LDS_CAP && grid.x >= 16u * 256u ? kLdsCapFive : 0u;
+  const bool cap = VEC == 8 && FMHC_LDS_CAP && grid.x >= 16u * 256u;
   with_lpt(lpt, [&](auto l) {
     constexpr int L = decltype(l)::value;
-    k4_fwd_kernel<VEC, L><<<grid, block_of<L>(), lds, s>>>(x, lo, H, hp, out, T, C);
+    static const unsigned lds = lds_reserve(reinterpret_cast<const void*>(&k4_fwd_kernel<VEC, L>), kLdsCapFive);
+    k4_fwd_kernel<VEC, L><<<grid, block_of<L>(), cap ? lds : 0u, s>>>(x, lo, H, hp, out, T, C);
   });
   return launch_status();
 }

@@ -68,11 +68,11 @@ SOURCE_FLAGS = {"k1.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 # tile from HBM instead of the memory-side cache.  premap_reread: the forward's
 # tile kernel instead of the single read.  premap_bwd_split: the pre-map
 # backward with one read of x (premap_split.hip) instead of K3's reduce pass,
-# K2 and K1.  k34_no_cap: K3 and K4 launched without the residency caps of
-# fmhc_common.h.
+# K2 and K1.  no_lds_cap: K1's backward dx, K3 and K4 launched without the
+# residency caps of fmhc_common.h.
 VARIANTS = {"k1_valu": ["-DFMHC_K1_VALU=1"], "premap_three_kernels": ["-DFMHC_PREMAP_TILE=0"],
             "premap_tile_nt": ["-DFMHC_PREMAP_TILE_NT=1"], "premap_reread": ["-DFMHC_PREMAP_RESIDENT=0"],
-            "premap_bwd_split": ["-DFMHC_PREMAP_SPLIT=1"], "k34_no_cap": ["-DFMHC_K34_LDS_CAP=0"]}
+            "premap_bwd_split": ["-DFMHC_PREMAP_SPLIT=1"], "no_lds_cap": ["-DFMHC_LDS_CAP=0"]}
 
 
 def variant_path(name: str) -> Path:
