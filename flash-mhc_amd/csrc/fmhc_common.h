@@ -171,6 +171,7 @@ __device__ __forceinline__ void k3_token(const uint16_t* __restrict__ x0, const 
 #endif
 constexpr unsigned kLdsCapSix = 24 * 1024;
 constexpr unsigned kLdsCapFive = 32 * 1024;
+constexpr unsigned kLdsCapFour = 40 * 1024;  // K4 backward, one group per lane (k4.hip)
 // One workgroup per CU (K1 backward dx, k1.hip).
 constexpr unsigned kLdsCapOne = 96 * 1024;
 constexpr unsigned kLdsPerCu = 160 * 1024;

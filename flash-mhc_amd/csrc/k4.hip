@@ -337,10 +337,16 @@ int pick_lpt_fwd(int C) {
 
 // Backward: a workgroup per token from C = 2048 on (the 20 per-token sums
 // then finish across the waves in LDS): 13% faster there than one wave per
-// token at T x C = 64 Mi elements; at C = 1024 two waves per token gain
-// under 1%, so one wave stays the choice below C = 2048.
+// token at T x C = 64 Mi elements.  At C = 1024 two waves per token (one
+// 16-byte group per lane) with the residency cap of launch_k4_bwd: at
+// T = 65536 6389-6454 against 6270-6291 GB/s in the six-kernel step, 32768
+// 6298-6330 against 6149-6150, 20000 6071-6121 against 5999-6008, 262144
+// 6298-6369 against 6145-6233; below the cap's threshold two waves were
+// already 1-4 us faster (T = 4096 22.1 -> 21.0 us).  Other widths below
+// 2048 keep one wave (a second wave would leave lanes without a group).
 template <int VEC>
 int pick_lpt_bwd(int C) {
+  if (VEC == 8 && C / VEC == 128) return 128;
   return C / VEC >= 256 ? wide_lpt<VEC>(C / VEC) : pick_lpt<VEC>(C);
 }
 
@@ -367,6 +373,15 @@ int launch_k4_bwd(const uint16_t* x, const uint16_t* lo, const float* H, const f
                   int64_t T, int C, hipStream_t s) {
   const int lpt = pick_lpt_bwd<VEC>(C);
   const dim3 grid(blocks_for(T, tokens_per_block(lpt)));
+  // Residency cap (fmhc_common.h): four workgroups per CU where each lane
+  // has one 16-byte group (C = 512, 1024, 2048), from 16 workgroups per CU
+  // on.  Six-kernel step, GB/s for K4 backward, no cap against four:
+  // T = 65536, C = 512 6401-6416 against 6448-6455, C = 2048 6139-6169
+  // against 6387-6395 (cold 6127-6155 against 6426-6467); T = 262144,
+  // C = 512 6278-6295 against 6452-6485.  With two groups per lane a cap
+  // lost (C = 1024 on one wave per token: 5949-5969 against 6242-6249;
+  // C = 4096: 4742 against 5624); at C = 2560 and 3072 it changed nothing.
+  const bool cap = VEC == 8 && FMHC_LDS_CAP && C / VEC == lpt && lpt <= 256 && grid.x >= 16u * 256u;
   // Few waves (up to 64 per CU): each iteration's loads go out before its
   // stores, so a wave waits for one round trip per iteration instead of five
   // (block step at C = 1024, HIP graph: T = 1024 96.5 -> 94.6 us, 6000 232.2
@@ -378,8 +393,10 @@ int launch_k4_bwd(const uint16_t* x, const uint16_t* lo, const float* H, const f
     constexpr bool E = decltype(early)::value;
     with_lpt(lpt, [&](auto l) {
       constexpr int L = decltype(l)::value;
-      k4_bwd_kernel<VEC, L, E && L >= kWave><<<grid, block_of<L>(), 0, s>>>(x, lo, H, hp, go, gx, glo, gH, ghp, T,
-                                                                            C);
+      static const unsigned lds =
+          lds_reserve(reinterpret_cast<const void*>(&k4_bwd_kernel<VEC, L, E && L >= kWave>), kLdsCapFour);
+      k4_bwd_kernel<VEC, L, E && L >= kWave><<<grid, block_of<L>(), cap ? lds : 0u, s>>>(x, lo, H, hp, go, gx, glo,
+                                                                                         gH, ghp, T, C);
     });
   };
   // Measured on the 16-byte path with a wave or more per token; narrower

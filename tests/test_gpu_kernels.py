@@ -304,11 +304,12 @@ def test_k4_bwd(T, C):
     check_fp32("k4 grad_hp", ghp, *ref["grad_hp"], C)
 
 
-@pytest.mark.parametrize("n,C", [(16384, 1024), (4096, 4096)])
+@pytest.mark.parametrize("n,C", [(8192, 1024), (4096, 4096), (16384, 512)])
 def test_k4_bwd_early_and_late_loads_agree(n, C):
     """K4's backward issues each iteration's loads before its stores up to
-    16384 tokens x 64 lanes (n tokens here) and keeps the plain loop above:
-    the same arithmetic in the same order, so the first n tokens of an
+    16384 tokens x 64 lanes (n tokens x the lanes per token here: 128 at
+    C = 1024, 256 at 4096, 64 at 512) and keeps the plain loop above: the
+    same arithmetic in the same order, so the first n tokens of an
     (n + 1)-token call equal an n-token call bit for bit."""
     x, lo, H, hp = (t.to(DEV) for t in _k4_inputs(n + 1, C, 97))
     go = randn((n + 1, 4, C), 98).to(DEV)
