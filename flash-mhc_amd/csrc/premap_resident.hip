@@ -16,15 +16,18 @@
 // Layout.  Four waves per workgroup (one per SIMD, up to 512 registers each);
 // wave w owns columns w CPW .. + CPW of each of the four streams (CPW = C / 4),
 // i.e. KS = C / 32 k-steps of the 16x16x32 MFMA.  A block is held as two
-// halves of KS / 2 k-steps, each half the same pieces of all four streams
-// (col_of below); for a k-step over 32 columns c0 .. c0 + 32 of stream j, lane
-// l holds
-//   x  (MFMA B):  x[t0 + (l & 15), j, c0 + 8 (l >> 4) + e]
-//   W  (MFMA A):  W[d, j C + c0 + 8 (l >> 4) + e], d = l & 15 and 16 + (l & 15)
-// so every lane holds the same token and columns of all four streams: K3 is
-// lane-local, with k3_token's arithmetic.  The sum of squares is the diagonal
-// of x x^T, a third MFMA on the same registers (exact bf16 products, fp32
-// sums), as in K1's one-pass kernel.  The waves' partial sums are added in
+// halves of KS / 2 k-steps, each half the same 64-column chunks of all four
+// streams.  x arrives as whole 128-byte lines: for chunk c0 .. c0 + 64 of
+// stream j, one load gives lane l
+//   x[t0 + (l >> 3), j, c0 + 8 (l & 7) + e]   (tokens 0-7; a second load 8-15)
+// so every lane holds the same tokens and columns of all four streams: K3 is
+// lane-local, with k3_token's arithmetic, and its stores are whole lines too.
+// For K1 the two loads go through a wave-private LDS tile (swizzled, free of
+// bank conflicts) into the MFMA layout of the chunk's two k-steps:
+//   x  (MFMA B):  x[t0 + (l & 15), j, c0 + 32 s + 8 (l >> 4) + e]
+//   W  (MFMA A):  W[d, j C + c0 + 32 s + 8 (l >> 4) + e], d = l & 15 and 16 + (l & 15)
+// The sum of squares is the diagonal of x x^T, a third MFMA on the same
+// operands (exact bf16 products, fp32 sums), as in K1's one-pass kernel.  The waves' partial sums are added in
 // wave order through LDS.  K2 runs 16 lanes per token (k2_token16_lds: the
 // chain's bits, its cross-lane values exchanged through LDS), and the block's
 // K1 / K2 outputs are staged in LDS and stored as whole 16-byte pieces of
@@ -34,6 +37,12 @@
 // Outputs: proj, inv_rms, h_pre, h_post, H_merged and the layer input, the
 // values of K1 -> K2 -> K3 up to K1's fp32 summation order (this kernel
 // partitions the contraction over four waves of C columns each).
+//
+// Loading x in the MFMA layout directly (16 tokens x 64 bytes per load, two
+// loads per line) took 150-153 us at T = 65536, C = 1024 against 145-146 us
+// with whole lines and the LDS tile (C = 512: 86 against 84 us), with the same
+// bits; with half lines the nontemporal hint cost 14% (each half fetched on
+// its own), with whole lines it gained nothing.
 //
 // Measured at T = 65536 (each launch after a cache flush): C = 1024 149 us
 // against 174 us for the tile kernel that re-reads x and 205 us for three
@@ -219,12 +228,15 @@ __global__ __launch_bounds__(NW * kWave) void premap_resident_fwd(const uint16_t
   constexpr int NC = 4 * C;
   constexpr int NT = NW * kWave;
   __shared__ ResidentSmem<NW, KS, KR> sm;
+  __shared__ u32x4 xt[NW][16 * 8];  // per wave: a chunk's 16 tokens x 8 swizzled 16-byte slots
 
   const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
   const int row = lane & 15;
   const int grp = lane >> 4;
   const int cbase = wave * CPW + 8 * grp;  // the lane's column within each stream, piece 0
+  const int lt = lane >> 3, ls = lane & 7;  // line layout: token lt (and 8 + lt), 16-byte slot ls
+  const int ccol = wave * CPW + 8 * ls;
 
   const int64_t nblocks = (T + 15) / 16;
   const int64_t g0 = blockIdx.x;
@@ -269,13 +281,23 @@ __global__ __launch_bounds__(NW * kWave) void premap_resident_fwd(const uint16_t
   // same loads in flight and the compiler's in-order wait counts stay exact
   // (with a conditional prefetch the wait for a block also waited for the
   // next one's loads).
+  constexpr int PPH = HH / 2;  // 64-column chunks per stream in a half
+  static_assert(HH % 2 == 0, "whole 64-column chunks");
+  // Register q of a half: stream q / (2 PPH), chunk (q / 2) % PPH of the
+  // half, tokens 0-7 (q even) or 8-15 (q odd).
   auto load_half = [&](u32x4 (&X)[NP], int i, int half) __attribute__((always_inline)) {
     const int ic = i < nb ? i : nb - 1;
     const int64_t t0 = (g0 + static_cast<int64_t>(ic) * G) * 16;
-    const int64_t t = t0 + row < T ? t0 + row : T - 1;
-    const uint16_t* base = x + t * NC + cbase;
+    const int64_t ta = t0 + lt < T ? t0 + lt : T - 1;
+    const int64_t tb = t0 + 8 + lt < T ? t0 + 8 + lt : T - 1;
+    const uint16_t* pa = x + ta * NC + ccol;
+    const uint16_t* pb = x + tb * NC + ccol;
 #pragma unroll
-    for (int q = 0; q < NP; ++q) X[q] = *reinterpret_cast<const u32x4*>(base + col_of(half * NP + q));
+    for (int q = 0; q < NP; ++q) {
+      const int j = q / (2 * PPH), pp = (q / 2) % PPH, th = q % 2;
+      const int off = j * C + 64 * (PPH * half + pp);
+      X[q] = *reinterpret_cast<const u32x4*>((th ? pb : pa) + off);
+    }
   };
 
   // Three half-block buffers in rotation: block i's halves are loaded one
@@ -304,15 +326,36 @@ __global__ __launch_bounds__(NW * kWave) void premap_resident_fwd(const uint16_t
     const int64_t t0 = (g0 + static_cast<int64_t>(i) * G) * 16;
     // K1: this wave's share of the 32 projections and of the sum of squares.
     f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0, gm = a0;
+    // Chunk by chunk through the wave's tile (slot s of token t at
+    // 8 t + (s ^ ((t >> 1) & 7))); same-wave LDS operations complete in
+    // order, so the tile needs no barrier.  The k-steps run in the order
+    // q = 0 .. KS - 1 of the W registers.
+    u32x4* tile = xt[wave];
+    const int wlo = lt * 8 + (ls ^ ((lt >> 1) & 7));
+    const int whi = (8 + lt) * 8 + (ls ^ (((8 + lt) >> 1) & 7));
+    const int rd0 = row * 8 + (grp ^ ((row >> 1) & 7));
+    const int rd1 = row * 8 + ((4 + grp) ^ ((row >> 1) & 7));
 #pragma unroll
-    for (int q = 0; q < KS; ++q) {
-      const u32x4 xq = q < NP ? A[q < NP ? q : 0] : B[q < NP ? 0 : q - NP];
-      const u32x4 wa = q < KR ? wr[q < KR ? q : 0][0] : sm.w[wave][q < KR ? 0 : q - KR][0][lane];
-      const u32x4 wb = q < KR ? wr[q < KR ? q : 0][1] : sm.w[wave][q < KR ? 0 : q - KR][1][lane];
-      a0 = mfma(wa, xq, a0);
-      a1 = mfma(wb, xq, a1);
-      gm = mfma(xq, xq, gm);
-    }
+    for (int half = 0; half < 2; ++half)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int pp = 0; pp < PPH; ++pp) {
+          const int r0 = j * 2 * PPH + 2 * pp;
+          tile[wlo] = half ? B[r0] : A[r0];
+          tile[whi] = half ? B[r0 + 1] : A[r0 + 1];
+          const u32x4 xs0 = tile[rd0], xs1 = tile[rd1];
+#pragma unroll
+          for (int sub = 0; sub < 2; ++sub) {
+            const u32x4 xq = sub ? xs1 : xs0;
+            const int q = half * NP + j * HH + 2 * pp + sub;
+            const u32x4 wa = q < KR ? wr[q < KR ? q : 0][0] : sm.w[wave][q < KR ? 0 : q - KR][0][lane];
+            const u32x4 wb = q < KR ? wr[q < KR ? q : 0][1] : sm.w[wave][q < KR ? 0 : q - KR][1][lane];
+            a0 = mfma(wa, xq, a0);
+            a1 = mfma(wb, xq, a1);
+            gm = mfma(xq, xq, gm);
+          }
+        }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       sm.u.r.red[wave][r][lane] = a0[r];
@@ -386,31 +429,36 @@ __global__ __launch_bounds__(NW * kWave) void premap_resident_fwd(const uint16_t
     // K3 on the rows still in registers, a half at a time: once a half is
     // mixed its registers take the next loads (block i + 1's second half,
     // then block i + 2's first half), so those are issued a half earlier.
-    const int64_t t = t0 + row;
-    const bool tv = t < T;
-    const float h0 = sm.hp[row][0], h1 = sm.hp[row][1], h2 = sm.hp[row][2], h3 = sm.hp[row][3];
-    uint16_t* orow = pt.layer_input + (tv ? t : 0) * C + cbase;
-    // Piece HH half + p of the four streams: k-steps HH j + p of that half.
+    const int64_t ta = t0 + lt, tb = t0 + 8 + lt;
+    const bool va = ta < T, vb = tb < T;
+    float hh[2][4];
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      hh[0][jj] = sm.hp[lt][jj];
+      hh[1][jj] = sm.hp[8 + lt][jj];
+    }
+    uint16_t* oa = pt.layer_input + (va ? ta : 0) * C + ccol;
+    uint16_t* ob = pt.layer_input + (vb ? tb : 0) * C + ccol;
     auto mix = [&](const u32x4 (&X)[NP], int half) __attribute__((always_inline)) {
 #pragma unroll
-      for (int p = 0; p < HH; ++p) {
+      for (int p2 = 0; p2 < 2 * PPH; ++p2) {
+        const int pp = p2 / 2, th = p2 % 2;
         float a[8], b[8], c[8], d[8], o[8];
-        unpack8(X[p], a);
-        unpack8(X[HH + p], b);
-        unpack8(X[2 * HH + p], c);
-        unpack8(X[3 * HH + p], d);
+        unpack8(X[0 * 2 * PPH + p2], a);
+        unpack8(X[1 * 2 * PPH + p2], b);
+        unpack8(X[2 * 2 * PPH + p2], c);
+        unpack8(X[3 * 2 * PPH + p2], d);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          float acc = h0 * a[e];
-          acc = __builtin_fmaf(h1, b[e], acc);
-          acc = __builtin_fmaf(h2, c[e], acc);
-          o[e] = __builtin_fmaf(h3, d[e], acc);
+          float acc = hh[th][0] * a[e];
+          acc = __builtin_fmaf(hh[th][1], b[e], acc);
+          acc = __builtin_fmaf(hh[th][2], c[e], acc);
+          o[e] = __builtin_fmaf(hh[th][3], d[e], acc);
         }
-        // Ordinary stores: each instruction writes half of 16 lines (64 of
-        // 128 bytes per row) and the next one the other half; L2 merges the
-        // two before writing back, where with the nontemporal hint about
-        // half the lines went out twice (WRITE_SIZE 1.44 x).
-        if (tv) *reinterpret_cast<u32x4*>(orow + 32 * (HH * half + p)) = pack8(o);
+        // Whole lines, ordinary stores (the nontemporal hint measured the
+        // same or slower).
+        uint16_t* dst = (th ? ob : oa) + 64 * (PPH * half + pp);
+        if (th ? vb : va) *reinterpret_cast<u32x4*>(dst) = pack8(o);
       }
     };
     mix(A, 0);
