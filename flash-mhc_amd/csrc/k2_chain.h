@@ -72,23 +72,34 @@ __device__ __forceinline__ void stage_params(const K2Params& P, K2Smem& sm) {
 
 // stage_params in two halves, so that a kernel can issue the parameter loads
 // early and store them to LDS later, before a barrier of its own: the same
-// values in the same places.
+// values in the same places.  The loads keep the raw parameter words and the
+// conversion waits for store(), so issuing them does not wait for them.
+__device__ __forceinline__ uint32_t ld_param_raw(const void* p, int i, bool bf16) {
+  return bf16 ? static_cast<uint32_t>(static_cast<const uint16_t*>(p)[i]) : static_cast<const uint32_t*>(p)[i];
+}
+
+__device__ __forceinline__ float param_value(uint32_t raw, bool bf16) {
+  return rb(__uint_as_float(bf16 ? raw << 16 : raw));  // ld_param's value, rounded as stage_params does
+}
+
 template <int THREADS>
 struct K2ParamRegs {
   static constexpr int kPerm = (kNF * kN * kN + THREADS - 1) / THREADS;
-  float perm[kPerm];
-  float sc = 0.f;
+  uint32_t perm[kPerm];
+  uint32_t sc = 0;
+  bool bf16 = false;
 
   __device__ __forceinline__ void load(const K2Params& P) {
+    bf16 = P.bf16;
 #pragma unroll
     for (int r = 0; r < kPerm; ++r) {
       const int i = static_cast<int>(threadIdx.x) + r * THREADS;
-      perm[r] = i < kNF * kN * kN ? rb(ld_param(P.perm, i, P.bf16)) : 0.f;
+      perm[r] = i < kNF * kN * kN ? ld_param_raw(P.perm, i, P.bf16) : 0u;
     }
     const int i = static_cast<int>(threadIdx.x);
     if (i < 3 + kDk) {
       const void* src = i == 0 ? P.alpha_pre : (i == 1 ? P.alpha_post : (i == 2 ? P.alpha_res : P.bias));
-      sc = rb(ld_param(src, i < 3 ? 0 : i - 3, P.bf16));
+      sc = ld_param_raw(src, i < 3 ? 0 : i - 3, P.bf16);
     }
   }
   __device__ __forceinline__ void store(K2Smem& sm) const {
@@ -96,9 +107,9 @@ struct K2ParamRegs {
 #pragma unroll
     for (int r = 0; r < kPerm; ++r) {
       const int i = static_cast<int>(threadIdx.x) + r * THREADS;
-      if (i < kNF * kN * kN) pf[i] = perm[r];
+      if (i < kNF * kN * kN) pf[i] = param_value(perm[r], bf16);
     }
-    if (threadIdx.x < 3 + kDk) sm.sc[threadIdx.x] = sc;
+    if (threadIdx.x < 3 + kDk) sm.sc[threadIdx.x] = param_value(sc, bf16);
   }
 };
 

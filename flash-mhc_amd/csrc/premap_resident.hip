@@ -44,15 +44,14 @@
 // bits; with half lines the nontemporal hint cost 14% (each half fetched on
 // its own), with whole lines it gained nothing.
 //
-// Measured at T = 65536 (each launch after a cache flush): C = 1024 149 us
+// Measured at T = 65536 (each launch after a cache flush): C = 1024 136-139 us
 // against 174 us for the tile kernel that re-reads x and 205 us for three
 // kernels, 1.04x the region's algorithmic bytes past L2 against 1.74x;
-// C = 512 86 against 94 us; T = 131072, C = 1024: 283 against 331 us.
-// The memory floor of the same loads and stores without
-// any arithmetic is 121-124 us at C = 1024: W (256 KiB) and one and a half
-// blocks of rows (192 KiB) fill the CU's registers and LDS, so the second
-// half of each block is issued only once the previous block is mixed, and
-// every step waits about one memory latency for it.
+// C = 512 78-79 against 94 us; T = 131072, C = 1024: 258 against 331 us.
+// W (256 KiB) and one and a half blocks of rows (192 KiB) fill the CU's
+// registers and LDS, so a block's second half is issued only once the
+// previous block's first half is mixed, and the K1 phase that needs it
+// waits for it.
 
 #include <hip/hip_runtime.h>
 
@@ -62,7 +61,6 @@
 
 namespace fmhc {
 namespace {
-
 
 __device__ __forceinline__ bf16x8 as_bf(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
@@ -255,9 +253,11 @@ __global__ __launch_bounds__(NW * kWave) void premap_resident_fwd(const uint16_t
     return j * C + 32 * (HH * half + p);
   };
 
-  // W, loaded once: k-steps below KR stay in registers, the others go to LDS.
-  // Their loads are issued before the first blocks of x, so waiting for them
-  // does not wait for x.
+  // K2's parameters first, then W, loaded once: k-steps below KR stay in
+  // registers, the others go to LDS.  Their loads are issued before the
+  // first blocks of x, so waiting for them does not wait for x.
+  K2ParamRegs<NT> prm;
+  prm.load(pt.P);
   u32x4 wr[KR > 0 ? KR : 1][2];
   u32x4 wl[KS > KR ? KS - KR : 1][2];
 #pragma unroll
@@ -300,29 +300,35 @@ __global__ __launch_bounds__(NW * kWave) void premap_resident_fwd(const uint16_t
     }
   };
 
-  // Three half-block buffers in rotation: block i's halves are loaded one
-  // and two steps ahead, so while a block is reduced, mixed and stored about
-  // one block of loads is in flight.
+  // Three half-block buffers in rotation.  Block i + 1's second half is
+  // loaded once block i's first half is mixed, its first half once block i's
+  // K1 phase is done: that phase then waits only for block i's second half,
+  // which is alone in flight.  Loading the first half two steps ahead instead
+  // (when block i - 1's second half is mixed) shares the bandwidth between
+  // the half that phase waits for and one it does not need yet.  Measured at
+  // T = 65536, each launch after a cache flush: C = 1024 136-139 against
+  // 143-146 us, C = 512 78-79 against 80-84 us; T = 32768 and 131072 at
+  // C = 1024: 76.4 against 81.5 us, 258 against 274 us.
   u32x4 H0[NP], H1[NP], H2[NP];
   __builtin_amdgcn_sched_barrier(0);  // W's loads first: waiting for them does not wait for x
   load_half(H0, 0, 0);  // nb >= 1: the grid has at most one workgroup per block
   load_half(H1, 0, 1);
-  __builtin_amdgcn_sched_barrier(0);
-  load_half(H2, 1, 0);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int q = KR; q < KS; ++q) {
     sm.w[wave][q - KR][0][lane] = wl[q - KR][0];
     sm.w[wave][q - KR][1][lane] = wl[q - KR][1];
   }
-  stage_params<NT>(pt.P, sm.k2);  // ends with a barrier
+  prm.store(sm.k2);
+  __syncthreads();
   {
     const float* pf = reinterpret_cast<const float*>(sm.k2.perm);  // perm[m][r], 24 x 16
     for (int i = threadIdx.x; i < kNF * kN * kN; i += NT) sm.permT[i % (kN * kN)][i / (kN * kN)] = pf[i];
   }  // read after the first block's barriers
 
-  // Block i with streams 0-1 in A and streams 2-3 in B.
-  auto step = [&](u32x4 (&A)[NP], u32x4 (&B)[NP], int i) __attribute__((always_inline)) {
+  // Block i with its first half in A and its second half in B; D is free
+  // until the step loads block i + 1's first half into it.
+  auto step = [&](u32x4 (&A)[NP], u32x4 (&B)[NP], u32x4 (&D)[NP], int i) __attribute__((always_inline)) {
     const int64_t t0 = (g0 + static_cast<int64_t>(i) * G) * 16;
     // K1: this wave's share of the 32 projections and of the sum of squares.
     f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0, gm = a0;
@@ -363,6 +369,10 @@ __global__ __launch_bounds__(NW * kWave) void premap_resident_fwd(const uint16_t
     }
     // The diagonal G[row][row] sits in lane row + 16 (row >> 2), register row & 3.
     if (grp == (row >> 2)) sm.u.r.red_ss[wave][row] = gm[row & 3];
+    // Block i + 1's first half, now that the loads in flight are none but
+    // its second half's.
+    load_half(D, i + 1, 0);
+    __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
     // Thread (r, l) adds D element r of lane l over the waves, in wave order:
     // projection d = 4 (l >> 4) + (r & 3) + 16 (r >> 2) of token l & 15.
@@ -465,18 +475,22 @@ __global__ __launch_bounds__(NW * kWave) void premap_resident_fwd(const uint16_t
     load_half(A, i + 1, 1);
     __builtin_amdgcn_sched_barrier(0);  // all of block i + 1 before block i + 2 (in-order wait counts)
     mix(B, 1);
-    load_half(B, i + 2, 0);
-    __builtin_amdgcn_sched_barrier(0);
   };
 
-  // Block i in (H[2i % 3], H[(2i + 1) % 3]); its step reloads both halves
-  // with block i + 1's second half and block i + 2's first half.
-  for (int i = 0; i < nb; i += 3) {
-    step(H0, H1, i);
-    if (i + 1 >= nb) break;
-    step(H2, H0, i + 1);
-    if (i + 2 >= nb) break;
-    step(H1, H2, i + 2);
+  // Block i in (H[2i % 3], H[(2i + 1) % 3]).  The loop body has no exit
+  // between its steps: with a `break` after a step, the reload issued there
+  // was dead on that path, and hipcc (ROCm 7.2) sank it into the next step,
+  // where the scheduler placed it after that step's K1 phase, which then
+  // waited for it.  The last one or two blocks run after the loop.
+  int i = 0;
+  for (; i + 3 <= nb; i += 3) {
+    step(H0, H1, H2, i);
+    step(H2, H0, H1, i + 1);
+    step(H1, H2, H0, i + 2);
+  }
+  if (i < nb) {
+    step(H0, H1, H2, i);
+    if (i + 1 < nb) step(H2, H0, H1, i + 1);
   }
 }
 
