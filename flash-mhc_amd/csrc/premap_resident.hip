@@ -47,7 +47,7 @@
 // Measured at T = 65536 (each launch after a cache flush): C = 1024 136-139 us
 // against 174 us for the tile kernel that re-reads x and 205 us for three
 // kernels, 1.04x the region's algorithmic bytes past L2 against 1.74x;
-// C = 512 78-79 against 94 us; T = 131072, C = 1024: 258 against 331 us.
+// C = 512 72-73 against 94 us; T = 131072, C = 1024: 258 against 331 us.
 // W (256 KiB) and one and a half blocks of rows (192 KiB) fill the CU's
 // registers and LDS, so a block's second half is issued only once the
 // previous block's first half is mixed, and the K1 phase that needs it
@@ -103,67 +103,16 @@ struct ResidentSmem {
   K2Smem k2;
 };
 
-// K2 forward of token tt on lanes q = 0..31 of a 32-lane group (p: the
-// token's projection q as a bf16 value): k2_token32's operations in its
-// order -- logit q, the maximum over the softmax logits, the softmax
-// denominator added over m = 0..23, weight q - 8, H_res entry q & 15 added
-// over m = 0..23, H_merged -- with the values other lanes hold read from LDS
-// instead of shuffled, so the results are k2_token32's (and the chain's) bit
-// for bit.  Outputs go to the block's staging area; returns the lane's
-// sigmoid value (h_pre[q] for q < 4).
-__device__ __forceinline__ float k2_token32_lds(const K2Smem& k2, const float (&permT)[kN * kN][kNF], K2Xchg& xc,
-                                                K2Out& out, float* hp_out, int tt, int q, float p) {
-#pragma clang fp contract(off)
-  const float alpha = q < kN ? k2.sc[0] : (q < 2 * kN ? k2.sc[1] : k2.sc[2]);
-  const float z = rb(rb(alpha * p) + k2.sc[3 + q]);
-  const float y = q < 2 * kN ? rb(sigmoid_f32(z)) : 0.f;  // h_pre (q < 4), sigmoid of the post logit
-  const float hq = rb(2.f * y);                             // h_post for 4 <= q < 8
-  float mx = q >= 2 * kN ? z : -INFINITY;
-#pragma unroll
-  for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 32));
-  const float e = q >= 2 * kN ? expf(z - mx) : 0.f;
-  if (q >= 2 * kN) xc.e[tt][q - 2 * kN] = e;
-  if (q < 2 * kN) xc.y[tt][q] = q < kN ? y : hq;
-  // The group is one wave's half: its LDS writes above precede these reads.
-  const f32x4* ev = reinterpret_cast<const f32x4*>(xc.e[tt]);
-  float sum = 0.f;
-#pragma unroll
-  for (int m4 = 0; m4 < kNF / 4; ++m4) {
-    const f32x4 v = ev[m4];
-    sum = sum + v[0];
-    sum = sum + v[1];
-    sum = sum + v[2];
-    sum = sum + v[3];
-  }
-  const float a = rb(e / sum);
-  if (q >= 2 * kN) xc.a[tt][q - 2 * kN] = a;
-  const int r = q & 15;
-  const f32x4* av = reinterpret_cast<const f32x4*>(xc.a[tt]);
-  const f32x4* pv = reinterpret_cast<const f32x4*>(permT[r]);
-  float acc = 0.f;
-#pragma unroll
-  for (int m4 = 0; m4 < kNF / 4; ++m4) {
-    const f32x4 am = av[m4], pm = pv[m4];
-    acc = acc + am[0] * pm[0];
-    acc = acc + am[1] * pm[1];
-    acc = acc + am[2] * pm[2];
-    acc = acc + am[3] * pm[3];
-  }
-  const float hp_j = xc.y[tt][q & 3];
-  const float hq_i = xc.y[tt][kN + (r >> 2)];
-  if (q < kN * kN) out.H[tt][q] = rb(rb(acc) - rb(hq_i * hp_j));
-  if (q < kN)
-    hp_out[q] = y;
-  else if (q < 2 * kN)
-    out.hq[tt][q - kN] = hq;
-  return y;
-}
-
-// The same with 16 lanes per token, so that four waves take a block's 16
-// tokens at once: lane r (0-15) computes logits r and 16 + r (r < 4: h_pre,
-// r < 8: h_post, otherwise softmax terms r - 8 and 8 + r), and H_res /
-// H_merged entry r.  Every value is k2_token32's expression in its order;
-// p0 / p1 are projections r and 16 + r as bf16 values.
+// K2 forward of token tt with 16 lanes per token, so that four waves take a
+// block's 16 tokens at once: lane r (0-15) computes logits r and 16 + r
+// (r < 4: h_pre, r < 8: h_post, otherwise softmax terms r - 8 and 8 + r),
+// and H_res / H_merged entry r.  Every value is k2_token32's expression in its
+// order (logits, the maximum over the softmax logits, the softmax denominator
+// added over m = 0..23, the weights, H_res added over m = 0..23, H_merged),
+// with the values other lanes hold read from LDS instead of shuffled, so the
+// results are the chain's bit for bit.  p0 / p1 are projections r and 16 + r
+// as bf16 values.  Outputs go to the block's staging area, and h_pre to
+// hp_out unless it is null.
 __device__ __forceinline__ void k2_token16_lds(const K2Smem& k2, const float (&permT)[kN * kN][kNF], K2Xchg& xc,
                                                K2Out& out, float* hp_out, int tt, int r, float p0, float p1) {
 #pragma clang fp contract(off)
@@ -207,19 +156,27 @@ __device__ __forceinline__ void k2_token16_lds(const K2Smem& k2, const float (&p
   const float hp_j = xc.y[tt][r & 3];
   const float hq_i = xc.y[tt][kN + (r >> 2)];
   out.H[tt][r] = rb(rb(acc) - rb(hq_i * hp_j));
-  if (r < kN)
-    hp_out[r] = y;
-  else if (r < 2 * kN)
+  if (r < kN) {
+    if (hp_out) hp_out[r] = y;
+  } else if (r < 2 * kN) {
     out.hq[tt][r - kN] = hq;
+  }
 }
 
-template <int NW, int KS, int KR>
+// h_pre alone, on lanes r < 4 of the token's 16: k2_token16_lds's first
+// operations for those lanes, so the same bits.  K3 needs nothing else of K2.
+__device__ __forceinline__ void k2_hpre16(const K2Smem& k2, float* hp_out, int r, float p0) {
+#pragma clang fp contract(off)
+  if (r < kN) hp_out[r] = rb(sigmoid_f32(rb(rb(k2.sc[0] * p0) + k2.sc[3 + r])));
+}
+
+template <int NW, int KS, int KR, bool K2LATE>
 __global__ __launch_bounds__(NW * kWave) void premap_resident_fwd(const uint16_t* __restrict__ x,
                                                                  const uint16_t* __restrict__ W,
                                                                  uint16_t* __restrict__ proj,
                                                                  float* __restrict__ inv_rms, const PremapTile pt,
                                                                  int64_t T) {
-  static_assert(KS % 4 == 0 && KR <= KS, "k-steps come in groups of four streams");
+  static_assert(NW == 4 && KS % 4 == 0 && KR <= KS, "four waves; k-steps come in groups of four streams");
   constexpr int HPS = KS / 4;      // k-steps per stream
   constexpr int CPW = 32 * HPS;    // columns per wave and stream
   constexpr int C = CPW * NW;
@@ -390,55 +347,59 @@ __global__ __launch_bounds__(NW * kWave) void premap_resident_fwd(const uint16_t
       sm.tok[threadIdx.x][kDk] = s2;
     }
     __syncthreads();
-    // K1's outputs and K2 on the block's 16 tokens at once: 16 lanes per
-    // token with four waves (token 4 wave + (lane >> 4)), 32 with eight
-    // (token 2 wave + (lane >> 5)).  Rows past T (the last block) hold
+    // K1's outputs and h_pre on the block's 16 tokens at once, 16 lanes per
+    // token (token 4 wave + (lane >> 4)).  Rows past T (the last block) hold
     // re-reads of token T - 1: computed, never stored.
-    if constexpr (NW == 4) {
-      const int tt = 4 * wave + (lane >> 4);
-      const int r = lane & 15;
-      const float inv = rsqrtf(sm.tok[tt][kDk] / static_cast<float>(NC) + kRmsEps);
-      const uint16_t pj0 = f32_to_bf16(sm.tok[tt][r] * inv);
-      const uint16_t pj1 = f32_to_bf16(sm.tok[tt][16 + r] * inv);
-      sm.out.pj[tt][r] = pj0;
-      sm.out.pj[tt][16 + r] = pj1;
-      if (r == 0) sm.out.inv[tt] = inv;
-      k2_token16_lds(sm.k2, sm.permT, sm.u.x, sm.out, sm.hp[tt], tt, r, bf16_to_f32(pj0), bf16_to_f32(pj1));
+    const int tt = 4 * wave + (lane >> 4);
+    const int r = lane & 15;
+    const float inv = rsqrtf(sm.tok[tt][kDk] / static_cast<float>(NC) + kRmsEps);
+    const uint16_t pj0 = f32_to_bf16(sm.tok[tt][r] * inv);
+    const uint16_t pj1 = f32_to_bf16(sm.tok[tt][16 + r] * inv);
+    sm.out.pj[tt][r] = pj0;
+    sm.out.pj[tt][16 + r] = pj1;
+    if (r == 0) sm.out.inv[tt] = inv;
+    // The block's K1 and K2 outputs, whole 16-byte pieces of contiguous rows.
+    // The next step's LDS writes come after its first barrier, which every
+    // wave reaches only after these reads.
+    auto store_outputs = [&]() __attribute__((always_inline)) {
+      if (wave == 0) {  // proj: token lane >> 2, projections 8 (lane & 3) .. + 8
+        const int64_t t = t0 + (lane >> 2);
+        if (t < T)
+          *reinterpret_cast<u32x4*>(proj + t * kDk + 8 * (lane & 3)) =
+              reinterpret_cast<const u32x4*>(sm.out.pj[lane >> 2])[lane & 3];
+      } else if (wave == 1) {  // H_merged: token lane >> 2, row lane & 3
+        const int64_t t = t0 + (lane >> 2);
+        if (t < T)
+          reinterpret_cast<f32x4*>(pt.H)[t * kN + (lane & 3)] =
+              reinterpret_cast<const f32x4*>(sm.out.H[lane >> 2])[lane & 3];
+      } else if (wave == 2) {  // h_pre (lanes 0-15), h_post (16-31), inv_rms (32-47)
+        const int64_t t = t0 + (lane & 15);
+        if (t < T) {
+          if (lane < 16)
+            reinterpret_cast<f32x4*>(pt.h_pre)[t] = *reinterpret_cast<const f32x4*>(sm.hp[lane]);
+          else if (lane < 32)
+            reinterpret_cast<f32x4*>(pt.h_post)[t] = *reinterpret_cast<const f32x4*>(sm.out.hq[lane & 15]);
+          else if (lane < 48)
+            inv_rms[t] = sm.out.inv[lane & 15];
+        }
+      }
+    };
+    // K2LATE: only h_pre stands between K1 and the mix, and the rest of K2
+    // (h_post, H_merged) runs after the mix, while the next block's loads
+    // are in flight.  Otherwise all of K2 and the outputs' stores come first.
+    // At T = 65536, each launch after a cache flush: C = 512 77.3 -> 73.2 us
+    // late; C = 1024 137.3 -> 143.3 us late (the next block's second half is
+    // then issued while its first half is still in flight), so it stays
+    // early there.
+    if constexpr (K2LATE) {
+      k2_hpre16(sm.k2, sm.hp[tt], r, bf16_to_f32(pj0));
     } else {
-      static_assert(NW == 8, "four or eight waves");
-      const int tt = 2 * wave + (lane >> 5);
-      const int q = lane & 31;
-      const float inv = rsqrtf(sm.tok[tt][kDk] / static_cast<float>(NC) + kRmsEps);
-      const uint16_t pj = f32_to_bf16(sm.tok[tt][q] * inv);
-      sm.out.pj[tt][q] = pj;
-      if (q == 0) sm.out.inv[tt] = inv;
-      k2_token32_lds(sm.k2, sm.permT, sm.u.x, sm.out, sm.hp[tt], tt, q, bf16_to_f32(pj));
+      k2_token16_lds(sm.k2, sm.permT, sm.u.x, sm.out, sm.hp[tt], tt, r, bf16_to_f32(pj0), bf16_to_f32(pj1));
     }
     __syncthreads();
-    // The block's K1 and K2 outputs, whole 16-byte pieces of contiguous rows.
-    if (wave == 0) {  // proj: token lane >> 2, projections 8 (lane & 3) .. + 8
-      const int64_t t = t0 + (lane >> 2);
-      if (t < T)
-        *reinterpret_cast<u32x4*>(proj + t * kDk + 8 * (lane & 3)) =
-            reinterpret_cast<const u32x4*>(sm.out.pj[lane >> 2])[lane & 3];
-    } else if (wave == 1) {  // H_merged: token lane >> 2, row lane & 3
-      const int64_t t = t0 + (lane >> 2);
-      if (t < T)
-        reinterpret_cast<f32x4*>(pt.H)[t * kN + (lane & 3)] = reinterpret_cast<const f32x4*>(sm.out.H[lane >> 2])[lane & 3];
-    } else if (wave == 2) {  // h_pre (lanes 0-15), h_post (16-31), inv_rms (32-47)
-      const int64_t t = t0 + (lane & 15);
-      if (t < T) {
-        if (lane < 16)
-          reinterpret_cast<f32x4*>(pt.h_pre)[t] = *reinterpret_cast<const f32x4*>(sm.hp[lane]);
-        else if (lane < 32)
-          reinterpret_cast<f32x4*>(pt.h_post)[t] = *reinterpret_cast<const f32x4*>(sm.out.hq[lane & 15]);
-        else if (lane < 48)
-          inv_rms[t] = sm.out.inv[lane & 15];
-      }
-    }
-    // K3 on the rows still in registers, a half at a time: once a half is
-    // mixed its registers take the next loads (block i + 1's second half,
-    // then block i + 2's first half), so those are issued a half earlier.
+    if constexpr (!K2LATE) store_outputs();
+    // K3 on the rows still in registers, a half at a time: once the first
+    // half is mixed its registers take block i + 1's second half.
     const int64_t ta = t0 + lt, tb = t0 + 8 + lt;
     const bool va = ta < T, vb = tb < T;
     float hh[2][4];
@@ -475,6 +436,12 @@ __global__ __launch_bounds__(NW * kWave) void premap_resident_fwd(const uint16_t
     load_half(A, i + 1, 1);
     __builtin_amdgcn_sched_barrier(0);  // all of block i + 1 before block i + 2 (in-order wait counts)
     mix(B, 1);
+    if constexpr (K2LATE) {
+      // The rest of K2 (h_post, H_merged; its h_pre is the value above).
+      k2_token16_lds(sm.k2, sm.permT, sm.u.x, sm.out, nullptr, tt, r, bf16_to_f32(pj0), bf16_to_f32(pj1));
+      __syncthreads();
+      store_outputs();
+    }
   };
 
   // Block i in (H[2i % 3], H[(2i + 1) % 3]).  The loop body has no exit
@@ -526,9 +493,9 @@ bool premap_resident(const uint16_t* x, const uint16_t* W, uint16_t* proj, float
   const int64_t nblocks = (T + 15) / 16;
   const unsigned grid = static_cast<unsigned>(nblocks < cus ? nblocks : cus);
   if (C == 1024)
-    premap_resident_fwd<4, 32, 16><<<grid, 4 * kWave, 0, s>>>(x, W, proj, inv_rms, pt, T);
+    premap_resident_fwd<4, 32, 16, false><<<grid, 4 * kWave, 0, s>>>(x, W, proj, inv_rms, pt, T);
   else
-    premap_resident_fwd<4, 16, 0><<<grid, 4 * kWave, 0, s>>>(x, W, proj, inv_rms, pt, T);
+    premap_resident_fwd<4, 16, 0, true><<<grid, 4 * kWave, 0, s>>>(x, W, proj, inv_rms, pt, T);
   *status = launch_status();
   return true;
 }
