@@ -46,7 +46,7 @@
 //
 // Measured at T = 65536 (each launch after a cache flush): C = 1024 136-139 us
 // against 174 us for the tile kernel that re-reads x and 205 us for three
-// kernels, 1.04x the region's algorithmic bytes past L2 against 1.74x;
+// kernels, 1.05x the region's algorithmic bytes past L2 against 1.74x;
 // C = 512 72-73 against 94 us; T = 131072, C = 1024: 258 against 331 us.
 // W (256 KiB) and one and a half blocks of rows (192 KiB) fill the CU's
 // registers and LDS, so a block's second half is issued only once the
