@@ -93,6 +93,68 @@ struct FwdFrag {
   u32x4 xv[2][R];      // x of the R token blocks, two k steps
 };
 
+// K3 over one 16-token block of the tile by one wave (rows of C, a multiple
+// of 1024: each lane takes groups lane, lane + 64, ... of every row), with
+// k3_token's loads, arithmetic and stores.  Pieces of a token (two groups of
+// the four streams, eight loads) follow each other token by token, and each
+// piece's loads go out before the previous piece's stores: the compiler does
+// not move a load above an earlier store, so k3_token called token by token
+// waits for its loads once per group.  The last trip reloads the last piece
+// (clamped, as every prefetch here) instead of branching.  The tile kernel
+// takes it for rows of 4096 and 8192: the pre-map forward at C = 4096, each
+// launch after a cache flush, T = 262144 3411 -> 3258 us, 131072 1684 ->
+// 1600, 65536 813 -> 778, 32768 393 -> 381, 16384 186 either way.  With
+// fewer pieces per token it lost (C = 2048, T = 65536: 343 -> 352 us;
+// C = 1024, T = 16384: 51.1 -> 52.7 us).
+__device__ __forceinline__ void k3_block_pipelined(const uint16_t* __restrict__ x, const f32x4* hpre,
+                                                   uint16_t* __restrict__ out, int64_t tb, int64_t T, int C,
+                                                   int lane) {
+  const int np = C / 1024;  // pieces per token
+  const int nu = 16 * np;   // pieces of the block, an even count
+  auto load = [&](u32x4 (&v)[8], int u) __attribute__((always_inline)) {
+    const int tt = u / np, p = u - tt * np;
+    const int64_t t = tb + tt < T ? tb + tt : T - 1;  // rows past T re-read the last one
+    const uint16_t* row = x + t * 4 * C;
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[4 * s + j] = Lanes<8>::raw(row + j * C, lane + 128 * p + 64 * s);
+  };
+  auto mix_store = [&](const u32x4 (&v)[8], int u) __attribute__((always_inline)) {
+    const int tt = u / np, p = u - tt * np;
+    const int64_t t = tb + tt;
+    if (t >= T) return;
+    const f32x4 hv = hpre[tt];
+    const float h[4] = {hv[0], hv[1], hv[2], hv[3]};
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      float a[8], b[8], c[8], d[8], o[8];
+      Lanes<8>::unpack(v[4 * s], a);
+      Lanes<8>::unpack(v[4 * s + 1], b);
+      Lanes<8>::unpack(v[4 * s + 2], c);
+      Lanes<8>::unpack(v[4 * s + 3], d);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float acc = h[0] * a[e];
+        acc = __builtin_fmaf(h[1], b[e], acc);
+        acc = __builtin_fmaf(h[2], c[e], acc);
+        o[e] = __builtin_fmaf(h[3], d[e], acc);
+      }
+      Lanes<8>::store(out + t * C, lane + 128 * p + 64 * s, o);
+    }
+  };
+  u32x4 va[8], vb[8];
+  load(va, 0);
+  for (int u = 0; u < nu; u += 2) {
+    load(vb, u + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    mix_store(va, u);
+    load(va, u + 2 < nu ? u + 2 : nu - 1);
+    __builtin_amdgcn_sched_barrier(0);
+    mix_store(vb, u + 1);
+  }
+}
+
 // SPLITK (few tokens): blockIdx.y selects a range of cps chunks, and the
 // workgroup writes its fp32 partial sums (32 projections + sum of squares per
 // token) to part[t][33][S4] (S4 = gridDim.y rounded up to 4) instead of the
@@ -421,12 +483,16 @@ __global__ __launch_bounds__(kWave * SPLIT) void k1_fwd_mfma(const uint16_t* __r
       if (qd == 0) tile_sm.hpre[16 * r + i] = f32x4{hp_all[0], hp_all[1], hp_all[2], hp_all[3]};
     }
     if (R >= SPLIT && pt.layer_input) {
-      for (int tt = 0; tt < 16; ++tt) {
-        const int64_t t = t0 + 16 * r + tt;
-        if (t >= T) break;
-        const f32x4 hv = tile_sm.hpre[16 * r + tt];
-        const float h[4] = {hv[0], hv[1], hv[2], hv[3]};
-        k3_token<8>(x + t * 4 * pt.C, h, pt.layer_input + t * pt.C, lane, kWave, pt.C);
+      if (pt.C % 4096 == 0) {
+        k3_block_pipelined(x, tile_sm.hpre + 16 * r, pt.layer_input, t0 + 16 * r, T, pt.C, lane);
+      } else {
+        for (int tt = 0; tt < 16; ++tt) {
+          const int64_t t = t0 + 16 * r + tt;
+          if (t >= T) break;
+          const f32x4 hv = tile_sm.hpre[16 * r + tt];
+          const float h[4] = {hv[0], hv[1], hv[2], hv[3]};
+          k3_token<8>(x + t * 4 * pt.C, h, pt.layer_input + t * pt.C, lane, kWave, pt.C);
+        }
       }
     }
     }
