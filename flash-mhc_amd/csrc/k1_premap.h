@@ -42,11 +42,12 @@ bool k1_premap_tile(const uint16_t* x, const uint16_t* W, uint16_t* proj, float*
 // rows in registers from K1 to K3.  Returns false (nothing launched) when the
 // shape, token count (below kResidentMinT), layer input or alignment does not
 // allow it.  Against the tile kernel, each launch after a cache flush:
-// C = 1024, T = 32768 84.9 against 91.2 us, 65536 151 against 174, 131072
-// 281 against 335; C = 512, T = 32768 48.9 against 49.7, 65536 83.8 against
-// 93.6.  At T = 16384 (C = 1024) an earlier form of it lost, 51.9 against
-// 49.9 us: too few blocks per CU to pay for loading W.
-constexpr int64_t kResidentMinT = 32768;
+// C = 1024, T = 16384 47-48 against 51 us, 24576 61 against 72-73, 32768
+// 76.4 against 91.2, 65536 136-139 against 174, 131072 258 against 335;
+// C = 512, T = 16384 27.6 against 31.5, 24576 35.0 against 42.9, 65536 72-73
+// against 94.  At T = 8192 it loses (31.1 against 30.0 us at C = 1024): too
+// few blocks per CU to pay for loading W.
+constexpr int64_t kResidentMinT = 16384;
 bool premap_resident(const uint16_t* x, const uint16_t* W, uint16_t* proj, float* inv_rms, const PremapTile& pt,
                      int64_t T, int64_t C, hipStream_t s, int* status);
 

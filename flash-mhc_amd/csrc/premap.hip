@@ -11,7 +11,7 @@
 // (bf16(grad_x_in + pre-map gradient), autograd's sum), which replaces
 // autograd's separate accumulation pass (1.5 x T x nC x 2 bytes).
 //
-// Forward.  Rows of C = 512 or 1024 per stream with at least 32768 tokens
+// Forward.  Rows of C = 512 or 1024 per stream with at least 16384 tokens
 // and a layer input: the single-read kernel (premap_resident.hip), which
 // keeps W on each CU and reads every row of x once.  Other shapes from the
 // token count where K1 runs one pass (no column split; T > 1024 up to

@@ -1,5 +1,5 @@
 """GPU parity of the single-read pre-map forward (premap_resident.hip): rows of
-C = 512 or 1024 per stream, at least 32768 tokens, with a layer input.
+C = 512 or 1024 per stream, at least 16384 tokens, with a layer input.
 
 Each stage is checked against the oracle with the kernel's own upstream
 outputs as the oracle's inputs (tests/parity.py): proj to K1's bf16 rule over
@@ -43,7 +43,8 @@ def _inputs(T, C, seed):
 
 # The threshold itself, a ragged last block, block counts that are and are
 # not multiples of the 256 workgroups, and both widths.
-@pytest.mark.parametrize("T,C", [(32768, 1024), (32769, 1024), (65536, 1024), (40001, 512), (70001, 512)])
+@pytest.mark.parametrize("T,C", [(16384, 1024), (32768, 1024), (32769, 1024), (65536, 1024), (20001, 512),
+                                 (40001, 512), (70001, 512)])
 def test_resident_stages(T, C):
     nC = 4 * C
     x, W, p = _inputs(T, C, 500 + T + C)

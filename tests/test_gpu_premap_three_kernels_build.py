@@ -52,14 +52,14 @@ def _run(lib, x, W, params, T, C, with_li):
     return out
 
 
-# Rows of C = 512 or 1024 with a layer input and at least 32768 tokens take the
+# Rows of C = 512 or 1024 with a layer input and at least 16384 tokens take the
 # single-read kernel instead (tests/test_gpu_premap_resident.py); the
 # metric-size tile kernel is covered here without the layer input and at
 # C = 2048, and against the three kernels in the premap_reread build there.
 # (16390, 4096) runs the tile's K3 part with the next piece's loads ahead of
 # each store (rows of 4096), a last block of 6 tokens included.
 @pytest.mark.parametrize("T,C,with_li", [(3000, 1024, True), (5000, 512, True), (7000, 1024, False),
-                                         (16384, 1024, True), (16417, 1024, True), (20000, 256, True),
+                                         (16000, 1024, True), (16383, 1024, True), (20000, 256, True),
                                          (16390, 4096, True), (65536, 1024, False), (32768, 2048, True)])
 def test_tile_kernel_equals_three_kernels(three_lib, T, C, with_li):
     g = torch.Generator().manual_seed(T + C)
