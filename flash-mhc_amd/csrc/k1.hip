@@ -103,7 +103,8 @@ struct FwdFrag {
 // (clamped, as every prefetch here) instead of branching.  The tile kernel
 // takes it for rows of 4096 and 8192: the pre-map forward at C = 4096, each
 // launch after a cache flush, T = 262144 3411 -> 3258 us, 131072 1684 ->
-// 1600, 65536 813 -> 778, 32768 393 -> 381, 16384 186 either way.  With
+// 1600, 65536 813 -> 778, 32768 393 -> 381, 16384 186 either way (inside
+// the eager training stack, 3136 against 3140 us at T = 262144).  With
 // fewer pieces per token it lost (C = 2048, T = 65536: 343 -> 352 us;
 // C = 1024, T = 16384: 51.1 -> 52.7 us).
 __device__ __forceinline__ void k3_block_pipelined(const uint16_t* __restrict__ x, const f32x4* hpre,
