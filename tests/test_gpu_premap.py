@@ -68,13 +68,14 @@ def test_premap_fwd_stages(T, C):
 
 @pytest.mark.parametrize("T,C", [(8192, 1024), (300, 1024), (1, 4096), (64, 4096), (257, 4096), (5, 8192),
                                  (3, 1000), (2721, 1024), (4000, 1024), (6000, 512), (8193, 1024), (12000, 512),
-                                 (16000, 1024), (16383, 512),
+                                 (16000, 1024), (16383, 512), (33000, 2048),
                                  (24576, 256), (28000, 256), (28673, 256)])
 def test_premap_matches_three_kernels(T, C):
     """Same outputs as K1 + K2 + K3 launched separately (few tokens: both
     take K1's column-split kernel; where no split is planned the pre-map runs
     its one-kernel tile path, K2 and K3 inside K1's workgroups, on tiles of
-    16 to 64 tokens)."""
+    16 to 64 tokens; from 513 tiles on the K1 op walks its tiles with two
+    workgroups per CU, k1_fwd_persist, which must give the tile's bits)."""
     x = randn((T, 4, C), 3).to(DEV)
     W = randn((32, 4 * C), 4, 0.02).to(DEV)
     p = [t.to(DEV) for t in (*_params(5), PERM)]
