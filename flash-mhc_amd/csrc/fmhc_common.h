@@ -162,7 +162,8 @@ __device__ __forceinline__ void k3_token(const uint16_t* __restrict__ x0, const 
 // 6440-6478 with five at C = 1024, 6135-6175 against 6364-6420 at C = 2048.
 // Where a cap lost it is not applied: K3 backward at C = 4096 (5.57 against
 // 5.35-5.41 TB/s at T = 262144) and in the pre-map backward's reduce-only
-// pass (C = 2048: 846 against 862-872 us), and K4 forward with few
+// pass (C = 2048: 846 against 862-872 us; at C = 1024 five per CU changed
+// nothing, 424-427 against 426-437 us at T = 65536), and K4 forward with few
 // workgroups per CU (T = 4096, C = 1024: a second round of workgroups).
 // Caps of five for K3 forward or six for K3 backward measured slower than
 // none, so the effect is not simply fewer memory requests in flight.
